@@ -1,0 +1,154 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of libbmx.
+//
+// Conventions used by every kernel in this library:
+//  * wave64; MFMA tiles are v_mfma_f32_32x32x16_bf16 (A/B: 8 bf16 per lane,
+//    C/D: 16 fp32 per lane).  Fragment layout (lane l, half h = l / 32):
+//      A (M x K): row l % 32, k-slot 8*h .. 8*h+7
+//      B (K x N): col l % 32, k-slot 8*h .. 8*h+7
+//      D (M x N): col l % 32, register r -> row 8*(r/4) + 4*h + (r%4)
+//    The hardware pairs A and B elements that sit in the same (half, slot), so
+//    any consistent k-permutation between A and B gives the same product.
+//  * bf16 is the compiler's __bf16; float -> bf16 rounds to nearest even
+//    (v_cvt_pk_bf16_f32), matching torch's casts.
+//  * All pointers are device pointers owned by the caller; kernels never
+//    allocate.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace bmx {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kC = 128;          // pair channels (c_z)
+constexpr int kLdsRow = kC + 8;  // padded LDS row (bf16 elements) for 128-wide tiles
+
+// dtype codes shared with include/bmx.h
+enum Dtype : int { kF32 = 0, kBF16 = 1 };
+
+__device__ __forceinline__ float rbf(float x) { return (float)(bf16)x; }
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + __expf(-x)); }
+
+__device__ __forceinline__ float load_f(const float* p) { return *p; }
+__device__ __forceinline__ float load_f(const bf16* p) { return (float)*p; }
+
+template <typename T>
+__device__ __forceinline__ void store_f(T* p, float v) {
+  *p = (T)v;
+}
+
+// 4 consecutive values as fp32.
+__device__ __forceinline__ f32x4 load4(const float* p) { return *(const f32x4*)p; }
+__device__ __forceinline__ f32x4 load4(const bf16* p) {
+  bf16x4 v = *(const bf16x4*)p;
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+// D-fragment row of register r for this lane (see header comment).
+__device__ __forceinline__ int drow(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// Sum / max across the 32 lanes of a half-wave.
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+// LayerNorm over 128 channels of one row held by a half-wave: 4 values per
+// lane (channels 4*hl .. 4*hl+3).  Two-pass mean/variance in fp32.
+__device__ __forceinline__ f32x4 ln128_half(f32x4 v, const float* w, const float* b, int hl, float eps) {
+  float s = v[0] + v[1] + v[2] + v[3];
+  float mean = half_sum(s) * (1.f / kC);
+  f32x4 d = v - mean;
+  float q = d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + d[3] * d[3];
+  float inv = rsqrtf(half_sum(q) * (1.f / kC) + eps);
+  f32x4 y = d * inv;
+  if (w) y = y * load4(w + 4 * hl);
+  if (b) y = y + load4(b + 4 * hl);
+  return y;
+}
+
+// Normalise TP rows of 128 channels into an LDS tile lds[TP][kLdsRow] (bf16).
+// row_ptr(p) returns the row's base pointer or nullptr for padding rows,
+// which are written as zeros.  256 threads: each half-wave takes TP/8 rows.
+template <int TP, typename TIn, typename RowPtr>
+__device__ __forceinline__ void ln_rows_to_lds(RowPtr row_ptr, const float* w, const float* b, float eps,
+                                               bf16* lds) {
+  const int hw = threadIdx.x >> 5, hl = threadIdx.x & 31;
+  constexpr int kPer = TP / 8;
+  f32x4 v[kPer];
+  bool ok[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const TIn* src = row_ptr(hw + 8 * u);
+    ok[u] = src != nullptr;
+    v[u] = ok[u] ? load4(src + 4 * hl) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    f32x4 y = ln128_half(v[u], w, b, hl, eps);
+    if (!ok[u]) y = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+    *(bf16x4*)(lds + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
+  }
+}
+
+// A or B fragment (8 bf16) for k-step ks from a row-major tile with leading
+// dimension ld (elements); the fragment row is row0 + lane % 32.
+__device__ __forceinline__ bf16x8 frag(const bf16* base, int ld, int row0, int ks) {
+  const int l = lane_id();
+  return *(const bf16x8*)(base + (row0 + (l & 31)) * ld + 16 * ks + 8 * (l >> 5));
+}
+
+}  // namespace bmx
+
+// ---------------------------------------------------------------------------
+// Error reporting shared by every C-ABI entry point (defined in api.hip).
+// ---------------------------------------------------------------------------
+namespace bmx {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace bmx
+
+#define BMX_OK 0
+#define BMX_EINVAL 1
+#define BMX_EUNSUPPORTED 2
+#define BMX_ELAUNCH 3
+
+#define BMX_REQUIRE(cond, ...)                                        \
+  do {                                                                \
+    if (!(cond)) return ::bmx::set_error(BMX_EINVAL, __VA_ARGS__);    \
+  } while (0)

@@ -1,0 +1,346 @@
+"""Torch-facing wrappers of the libbmx C ABI.
+
+Two groups:
+
+* the reference's native operator set, same names and argument meaning as
+  the reference's extension functions (``norm``, ``gate``, ``split``,
+  ``pack``, ``silu_mul``, ``epilogue``, ``ordered_softmax``), each raising
+  ``RuntimeError`` on bad input like the reference's ``TORCH_CHECK``s;
+* the fused hot-path modules (``trimul``, ``triattn``, ``pair_transition``,
+  ``adaln``) that take a module with Boltz's parameter names.
+
+Every call launches on torch's current stream of the input's device, allocates
+outputs and workspaces through torch's caching allocator and never
+synchronises.  There is no fallback: without the built library every call
+raises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+
+C = 128
+
+# ---------------------------------------------------------------- helpers
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return N.F32
+    if dtype == torch.bfloat16:
+        return N.BF16
+    raise RuntimeError(f"unsupported dtype {dtype}; expected float32 or bfloat16")
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _cuda(*tensors: torch.Tensor) -> None:
+    dev = tensors[0].device
+    for t in tensors:
+        _check(t.is_cuda, "expected CUDA (HIP) tensors")
+        _check(t.device == dev, "all tensors must be on the same device")
+
+
+def _inference_only() -> None:
+    _check(not torch.is_grad_enabled(), "Inference only")
+
+
+def cached_weight(module, name: str, sources, build):
+    """Derived weight (e.g. a bf16 concatenation) cached on ``module``.
+
+    Reused only while every source parameter keeps its identity, version,
+    device and dtype (the rule of the reference's joint projection cache,
+    multiplication.py:29-40)."""
+    key = tuple((id(p), p._version, p.device, p.dtype) for p in sources)
+    cache = module.__dict__.setdefault("_bmx_weight_cache", {})
+    hit = cache.get(name)
+    if hit is None or hit[0] != key:
+        with torch.no_grad():
+            value = build(*sources).contiguous()
+        hit = (key, value)
+        cache[name] = hit
+    return hit[1]
+
+
+def _bf16(*ws):
+    return torch.cat([w.detach() for w in ws], 0).to(torch.bfloat16)
+
+
+def _f32(t):
+    return t.detach().to(torch.float32).contiguous()
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# ------------------------------------------------- reference operator set
+
+
+def norm(x, weight, bias, eps, channel_first=False, waves=None, rows=None, bf16_output=True):
+    """LayerNorm over 128 channels (reference ``multiplication_norm``,
+    kernels/multiplication_hip.cu:105-156).  ``waves``/``rows`` were gfx90a
+    launch-table knobs and are accepted for signature compatibility only."""
+    _cuda(x, weight, bias)
+    _check(x.is_contiguous() and weight.is_contiguous() and bias.is_contiguous(), "expected contiguous tensors")
+    _check(x.dim() == 2 and (x.size(0) == C if channel_first else x.size(1) == C), "expected 128 channels")
+    _check(weight.numel() == C and bias.numel() == C and weight.dtype == torch.float32
+           and bias.dtype == torch.float32, "expected fp32 weight/bias of 128 elements")
+    _inference_only()
+    _check(eps > 0, "eps must be positive")
+    m = x.size(1) if channel_first else x.size(0)
+    out = torch.empty((m, C), device=x.device, dtype=torch.bfloat16 if bf16_output else torch.float32)
+    if m:
+        N.call("bmx_layernorm128", x.data_ptr(), _code(x.dtype), int(channel_first), weight.data_ptr(),
+               bias.data_ptr(), float(eps), out.data_ptr(), _code(out.dtype), m, _stream(x))
+    return out
+
+
+def layer_norm(x, weight, bias, eps):
+    """LayerNorm over the last axis (<= 1024 channels) with optional weight/bias."""
+    _cuda(x)
+    _check(x.is_contiguous(), "expected a contiguous input")
+    d = x.shape[-1]
+    out = torch.empty_like(x)
+    rows = x.numel() // d if d else 0
+    w = None if weight is None else _f32(weight)
+    b = None if bias is None else _f32(bias)
+    if rows:
+        N.call("bmx_layernorm", x.data_ptr(), None if w is None else w.data_ptr(), None if b is None else b.data_ptr(),
+               float(eps), out.data_ptr(), _code(x.dtype), rows, d, _stream(x))
+    return out
+
+
+def gate(p, g):
+    """``bf16(p * bf16(sigmoid(g)))`` (reference ``multiplication_gate``)."""
+    _cuda(p, g)
+    _check(p.shape == g.shape, "shape mismatch")
+    _check(p.dtype == torch.bfloat16 and g.dtype == torch.bfloat16, "expected bf16 inputs")
+    _inference_only()
+    _check(p.is_contiguous() and g.is_contiguous(), "expected contiguous tensors")
+    out = torch.empty_like(p)
+    if p.numel():
+        N.call("bmx_gate", p.data_ptr(), g.data_ptr(), out.data_ptr(), p.numel(), _stream(p))
+    return out
+
+
+def _check_projection(p, g, mask):
+    _cuda(p, g, mask)
+    _check(p.shape == g.shape and p.dtype == torch.bfloat16 and g.dtype == torch.bfloat16, "expected bf16 p, g")
+    _inference_only()
+    _check(p.dim() == 4 and p.size(0) == 1 and p.size(1) == p.size(2) and p.size(3) == 2 * C,
+           "expected [1, N, N, 256] projections")
+    s = p.stride()
+    _check(s[3] == 1 and s[2] in (2 * C, 4 * C) and s[1] == p.size(2) * s[2] and g.stride() == s,
+           "Expected dense or joint-projection rows")
+    _check(mask.dtype == torch.float32 and mask.is_contiguous() and mask.numel() * 2 * C == p.numel(),
+           "expected an fp32 contiguous [1, N, N] mask")
+    return s[2]
+
+
+def split(p, g, mask):
+    """Gate and mask into channel-last a, b (reference ``multiplication_gate_split``)."""
+    stride = _check_projection(p, g, mask)
+    n = p.size(1)
+    a = torch.empty((1, n, n, C), device=p.device, dtype=torch.bfloat16)
+    b = torch.empty_like(a)
+    if n:
+        N.call("bmx_trimul_split", p.data_ptr(), g.data_ptr(), mask.data_ptr(), a.data_ptr(), b.data_ptr(), n * n,
+               stride, _stream(p))
+    return a, b
+
+
+def pack(p, g, mask, outgoing, channels_per_tile=None):
+    """Gate, mask and channel-major operand layout (reference ``multiplication_gate_pack``)."""
+    stride = _check_projection(p, g, mask)
+    n = p.size(1)
+    a = torch.empty((C, n, n), device=p.device, dtype=torch.bfloat16)
+    b = torch.empty_like(a)
+    if n:
+        N.call("bmx_trimul_pack", p.data_ptr(), g.data_ptr(), mask.data_ptr(), a.data_ptr(), b.data_ptr(), n, stride,
+               int(bool(outgoing)), _stream(p))
+    return a, b
+
+
+def silu_mul(a, b):
+    """``bf16(bf16(silu(a)) * b)`` (reference ``pair_silu_mul``)."""
+    _cuda(a, b)
+    _check(a.shape == b.shape, "shape mismatch")
+    _check(a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16 and a.is_contiguous() and b.is_contiguous(),
+           "expected contiguous bf16 inputs")
+    _check(not a.requires_grad and not b.requires_grad, "Inference only")
+    out = torch.empty_like(a)
+    if a.numel():
+        N.call("bmx_silu_mul", a.data_ptr(), b.data_ptr(), out.data_ptr(), a.numel(), _stream(a))
+    return out
+
+
+MODULATION, GATE, GATED_SWIGLU = 0, 1, 3
+
+
+def epilogue(a, b, c, kind):
+    """Diffusion epilogues (reference ``diffusion_epilogue``, op codes diffusion.py:27)."""
+    _check(kind in (MODULATION, GATE, GATED_SWIGLU), "unknown epilogue kind")
+    _cuda(a, b)
+    _check(a.dtype == b.dtype and a.dtype in (torch.float32, torch.bfloat16), "expected fp32 or bf16 inputs")
+    _check(a.is_contiguous() and b.is_contiguous(), "expected contiguous inputs")
+    shape = list(a.shape)
+    cols = shape[-1]
+    if kind == GATED_SWIGLU:
+        _check(cols % 2 == 0, "SwiGLU input needs an even last dimension")
+        cols //= 2
+        shape[-1] = cols
+    _check(list(b.shape) == shape, "b must match the output shape")
+    if kind == MODULATION:
+        _check(c is not None and list(c.shape) == shape and c.dtype == a.dtype and c.is_contiguous()
+               and c.device == a.device, "MODULATION needs c of the output shape")
+    out = torch.empty(shape, device=a.device, dtype=a.dtype)
+    n = out.numel()
+    if n:
+        N.call("bmx_diffusion_epilogue", kind, a.data_ptr(), b.data_ptr(), None if c is None else c.data_ptr(),
+               out.data_ptr(), _code(a.dtype), n // cols, cols, _stream(a))
+    return out
+
+
+def ordered_softmax(scores, bias, mask, *, rows=None, waves_per_eu=None, allow_large=False):
+    """``softmax(round(round(scores + mask) + bias))`` over keys
+    (reference ``ordered_softmax``, kernels/triangle_softmax.py:117-161).
+    scores [B,I,H,Q,K], bias [B,1,H,Q,K] (broadcast over I), mask [B,I,1,1,K]."""
+    if torch.is_grad_enabled() or scores.dtype not in (torch.float32, torch.bfloat16) or scores.ndim != 5:
+        raise ValueError("Expected inference-only FP32/BF16 triangle scores")
+    bt, i, h, q, k = scores.shape
+    if q <= 0 or k != q:
+        raise ValueError("Expected nonempty square score matrices")
+    _cuda(scores, bias, mask)
+    if bias.dtype != scores.dtype or mask.dtype != torch.float32:
+        raise ValueError("bias must match the score dtype and mask must be fp32")
+    out = torch.empty(scores.shape, device=scores.device, dtype=scores.dtype)
+    N.call("bmx_bias_softmax", scores.data_ptr(), bias.data_ptr(), mask.data_ptr(), out.data_ptr(),
+           _code(scores.dtype), N.int64_array(scores.shape), N.int64_array(scores.stride()),
+           N.int64_array(bias.stride()), N.int64_array(mask.stride()), _stream(scores))
+    return out
+
+
+# ----------------------------------------------------- fused hot-path ops
+
+OUT_BF16, OUT_F32, OUT_ACCUMULATE = 0, 1, 2
+
+
+def _out_tensor(x, out, out_mode):
+    if out_mode == OUT_ACCUMULATE:
+        _check(out is not None and out.dtype == torch.float32 and out.shape == x.shape and out.is_contiguous(),
+               "accumulate mode needs an fp32 contiguous `out` of x's shape")
+        return out
+    dtype = torch.bfloat16 if out_mode == OUT_BF16 else torch.float32
+    if out is None:
+        return torch.empty(x.shape, device=x.device, dtype=dtype)
+    _check(out.dtype == dtype and out.shape == x.shape and out.is_contiguous(), "bad `out` tensor")
+    return out
+
+
+def trimul(module, x, mask, outgoing, out_mode=OUT_BF16, out=None, workspace=None):
+    """Fused TriangleMultiplication{Outgoing,Incoming} for x [N, N, 128] fp32."""
+    _cuda(x, mask)
+    _check(x.dim() == 3 and x.size(0) == x.size(1) and x.size(2) == C, "expected x of shape [N, N, 128]")
+    _check(x.dtype == torch.float32 and x.is_contiguous(), "expected contiguous fp32 x")
+    _check(mask.shape == x.shape[:2] and mask.dtype == torch.float32 and mask.is_contiguous(),
+           "expected a contiguous fp32 [N, N] mask")
+    n = x.size(0)
+    w_in = cached_weight(module, "w_in", (module.p_in.weight, module.g_in.weight), _bf16)
+    w_pout = cached_weight(module, "w_pout", (module.p_out.weight,), _bf16)
+    w_gout = cached_weight(module, "w_gout", (module.g_out.weight,), _bf16)
+    ni, no = module.norm_in, module.norm_out
+    niw, nib = cached_weight(module, "ni_w", (ni.weight,), _f32), cached_weight(module, "ni_b", (ni.bias,), _f32)
+    now, nob = cached_weight(module, "no_w", (no.weight,), _f32), cached_weight(module, "no_b", (no.bias,), _f32)
+    out = _out_tensor(x, out, out_mode)
+    nbytes = N.lib().bmx_trimul_workspace_bytes(n)
+    ws = workspace if workspace is not None and workspace.numel() >= nbytes else _workspace(nbytes, x.device)
+    if n:
+        N.call("bmx_trimul_fwd", x.data_ptr(), mask.data_ptr(), n, int(bool(outgoing)), niw.data_ptr(),
+               nib.data_ptr(), float(ni.eps), w_in.data_ptr(), now.data_ptr(), nob.data_ptr(), float(no.eps),
+               w_pout.data_ptr(), w_gout.data_ptr(), out.data_ptr(), out_mode, ws.data_ptr(), ws.numel(),
+               _stream(x))
+    return out
+
+
+def _triattn_proj_weight(wq, wk, wv, wb):
+    rows = N.lib().bmx_triattn_proj_rows()
+    w = torch.zeros((rows, C), dtype=torch.bfloat16, device=wq.device)
+    used = torch.cat([wq, wk, wv, wb], 0)
+    w[: used.shape[0]] = used.to(torch.bfloat16)
+    return w
+
+
+def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=None):
+    """Fused TriangleAttention (starting or ending node) for x [N, N, 128].
+
+    ``module`` carries Boltz's TriangleAttention parameters: ``layer_norm``,
+    ``linear`` (triangle bias), ``mha.linear_{q,k,v,g,o}``, ``inf``."""
+    _cuda(x)
+    _check(x.dim() == 3 and x.size(0) == x.size(1) and x.size(2) == C, "expected x of shape [N, N, 128]")
+    _check(x.dtype in (torch.float32, torch.bfloat16) and x.is_contiguous(), "expected contiguous fp32/bf16 x")
+    n = x.size(0)
+    if mask is not None:
+        _cuda(x, mask)
+        _check(mask.shape == x.shape[:2] and mask.dtype == torch.float32 and mask.is_contiguous(),
+               "expected a contiguous fp32 [N, N] mask")
+    mha = module.mha
+    w_proj = cached_weight(module, "w_proj", (mha.linear_q.weight, mha.linear_k.weight, mha.linear_v.weight,
+                                              module.linear.weight), _triattn_proj_weight)
+    w_g = cached_weight(module, "w_g", (mha.linear_g.weight,), _bf16)
+    w_o = cached_weight(module, "w_o", (mha.linear_o.weight,), _bf16)
+    b_g = cached_weight(module, "b_g", (mha.linear_g.bias,), _f32)
+    b_o = cached_weight(module, "b_o", (mha.linear_o.bias,), _f32)
+    ln = module.layer_norm
+    lnw, lnb = cached_weight(module, "ln_w", (ln.weight,), _f32), cached_weight(module, "ln_b", (ln.bias,), _f32)
+    out = _out_tensor(x, out, out_mode)
+    nbytes = N.lib().bmx_triattn_workspace_bytes(n)
+    ws = workspace if workspace is not None and workspace.numel() >= nbytes else _workspace(nbytes, x.device)
+    if n:
+        N.call("bmx_triattn_fwd", x.data_ptr(), _code(x.dtype), None if mask is None else mask.data_ptr(), n,
+               int(bool(starting)), float(module.inf), lnw.data_ptr(), lnb.data_ptr(), float(ln.eps),
+               w_proj.data_ptr(), w_g.data_ptr(), b_g.data_ptr(), w_o.data_ptr(), b_o.data_ptr(), out.data_ptr(),
+               out_mode, ws.data_ptr(), ws.numel(), _stream(x))
+    return out
+
+
+def pair_transition(module, x, out_mode=OUT_BF16, out=None):
+    """Fused Transition(128, 512) over the rows of x [..., 128]."""
+    _cuda(x)
+    _check(x.shape[-1] == C and x.dtype in (torch.float32, torch.bfloat16) and x.is_contiguous(),
+           "expected contiguous fp32/bf16 x with 128 channels")
+    _check(module.fc1.weight.shape == (4 * C, C) and module.fc3.weight.shape == (C, 4 * C),
+           "expected a 128 -> 512 -> 128 transition")
+    w12 = cached_weight(module, "w12", (module.fc1.weight, module.fc2.weight), _bf16)
+    w3 = cached_weight(module, "w3", (module.fc3.weight,), _bf16)
+    lnw = cached_weight(module, "ln_w", (module.norm.weight,), _f32)
+    lnb = cached_weight(module, "ln_b", (module.norm.bias,), _f32)
+    out = _out_tensor(x, out, out_mode)
+    rows = x.numel() // C
+    if rows:
+        N.call("bmx_pair_transition_fwd", x.data_ptr(), _code(x.dtype), rows, lnw.data_ptr(), lnb.data_ptr(),
+               float(module.norm.eps), w12.data_ptr(), w3.data_ptr(), out.data_ptr(), out_mode, _stream(x))
+    return out
+
+
+def adaln_modulate(a, scale, shift, eps):
+    """``sigmoid(scale) * LN_noaffine(a) + shift`` in one pass."""
+    _cuda(a, scale, shift)
+    _check(a.shape == scale.shape == shift.shape and a.dtype == scale.dtype == shift.dtype, "shape/dtype mismatch")
+    _check(a.is_contiguous() and scale.is_contiguous() and shift.is_contiguous(), "expected contiguous inputs")
+    d = a.shape[-1]
+    out = torch.empty_like(a)
+    rows = a.numel() // d if d else 0
+    if rows:
+        N.call("bmx_adaln", a.data_ptr(), scale.data_ptr(), shift.data_ptr(), out.data_ptr(), _code(a.dtype), rows,
+               d, float(eps), _stream(a))
+    return out

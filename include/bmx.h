@@ -1,0 +1,131 @@
+/*
+ * bmx.h -- C ABI of libbmx, the gfx950 (MI355X) kernels for Boltz-2's
+ * pair-representation hot path.
+ *
+ * Every entry point:
+ *   - takes device pointers owned by the caller (no allocation, no host sync);
+ *   - launches asynchronously on `stream` (a hipStream_t; 0 = null stream);
+ *   - returns 0 on success, BMX_EINVAL (1) for a rejected argument,
+ *     BMX_EUNSUPPORTED (2) for an unsupported shape, BMX_ELAUNCH (3) when a
+ *     launch failed; bmx_last_error() then describes the failure (per thread).
+ * dtype codes: 0 = fp32, 1 = bf16.  Pair tensors are [n, n, 128] row-major
+ * (one batch element), masks [n, n] fp32.  Weights passed as "bf16" are the
+ * module's fp32 parameters rounded to bf16 by the caller.
+ *
+ * Citations name the reference (lauritsf/boltz-lumi) interface each entry
+ * point replaces, relative to the reference repository root.
+ */
+#ifndef BMX_H
+#define BMX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* bmx_stream_t; /* hipStream_t */
+
+/* Last error message of the calling thread ("" after a successful call). */
+const char* bmx_last_error(void);
+int bmx_abi_version(void);
+
+/* ---- Layer norm -------------------------------------------------------- */
+
+/* LN over exactly 128 channels.  channel_first=0: x[rows][128];
+ * channel_first=1: x[128][rows].  out is always [rows][128].
+ * Replaces multiplication_norm (src/boltz_lumi/kernels/multiplication_hip.cu:149-156,
+ * bound as `norm` in multiplication_hip.cpp) used by normalized_forward
+ * (multiplication.py:81-90,117-126) and normalization_forward (triangle.py:107-146). */
+int bmx_layernorm128(const void* x, int x_dtype, int channel_first, const float* weight, const float* bias, float eps,
+                     void* out, int out_dtype, int64_t rows, bmx_stream_t stream);
+
+/* General LN over dim <= 1024 (dim % 4 == 0) with optional weight/bias (NULL = none).
+ * Serves AdaLN.a_norm / s_norm, which the reference leaves to torch (diffusion.py:83-84). */
+int bmx_layernorm(const void* x, const float* weight, const float* bias, float eps, void* out, int dtype, int64_t rows,
+                  int dim, bmx_stream_t stream);
+
+/* out = sigmoid(scale) * LN_noaffine(a) + shift, one pass.
+ * Replaces a_norm + the MODULATION epilogue of adaln_forward
+ * (src/boltz_lumi/diffusion.py:52-57; kernels/diffusion_hip.cu:14-18,80-126). */
+int bmx_adaln(const void* a, const void* scale, const void* shift, void* out, int dtype, int64_t rows, int dim,
+              float eps, bmx_stream_t stream);
+
+/* ---- Elementwise operators (reference's unfused operator set) ---------- */
+
+/* out = bf16(x * bf16(sigmoid(g))), bf16.
+ * Replaces multiplication_gate (kernels/multiplication_gate_hip.cu:81-94, `gate`). */
+int bmx_gate(const void* x, const void* g, void* out, int64_t n, bmx_stream_t stream);
+
+/* a,b[pairs][128] = bf16(gate(p, g)) * mask from p,g rows of 256 channels at row_stride (256 or 512).
+ * Replaces multiplication_gate_split (kernels/multiplication_gate_hip.cu:140-172, `split`). */
+int bmx_trimul_split(const void* p, const void* g, const float* mask, void* a, void* b, int64_t pairs, int row_stride,
+                     bmx_stream_t stream);
+
+/* Channel-major bmm operands a,b[128][n][n] (outgoing: b transposed; incoming: a transposed).
+ * Replaces multiplication_gate_pack (kernels/multiplication_gate_hip.cu:96-123, `pack`). */
+int bmx_trimul_pack(const void* p, const void* g, const float* mask, void* a, void* b, int64_t n, int row_stride,
+                    int outgoing, bmx_stream_t stream);
+
+/* out = bf16(bf16(silu(a)) * b), bf16.
+ * Replaces pair_silu_mul (kernels/pair_hip.cu:42-64, `silu_mul`). */
+int bmx_silu_mul(const void* a, const void* b, void* out, int64_t n, bmx_stream_t stream);
+
+/* kind 0 MODULATION: sigmoid(b)*a + c;  1 GATE: sigmoid(a)*b;
+ * 3 GATED_SWIGLU: silu(a[:, cols:]) * a[:, :cols] * b  (a has 2*cols columns).
+ * Replaces diffusion_epilogue (kernels/diffusion_hip.cu:80-126, `epilogue`; op codes diffusion.py:27). */
+int bmx_diffusion_epilogue(int kind, const void* a, const void* b, const void* c, void* out, int dtype, int64_t rows,
+                           int64_t cols, bmx_stream_t stream);
+
+/* P = softmax(round(round(S + mask) + bias)) over the last axis, rounding to dtype.
+ * shape = {B, I, H, Q, K}; element strides of scores [B,I,H,Q,K], bias [B,1,H,Q,K], mask [B,I,1,1,K].
+ * out is contiguous.  Replaces ordered_softmax (kernels/triangle_softmax.py:117-161) and
+ * triangle_block_softmax (kernels/triangle_block_softmax_hip.cu:120-143). */
+int bmx_bias_softmax(const void* scores, const void* bias, const float* mask, void* out, int dtype,
+                     const int64_t* shape, const int64_t* s_strides, const int64_t* b_strides,
+                     const int64_t* m_strides, bmx_stream_t stream);
+
+/* ---- Fused hot-path modules -------------------------------------------- */
+
+/* out_mode for the fused modules: 0 = write bf16 [n,n,128], 1 = write fp32,
+ * 2 = add into fp32 `out` (residual stream; out may alias x). */
+
+/* Workspace needed by bmx_trimul_fwd (bytes; 3 * 128 * np^2 bf16, np = round_up(n,128)). */
+size_t bmx_trimul_workspace_bytes(int64_t n);
+
+/* TriangleMultiplication{Outgoing,Incoming}.forward for one batch element.
+ * w_in: bf16 [512][128] = [p_in.weight; g_in.weight]; w_pout, w_gout: bf16 [128][128].
+ * Replaces normalized_forward (src/boltz_lumi/multiplication.py:48-137) end to end. */
+int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, const float* norm_in_w,
+                   const float* norm_in_b, float eps_in, const void* w_in, const float* norm_out_w,
+                   const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
+                   int out_mode, void* workspace, size_t workspace_bytes, bmx_stream_t stream);
+
+/* Workspace needed by bmx_triattn_fwd (bytes). */
+size_t bmx_triattn_workspace_bytes(int64_t n);
+
+/* Rows of the packed projection weight of bmx_triattn_fwd (416). */
+int bmx_triattn_proj_rows(void);
+
+/* TriangleAttention{,EndingNode}.forward (c_in 128, 4 heads x 32) for one batch element.
+ * w_proj: bf16 [416][128] = [linear_q; linear_k; linear_v; linear (4 rows); zeros];
+ * w_g, w_o: bf16 [128][128] with fp32 biases b_g, b_o.  mask may be NULL (all ones).
+ * Replaces TriangleAttention.forward with the reference's patched layer_norm, _chunk and
+ * mha.forward (src/boltz_lumi/triangle.py:18-22,32-104,107-146). */
+int bmx_triattn_fwd(const void* x, int x_dtype, const float* mask, int64_t n, int starting, float inf,
+                    const float* ln_w, const float* ln_b, float eps, const void* w_proj, const void* w_g,
+                    const float* b_g, const void* w_o, const float* b_o, void* out, int out_mode, void* workspace,
+                    size_t workspace_bytes, bmx_stream_t stream);
+
+/* Transition(128, 512).forward on `rows` rows of 128 channels.
+ * w12: bf16 [1024][128] = [fc1.weight; fc2.weight]; w3: bf16 [128][512] = fc3.weight.
+ * Replaces transition_forward (src/boltz_lumi/pair_transition.py:8-28). */
+int bmx_pair_transition_fwd(const void* x, int x_dtype, int64_t rows, const float* ln_w, const float* ln_b, float eps,
+                            const void* w12, const void* w3, void* out, int out_mode, bmx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BMX_H */

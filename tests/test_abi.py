@@ -1,0 +1,68 @@
+"""CPU checks of the C ABI: the library loads and exports every symbol that
+include/bmx.h declares, and argument validation fails loudly without a GPU
+(no kernel is launched by these tests)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from boltz_lumi_amd import _native as N
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "bmx.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(bmx_\w+)\(", text, re.M)))
+
+
+def test_header_matches_binding_table():
+    assert declared_symbols() == sorted(N.SIGNATURES)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not N.lib_path().exists():
+        pytest.skip("libbmx.so not built")
+    return N.lib()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.bmx_abi_version() == 1
+
+
+def test_workspace_queries(lib):
+    assert lib.bmx_trimul_workspace_bytes(0) == 0
+    assert lib.bmx_trimul_workspace_bytes(1024) == 3 * 128 * 1024 * 1024 * 2
+    assert lib.bmx_trimul_workspace_bytes(100) == 3 * 128 * 128 * 128 * 2
+    assert lib.bmx_triattn_workspace_bytes(1024) > 3 * 1024 * 1024 * 128 * 2
+    assert lib.bmx_triattn_proj_rows() == 3 * 128 + 32
+
+
+def test_argument_validation_needs_no_gpu(lib):
+    # Rejected before any launch: bad dtype code, bad out_mode, empty input.
+    rc = lib.bmx_layernorm128(None, 7, 0, None, None, 1e-5, None, 0, 4, None)
+    assert rc == N.BMX_EINVAL and b"dtypes" in lib.bmx_last_error()
+    rc = lib.bmx_trimul_fwd(None, None, 4, 1, None, None, 1e-5, None, None, None, 1e-5, None, None, None, 9, None, 0,
+                            None)
+    assert rc == N.BMX_EINVAL and b"out_mode" in lib.bmx_last_error()
+    rc = lib.bmx_trimul_fwd(None, None, 4, 1, None, None, 1e-5, None, None, None, 1e-5, None, None, None, 0, None, 0,
+                            None)
+    assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
+    assert lib.bmx_gate(None, None, None, 0, None) == N.BMX_OK
+    rc = lib.bmx_diffusion_epilogue(2, None, None, None, None, 0, 1, 4, None)
+    assert rc == N.BMX_EINVAL and b"kind" in lib.bmx_last_error()
+    rc = lib.bmx_triattn_fwd(None, 0, None, 8, 1, 1e9, None, None, 1e-5, None, None, None, None, None, None, 0,
+                             None, 0, None)
+    assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
+    rc = lib.bmx_pair_transition_fwd(None, 1, 8, None, None, 1e-5, None, None, None, 2, None)
+    assert rc == N.BMX_EINVAL and b"residual" in lib.bmx_last_error()
+
+
+def test_call_raises_with_message(lib):
+    with pytest.raises(N.BmxError, match="eps must be positive"):
+        N.call("bmx_layernorm", None, None, None, 0.0, None, 0, 1, 4, None)
