@@ -1,0 +1,222 @@
+#!/usr/bin/env python
+"""Benchmark: one Boltz-2 PairformerLayer forward at N=1024 on one MI355X.
+
+Metric: "Pairformer layer ms @N=1024 bf16; tri-attn/mult % of
+MFMA/HBM roofline".  A step is one full PairformerLayer forward (v2, eval):
+tri_mul_out, tri_mul_in, tri_att_start, tri_att_end, transition_z on the fp32
+pair stream with the bf16 gfx950 kernels, then the fp32 sequence stack.  Inputs
+(z [1,N,N,128], s [1,N,384], masks all ones) and random-init weights (seed 0,
+N(0, 0.08), norm weights N(1, 0.08)) are resident in HBM before timing.
+
+Prints one JSON line.  ``roofline`` covers the kernel with the largest share
+of the layer, timed with HIP events on the launch stream; ``breakdown`` lists
+every kernel.  ``cpu_baseline`` times the CPU oracle on the host cores for one
+layer at --cpu-n (default: the benchmark N) -- a reported baseline only.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--n", type=int, default=1024)
+    p.add_argument("--cpu-n", type=int, default=None, help="token count of the CPU sample (default: --n)")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--kernel-reps", type=int, default=3, help="repetitions of the per-kernel timing pass")
+    return p.parse_args()
+
+
+def init_weights(module, seed: int):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in module.named_parameters():
+            mean = 1.0 if "norm" in name and name.endswith("weight") else 0.0
+            p.copy_(torch.randn(p.shape, generator=g) * 0.08 + mean)
+    return module
+
+
+def kernel_table(n: int):
+    """Algorithmic flops and compulsory HBM bytes per launch, per kernel."""
+    n2, n3 = float(n) ** 2, float(n) ** 3
+    return {
+        # name: (flops, bytes, bound)
+        "trimul_proj": (2 * n2 * 128 * 512, n2 * (512 + 4 + 2 * 256), "hbm"),
+        "trimul_contract": (2 * 128 * n3, n2 * 128 * 2 * 3, "mfma"),
+        "trimul_out": (2 * n2 * 128 * 256, n2 * (256 + 512 + 512), "hbm"),
+        "triattn_proj": (2 * n2 * 128 * 388, n2 * (512 + 4 + 3 * 256 + 16), "hbm"),
+        "triattn_core": (4 * 4 * 32 * n3, n2 * 4 * 3 * 64 + n2 * 256, "mfma"),
+        "triattn_out": (2 * n2 * 128 * 256, n2 * (512 + 256 + 512), "hbm"),
+        "pair_transition": (2 * n2 * 128 * 1536, n2 * 1024, "hbm"),
+    }
+
+
+def per_kernel_times(layer, s, z, mask, pair_mask, z_out, ws, reps):
+    """Average ms per launch of every kernel of the layer, from HIP events
+    recorded on torch's current stream (the stream the kernels launch on)."""
+    import torch
+    from boltz_lumi_amd import ops
+
+    zi, zo, mb = z[0], z_out[0], pair_mask[0].float().contiguous()
+    plan = []
+    for mod, outgoing, first in ((layer.tri_mul_out, True, True), (layer.tri_mul_in, False, False)):
+        mode = ops.OUT_RESIDUAL if first else ops.OUT_ACCUMULATE
+        src = zi if first else zo
+        for stage, name in ((1, "trimul_proj"), (2, "trimul_contract"), (4, "trimul_out")):
+            plan.append((name, lambda m=mod, o=outgoing, md=mode, x=src, st=stage:
+                         ops.trimul(m, x, mb, o, md, zo, ws, stages=st)))
+    for mod, starting in ((layer.tri_att_start, True), (layer.tri_att_end, False)):
+        for stage, name in ((1, "triattn_proj"), (2, "triattn_core"), (4, "triattn_out")):
+            plan.append((name, lambda m=mod, st_=starting, st=stage:
+                         ops.triattn(m, zo, mb, st_, ops.OUT_ACCUMULATE, zo, ws, stages=st)))
+    plan.append(("pair_transition", lambda: ops.pair_transition(layer.transition_z, zo, ops.OUT_ACCUMULATE, zo)))
+    plan.append(("sequence_stack", lambda: layer.sequence_stack(s, z_out, mask)))
+    totals = {}
+    counts = {}
+    for _ in range(reps):
+        events = []
+        for name, fn in plan:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            events.append((name, e0, e1))
+        torch.cuda.synchronize()
+        for name, e0, e1 in events:
+            totals[name] = totals.get(name, 0.0) + e0.elapsed_time(e1)
+            counts[name] = counts.get(name, 0) + 1
+    return {k: (totals[k] / counts[k], counts[k] // reps) for k in totals}
+
+
+def cpu_baseline(n: int, seed: int):
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import boltz_ref as R  # the checker, timed as the reference CPU path
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    layer = init_weights(R.PairformerLayer(), seed).eval()
+    g = torch.Generator().manual_seed(seed)
+    z = torch.randn(1, n, n, 128, generator=g)
+    s = torch.randn(1, n, 384, generator=g)
+    mask, pm = torch.ones(1, n), torch.ones(1, n, n)
+    with torch.inference_mode():
+        layer(s[:, :32], z[:, :32, :32], mask[:, :32], pm[:, :32, :32], chunk_size_tri_attn=32)  # thread warm-up
+        t0 = time.perf_counter()
+        layer(s, z, mask, pm, chunk_size_tri_attn=64)
+        dt = time.perf_counter() - t0
+    return dt * 1e3, cores
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding of the pair stack is a design note, not built)"}))
+        sys.exit(2)
+    import torch
+    from boltz_lumi_amd import layers, ops
+
+    dev = torch.device("cuda:0")
+    n = args.n
+    layer = init_weights(layers.PairformerLayer(), 0).to(dev).eval()
+    g = torch.Generator().manual_seed(0)
+    z = torch.randn(1, n, n, 128, generator=g).to(dev)
+    s = torch.randn(1, n, 384, generator=g).to(dev)
+    mask = torch.ones(1, n, device=dev)
+    pair_mask = torch.ones(1, n, n, device=dev)
+    ws = ops.new_workspace(n, dev)
+    z_out = torch.empty_like(z)
+
+    def step():
+        layer(s, z, mask, pair_mask, z_out=z_out, workspace=ws)
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        wall0 = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        ms = e0.elapsed_time(e1) / args.steps
+        kt = per_kernel_times(layer, s, z, mask, pair_mask, z_out, ws, args.kernel_reps)
+
+    table = kernel_table(n)
+    breakdown = {}
+    for name, (avg_ms, launches) in kt.items():
+        entry = {"ms": round(avg_ms, 4), "launches_per_layer": launches}
+        if name in table:
+            flops, nbytes, bound = table[name]
+            entry["tflops"] = round(flops / (avg_ms * 1e-3) / 1e12, 2)
+            entry["gbs"] = round(nbytes / (avg_ms * 1e-3) / 1e9, 1)
+            entry["bound"] = bound
+            entry["frac"] = round(entry["tflops"] / PEAK_BF16_TFLOPS if bound == "mfma"
+                                  else entry["gbs"] / PEAK_HBM_GBS, 4)
+        breakdown[name] = entry
+    dominant = max((k for k in breakdown if k in table),
+                   key=lambda k: breakdown[k]["ms"] * breakdown[k]["launches_per_layer"])
+    d = breakdown[dominant]
+    roofline = {
+        "kernel": dominant,
+        "bound": d["bound"],
+        "achieved": d["tflops"] if d["bound"] == "mfma" else d["gbs"],
+        "peak": PEAK_BF16_TFLOPS if d["bound"] == "mfma" else PEAK_HBM_GBS,
+        "unit": "TFLOP/s" if d["bound"] == "mfma" else "GB/s",
+        "frac": d["frac"],
+        "traffic": None,
+    }
+    out = {
+        "metric": "Pairformer layer ms @N=1024 bf16",
+        "value": round(ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (z, s ~ N(0,1); masks ones; random-init weights seed 0)",
+        "config": {"workload": f"PairformerLayer forward, N={n}, c_z=128, c_s=384, tri-att 4x32, "
+                               f"tri-mult 128, transition x4, single attention 16 heads (BASELINE configs[3], "
+                               f"one of 64 blocks)", "n_tokens": n, "batch": 1},
+        "wall_s": round(wall, 3),
+        "roofline": roofline,
+        "breakdown": breakdown,
+    }
+    if not args.no_cpu_baseline:
+        cpu_n = args.cpu_n or n
+        cpu_ms, cores = cpu_baseline(cpu_n, 0)
+        out["cpu_baseline"] = {
+            "value": round(cpu_ms, 1),
+            "unit": "ms per layer",
+            "cores": cores,
+            "kind": "port",
+            "sample": f"one PairformerLayer forward at N={cpu_n}, fp32 CPU oracle (oracle/boltz_ref.py), "
+                      f"tri-attention chunked 64 rows, {cores} threads",
+        }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

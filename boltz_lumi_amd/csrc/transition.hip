@@ -79,8 +79,10 @@ __global__ __launch_bounds__(256) void pair_transition_kernel(const TIn* x, cons
         ((bf16*)out)[off] = (bf16)v;
       else if (out_mode == 1)
         ((float*)out)[off] = v;
-      else
+      else if (out_mode == 2)
         ((float*)out)[off] += v;
+      else
+        ((float*)out)[off] = (float)x[off] + v;
     }
 }
 
@@ -92,8 +94,8 @@ int bmx_pair_transition_fwd(const void* x, int x_dtype, int64_t rows, const floa
                             const void* w12, const void* w3, void* out, int out_mode, hipStream_t stream) {
   BMX_REQUIRE(rows >= 0, "bmx_pair_transition_fwd: rows must be >= 0");
   BMX_REQUIRE(x_dtype == kF32 || x_dtype == kBF16, "bmx_pair_transition_fwd: x dtype must be fp32 or bf16");
-  BMX_REQUIRE(out_mode >= 0 && out_mode <= 2,
-              "bmx_pair_transition_fwd: out_mode must be 0 (bf16), 1 (fp32) or 2 (fp32 +=)");
+  BMX_REQUIRE(out_mode >= 0 && out_mode <= 3,
+              "bmx_pair_transition_fwd: out_mode must be 0 (bf16), 1 (fp32), 2 (fp32 +=) or 3 (fp32 x + y)");
   BMX_REQUIRE(out_mode != 2 || x_dtype == kF32, "bmx_pair_transition_fwd: residual mode needs fp32 x");
   BMX_REQUIRE(eps > 0.f, "bmx_pair_transition_fwd: eps must be positive");
   if (rows == 0) return BMX_OK;

@@ -298,8 +298,10 @@ __global__ __launch_bounds__(256) void triattn_out_kernel(const TIn* x, const fl
         ((bf16*)out)[off] = (bf16)y;
       else if (out_mode == 1)
         ((float*)out)[off] = y;
-      else
+      else if (out_mode == 2)
         ((float*)out)[off] += y;
+      else
+        ((float*)out)[off] = (float)x[off] + y;
     }
   }
 }
@@ -329,17 +331,24 @@ Layout make_layout(void* ws, int n) {
 template <typename TIn>
 int run(const TIn* x, const float* mask, int n, int starting, float inf, const float* ln_w, const float* ln_b,
         float eps, const bf16* w_proj, const bf16* w_g, const float* b_g, const bf16* w_o, const float* b_o,
-        void* out, int out_mode, void* ws, hipStream_t st) {
+        void* out, int out_mode, void* ws, int stages, hipStream_t st) {
   Layout L = make_layout(ws, n);
-  triattn_proj_kernel<TIn><<<dim3(L.np / kTP, L.np), 256, 0, st>>>(x, mask, ln_w, ln_b, eps, w_proj, inf,
-                                                                    starting, L);
-  if (int rc = check_launch("triattn_proj")) return rc;
   const int qtiles = (n + kTP - 1) / kTP;
-  triattn_core_kernel<<<dim3((unsigned)((int64_t)n * kH * qtiles)), 256, 0, st>>>(L);
-  if (int rc = check_launch("triattn_core")) return rc;
-  triattn_out_kernel<TIn><<<dim3(qtiles, n), 256, 0, st>>>(x, ln_w, ln_b, eps, w_g, b_g, w_o, b_o, starting, out,
-                                                           out_mode, L);
-  return check_launch("triattn_out");
+  if (stages & 1) {
+    triattn_proj_kernel<TIn><<<dim3(L.np / kTP, L.np), 256, 0, st>>>(x, mask, ln_w, ln_b, eps, w_proj, inf,
+                                                                      starting, L);
+    if (int rc = check_launch("triattn_proj")) return rc;
+  }
+  if (stages & 2) {
+    triattn_core_kernel<<<dim3((unsigned)((int64_t)n * kH * qtiles)), 256, 0, st>>>(L);
+    if (int rc = check_launch("triattn_core")) return rc;
+  }
+  if (stages & 4) {
+    triattn_out_kernel<TIn><<<dim3(qtiles, n), 256, 0, st>>>(x, ln_w, ln_b, eps, w_g, b_g, w_o, b_o, starting,
+                                                             out, out_mode, L);
+    if (int rc = check_launch("triattn_out")) return rc;
+  }
+  return BMX_OK;
 }
 
 }  // namespace
@@ -356,11 +365,13 @@ size_t bmx_triattn_workspace_bytes(int64_t n) {
 int bmx_triattn_fwd(const void* x, int x_dtype, const float* mask, int64_t n, int starting, float inf,
                     const float* ln_w, const float* ln_b, float eps, const void* w_proj, const void* w_g,
                     const float* b_g, const void* w_o, const float* b_o, void* out, int out_mode, void* workspace,
-                    size_t workspace_bytes, hipStream_t stream) {
+                    size_t workspace_bytes, int stages, hipStream_t stream) {
   BMX_REQUIRE(n >= 0 && n <= 8192, "bmx_triattn_fwd: n must be in [0, 8192] (got %lld)", (long long)n);
   BMX_REQUIRE(x_dtype == kF32 || x_dtype == kBF16, "bmx_triattn_fwd: x dtype must be fp32 or bf16");
-  BMX_REQUIRE(out_mode >= 0 && out_mode <= 2, "bmx_triattn_fwd: out_mode must be 0 (bf16), 1 (fp32) or 2 (fp32 +=)");
+  BMX_REQUIRE(out_mode >= 0 && out_mode <= 3,
+              "bmx_triattn_fwd: out_mode must be 0 (bf16), 1 (fp32), 2 (fp32 +=) or 3 (fp32 x + y)");
   BMX_REQUIRE(out_mode != 2 || x_dtype == kF32, "bmx_triattn_fwd: residual mode needs fp32 x");
+  BMX_REQUIRE(stages >= 1 && stages <= 7, "bmx_triattn_fwd: stages must be a non-empty subset of 1|2|4");
   BMX_REQUIRE(eps > 0.f && inf > 0.f, "bmx_triattn_fwd: eps and inf must be positive");
   if (n == 0) return BMX_OK;
   BMX_REQUIRE(x && ln_w && ln_b && w_proj && w_g && b_g && w_o && b_o && out, "bmx_triattn_fwd: null pointer");
@@ -372,9 +383,9 @@ int bmx_triattn_fwd(const void* x, int x_dtype, const float* mask, int64_t n, in
               "bmx_triattn_fwd: x and weights must be 16-byte aligned, workspace 256-byte aligned");
   if (x_dtype == kF32)
     return run<float>((const float*)x, mask, (int)n, starting, inf, ln_w, ln_b, eps, (const bf16*)w_proj,
-                      (const bf16*)w_g, b_g, (const bf16*)w_o, b_o, out, out_mode, workspace, stream);
+                      (const bf16*)w_g, b_g, (const bf16*)w_o, b_o, out, out_mode, workspace, stages, stream);
   return run<bf16>((const bf16*)x, mask, (int)n, starting, inf, ln_w, ln_b, eps, (const bf16*)w_proj,
-                   (const bf16*)w_g, b_g, (const bf16*)w_o, b_o, out, out_mode, workspace, stream);
+                   (const bf16*)w_g, b_g, (const bf16*)w_o, b_o, out, out_mode, workspace, stages, stream);
 }
 
 int bmx_triattn_proj_rows(void) { return kProjRows; }

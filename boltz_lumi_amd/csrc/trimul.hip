@@ -208,12 +208,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
 }
 
 // ------------------------------------------------------------------ K3
-__global__ __launch_bounds__(256) void trimul_out_kernel(const float* __restrict__ x, const bf16* __restrict__ o_pl,
+__global__ __launch_bounds__(256) void trimul_out_kernel(const float* x, const bf16* __restrict__ o_pl,
                                                          const float* __restrict__ in_w, const float* __restrict__ in_b,
                                                          float eps_in, const float* __restrict__ out_w,
                                                          const float* __restrict__ out_b, float eps_out,
                                                          const bf16* __restrict__ w_pout,
-                                                         const bf16* __restrict__ w_gout, void* __restrict__ out,
+                                                         const bf16* __restrict__ w_gout, void* out,
                                                          int out_mode, int n, int np) {
   __shared__ __attribute__((aligned(16))) bf16 xo[kTP * kLdsRow];  // LN_out(O), pairs x channels
   __shared__ __attribute__((aligned(16))) bf16 xg[kTP * kLdsRow];  // LN_in(x), pairs x channels
@@ -274,8 +274,10 @@ __global__ __launch_bounds__(256) void trimul_out_kernel(const float* __restrict
         ((bf16*)out)[o] = (bf16)y;
       else if (out_mode == 1)
         ((float*)out)[o] = y;
-      else
+      else if (out_mode == 2)
         ((float*)out)[o] += y;
+      else
+        ((float*)out)[o] = x[o] + y;
     }
   }
 }
@@ -295,9 +297,11 @@ size_t bmx_trimul_workspace_bytes(int64_t n) {
 int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, const float* norm_in_w,
                    const float* norm_in_b, float eps_in, const void* w_in, const float* norm_out_w,
                    const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
-                   int out_mode, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                   int out_mode, void* workspace, size_t workspace_bytes, int stages, hipStream_t stream) {
   BMX_REQUIRE(n >= 0 && n <= 16384, "bmx_trimul_fwd: n must be in [0, 16384] (got %lld)", (long long)n);
-  BMX_REQUIRE(out_mode >= 0 && out_mode <= 2, "bmx_trimul_fwd: out_mode must be 0 (bf16), 1 (fp32) or 2 (fp32 +=)");
+  BMX_REQUIRE(out_mode >= 0 && out_mode <= 3,
+              "bmx_trimul_fwd: out_mode must be 0 (bf16), 1 (fp32), 2 (fp32 +=) or 3 (fp32 x + y)");
+  BMX_REQUIRE(stages >= 1 && stages <= 7, "bmx_trimul_fwd: stages must be a non-empty subset of 1|2|4");
   BMX_REQUIRE(eps_in > 0.f && eps_out > 0.f, "bmx_trimul_fwd: eps must be positive");
   if (n == 0) return BMX_OK;
   BMX_REQUIRE(x && mask && norm_in_w && norm_in_b && w_in && norm_out_w && norm_out_b && w_pout && w_gout && out,
@@ -315,20 +319,25 @@ int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, c
   bf16* b_pl = a_pl + plane;
   bf16* o_pl = b_pl + plane;
 
-  trimul_proj_kernel<<<dim3(np / kTP, np), 256, 0, stream>>>(x, mask, norm_in_w, norm_in_b, eps_in,
-                                                              (const bf16*)w_in, a_pl, b_pl, ni, np, outgoing);
-  if (int rc = check_launch("trimul_proj")) return rc;
-
-  constexpr int BM = 128, BN = 128, BK = 64;
-  const int tiles_n = np / BN, tiles_per_ch = (np / BM) * tiles_n;
-  trimul_contract_kernel<BM, BN, BK, 64, 64><<<dim3(kC * tiles_per_ch), 256, 0, stream>>>(a_pl, b_pl, o_pl, np,
-                                                                                           tiles_n, tiles_per_ch);
-  if (int rc = check_launch("trimul_contract")) return rc;
-
-  trimul_out_kernel<<<dim3((ni + kTP - 1) / kTP, ni), 256, 0, stream>>>(
-      x, o_pl, norm_in_w, norm_in_b, eps_in, norm_out_w, norm_out_b, eps_out, (const bf16*)w_pout,
-      (const bf16*)w_gout, out, out_mode, ni, np);
-  return check_launch("trimul_out");
+  if (stages & 1) {
+    trimul_proj_kernel<<<dim3(np / kTP, np), 256, 0, stream>>>(x, mask, norm_in_w, norm_in_b, eps_in,
+                                                                (const bf16*)w_in, a_pl, b_pl, ni, np, outgoing);
+    if (int rc = check_launch("trimul_proj")) return rc;
+  }
+  if (stages & 2) {
+    constexpr int BM = 128, BN = 128, BK = 64;
+    const int tiles_n = np / BN, tiles_per_ch = (np / BM) * tiles_n;
+    trimul_contract_kernel<BM, BN, BK, 64, 64><<<dim3(kC * tiles_per_ch), 256, 0, stream>>>(
+        a_pl, b_pl, o_pl, np, tiles_n, tiles_per_ch);
+    if (int rc = check_launch("trimul_contract")) return rc;
+  }
+  if (stages & 4) {
+    trimul_out_kernel<<<dim3((ni + kTP - 1) / kTP, ni), 256, 0, stream>>>(
+        x, o_pl, norm_in_w, norm_in_b, eps_in, norm_out_w, norm_out_b, eps_out, (const bf16*)w_pout,
+        (const bf16*)w_gout, out, out_mode, ni, np);
+    if (int rc = check_launch("trimul_out")) return rc;
+  }
+  return BMX_OK;
 }
 
 }  // extern "C"

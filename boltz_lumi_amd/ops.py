@@ -232,7 +232,9 @@ def ordered_softmax(scores, bias, mask, *, rows=None, waves_per_eu=None, allow_l
 
 # ----------------------------------------------------- fused hot-path ops
 
-OUT_BF16, OUT_F32, OUT_ACCUMULATE = 0, 1, 2
+# out_mode: write bf16 / write fp32 / out += y (in-place residual) / out = x + y
+OUT_BF16, OUT_F32, OUT_ACCUMULATE, OUT_RESIDUAL = 0, 1, 2, 3
+ALL_STAGES = 7
 
 
 def _out_tensor(x, out, out_mode):
@@ -244,11 +246,16 @@ def _out_tensor(x, out, out_mode):
     if out is None:
         return torch.empty(x.shape, device=x.device, dtype=dtype)
     _check(out.dtype == dtype and out.shape == x.shape and out.is_contiguous(), "bad `out` tensor")
+    if out_mode == OUT_RESIDUAL:
+        _check(out.data_ptr() != x.data_ptr(), "residual-write mode needs `out` distinct from x")
     return out
 
 
-def trimul(module, x, mask, outgoing, out_mode=OUT_BF16, out=None, workspace=None):
-    """Fused TriangleMultiplication{Outgoing,Incoming} for x [N, N, 128] fp32."""
+def trimul(module, x, mask, outgoing, out_mode=OUT_BF16, out=None, workspace=None, stages=ALL_STAGES):
+    """Fused TriangleMultiplication{Outgoing,Incoming} for x [N, N, 128] fp32.
+
+    ``stages`` selects the kernels (1 projection, 2 contraction, 4 output);
+    separate calls must share ``workspace``."""
     _cuda(x, mask)
     _check(x.dim() == 3 and x.size(0) == x.size(1) and x.size(2) == C, "expected x of shape [N, N, 128]")
     _check(x.dtype == torch.float32 and x.is_contiguous(), "expected contiguous fp32 x")
@@ -267,9 +274,19 @@ def trimul(module, x, mask, outgoing, out_mode=OUT_BF16, out=None, workspace=Non
     if n:
         N.call("bmx_trimul_fwd", x.data_ptr(), mask.data_ptr(), n, int(bool(outgoing)), niw.data_ptr(),
                nib.data_ptr(), float(ni.eps), w_in.data_ptr(), now.data_ptr(), nob.data_ptr(), float(no.eps),
-               w_pout.data_ptr(), w_gout.data_ptr(), out.data_ptr(), out_mode, ws.data_ptr(), ws.numel(),
+               w_pout.data_ptr(), w_gout.data_ptr(), out.data_ptr(), out_mode, ws.data_ptr(), ws.numel(), stages,
                _stream(x))
     return out
+
+
+def workspace_bytes(n: int) -> int:
+    """Workspace that serves both fused triangle ops at size n."""
+    lib = N.lib()
+    return max(lib.bmx_trimul_workspace_bytes(n), lib.bmx_triattn_workspace_bytes(n))
+
+
+def new_workspace(n: int, device) -> torch.Tensor:
+    return _workspace(workspace_bytes(n), device)
 
 
 def _triattn_proj_weight(wq, wk, wv, wb):
@@ -280,11 +297,12 @@ def _triattn_proj_weight(wq, wk, wv, wb):
     return w
 
 
-def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=None):
+def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=None, stages=ALL_STAGES):
     """Fused TriangleAttention (starting or ending node) for x [N, N, 128].
 
     ``module`` carries Boltz's TriangleAttention parameters: ``layer_norm``,
-    ``linear`` (triangle bias), ``mha.linear_{q,k,v,g,o}``, ``inf``."""
+    ``linear`` (triangle bias), ``mha.linear_{q,k,v,g,o}``, ``inf``.
+    ``stages`` selects the kernels (1 projection, 2 attention core, 4 output)."""
     _cuda(x)
     _check(x.dim() == 3 and x.size(0) == x.size(1) and x.size(2) == C, "expected x of shape [N, N, 128]")
     _check(x.dtype in (torch.float32, torch.bfloat16) and x.is_contiguous(), "expected contiguous fp32/bf16 x")
@@ -309,7 +327,7 @@ def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=No
         N.call("bmx_triattn_fwd", x.data_ptr(), _code(x.dtype), None if mask is None else mask.data_ptr(), n,
                int(bool(starting)), float(module.inf), lnw.data_ptr(), lnb.data_ptr(), float(ln.eps),
                w_proj.data_ptr(), w_g.data_ptr(), b_g.data_ptr(), w_o.data_ptr(), b_o.data_ptr(), out.data_ptr(),
-               out_mode, ws.data_ptr(), ws.numel(), _stream(x))
+               out_mode, ws.data_ptr(), ws.numel(), stages, _stream(x))
     return out
 
 

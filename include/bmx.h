@@ -89,7 +89,11 @@ int bmx_bias_softmax(const void* scores, const void* bias, const float* mask, vo
 /* ---- Fused hot-path modules -------------------------------------------- */
 
 /* out_mode for the fused modules: 0 = write bf16 [n,n,128], 1 = write fp32,
- * 2 = add into fp32 `out` (residual stream; out may alias x). */
+ * 2 = add into fp32 `out` (residual stream; out may alias x),
+ * 3 = write fp32 out = x + y (out-of-place residual; out must not alias x).
+ * stages (trimul / triattn): bitmask of the kernels to launch, 1 = projection,
+ * 2 = contraction / attention core, 4 = output; 7 runs the whole module.  The
+ * workspace carries the intermediates between separately launched stages. */
 
 /* Workspace needed by bmx_trimul_fwd (bytes; 3 * 128 * np^2 bf16, np = round_up(n,128)). */
 size_t bmx_trimul_workspace_bytes(int64_t n);
@@ -100,7 +104,7 @@ size_t bmx_trimul_workspace_bytes(int64_t n);
 int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, const float* norm_in_w,
                    const float* norm_in_b, float eps_in, const void* w_in, const float* norm_out_w,
                    const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
-                   int out_mode, void* workspace, size_t workspace_bytes, bmx_stream_t stream);
+                   int out_mode, void* workspace, size_t workspace_bytes, int stages, bmx_stream_t stream);
 
 /* Workspace needed by bmx_triattn_fwd (bytes). */
 size_t bmx_triattn_workspace_bytes(int64_t n);
@@ -116,7 +120,7 @@ int bmx_triattn_proj_rows(void);
 int bmx_triattn_fwd(const void* x, int x_dtype, const float* mask, int64_t n, int starting, float inf,
                     const float* ln_w, const float* ln_b, float eps, const void* w_proj, const void* w_g,
                     const float* b_g, const void* w_o, const float* b_o, void* out, int out_mode, void* workspace,
-                    size_t workspace_bytes, bmx_stream_t stream);
+                    size_t workspace_bytes, int stages, bmx_stream_t stream);
 
 /* Transition(128, 512).forward on `rows` rows of 128 channels.
  * w12: bf16 [1024][128] = [fc1.weight; fc2.weight]; w3: bf16 [128][512] = fc3.weight.
