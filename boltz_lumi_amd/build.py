@@ -30,6 +30,9 @@ FLAGS = [
     "-Wno-unused-variable",
     # Packed fp32 VALU ops (v_pk_{add,mul,fma}_f32) are kept out of device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Keep MFMA accumulators in VGPRs: the default AGPR form costs a
+    # v_accvgpr_read/write per element whenever VALU code touches them.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", str(CSRC),
     "-I", str(PKG.parent / "include"),
 ]

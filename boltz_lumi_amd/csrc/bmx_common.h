@@ -126,6 +126,27 @@ __device__ __forceinline__ void ln_rows_to_lds(RowPtr row_ptr, const float* w, c
   }
 }
 
+// Output modes of the fused pair kernels (include/bmx.h).
+enum OutMode : int { kOutBF16 = 0, kOutF32 = 1, kOutAccumulate = 2, kOutResidual = 3 };
+
+constexpr int kYRow = kC + 4;  // fp32 LDS row used to re-layout results for row-wise stores
+
+// Store 4 consecutive channels of one result row.  y is the module output
+// (already rounded to bf16 precision); xres holds the same 4 input values
+// when the caller has them in registers (residual modes with out aliasing x
+// or out-of-place residual writes).
+__device__ __forceinline__ void store_row4(void* out, int64_t off, f32x4 y, f32x4 xres, int mode, bool x_in_regs) {
+  if (mode == kOutBF16) {
+    bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+    *(bf16x4*)((bf16*)out + off) = o;
+  } else if (mode == kOutF32) {
+    *(f32x4*)((float*)out + off) = y;
+  } else {
+    f32x4 base = (mode == kOutAccumulate && !x_in_regs) ? *(const f32x4*)((float*)out + off) : xres;
+    *(f32x4*)((float*)out + off) = base + y;
+  }
+}
+
 // A or B fragment (8 bf16) for k-step ks from a row-major tile with leading
 // dimension ld (elements); the fragment row is row0 + lane % 32.
 __device__ __forceinline__ bf16x8 frag(const bf16* base, int ld, int row0, int ks) {
@@ -141,6 +162,9 @@ __device__ __forceinline__ bf16x8 frag(const bf16* base, int ld, int row0, int k
 namespace bmx {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Compute units of the current device (cached per device; used to size
+// persistent grids).
+int device_cu_count();
 }  // namespace bmx
 
 #define BMX_OK 0

@@ -28,14 +28,18 @@ using namespace bmx;
 
 namespace {
 
-constexpr int kH = 4, kD = 32, kTP = 128, kPad = 128;
+constexpr int kH = 4, kD = 32, kTP = 128, kPad = 256;  // row padding: a multiple of both kTP and the attention query tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kProjRows = 3 * kC + 32;  // q, k, v, then H triangle-bias rows (+ zero rows)
+// Triangle-bias storage type.  bf16 halves the bias traffic of the attention
+// core; upstream's bf16 path rounds the bias to bf16 as well.
+using tb_t = bf16;
 
 struct Layout {
   int n, np;
   bf16 *q, *k, *vt, *o;
-  float *tb, *mb;
+  tb_t* tb;
+  float* mb;
 };
 
 __host__ __device__ inline int64_t qkv_elems(int np) { return (int64_t)np * kH * np * kD; }
@@ -104,7 +108,7 @@ __global__ __launch_bounds__(256) void triattn_proj_kernel(const TIn* __restrict
 #pragma unroll
           for (int r = 0; r < kH; ++r) {
             float v = j < n ? acc[r] * kLog2e : -INFINITY;
-            L.tb[((int64_t)r * np + i) * np + j] = v;
+            L.tb[((int64_t)r * np + i) * np + j] = (tb_t)v;
           }
         }
       }
@@ -117,192 +121,304 @@ constexpr int kKT = 64;             // keys per pipeline stage
 constexpr int kKLd = kD + 8;        // K tile row (bf16)
 constexpr int kVLd = kKT + 8;       // V^T tile row (bf16)
 
-__global__ __launch_bounds__(256) void triattn_core_kernel(Layout L) {
-  __shared__ __attribute__((aligned(16))) bf16 ks_lds[2][kKT * kKLd];
-  __shared__ __attribute__((aligned(16))) bf16 vs_lds[2][kD * kVLd];
+// Rescale the running output only when a query's max grows by more than
+// 2^kLazy: until then p = exp2(s - m) stays <= 2^kLazy, exact in fp32/bf16.
+constexpr float kLazy = 8.f;
+
+// Blocks are dispatched round-robin over the 8 XCDs.  A "column" is one
+// (head, query tile); every XCD owns a contiguous run of columns, so the
+// triangle-bias rows those columns re-read for every row i stay in that
+// XCD's L2 instead of being fetched again from HBM / MALL.
+constexpr int kCoreWaves = 4;              // waves per attention block
+constexpr int kCoreQ = 32 * kCoreWaves;    // queries per attention block
+constexpr int kCoreThreads = 64 * kCoreWaves;
+
+__host__ __device__ inline int core_qtiles(int n) { return (n + kCoreQ - 1) / kCoreQ; }
+__host__ __device__ inline int core_cols_per_xcd(int n) { return (kH * core_qtiles(n) + 7) / 8; }
+
+// Rows i processed together by one block: every triangle-bias tile loaded
+// into registers serves all of them, which divides the dominant bias
+// traffic (N x the [H, N, N] bias per direction) by kRows.
+constexpr int kRows = 2;
+
+template <bool MASKED>
+__device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0, bf16* ks, bf16* vs) {
+  constexpr int G = kRows;
+  constexpr int kKs = kKT * kKLd, kVs = kD * kVLd;  // per-row LDS tile sizes
   const int n = L.n, np = L.np;
-  const int qtiles = (n + kTP - 1) / kTP;
-  const int bid = blockIdx.x;
-  const int qt = bid % qtiles, h = (bid / qtiles) % kH, i = bid / (qtiles * kH);
-  const int t = threadIdx.x, l = lane_id(), w = t >> 6, hf = l >> 5;
-  const int q0 = qt * kTP + 32 * w;  // this wave's 32 queries
+  const int t = threadIdx.x, l = lane_id(), hf = l >> 5;
   const int nk = (n + kKT - 1) / kKT * kKT;
-
-  const float* mbrow = L.mb + (int64_t)i * np;
-  bool masked_row = false;
-  for (int k = t; k < n; k += 256) masked_row |= mbrow[k] != 0.f;
-  masked_row = __syncthreads_or(masked_row);
-
-  const bf16* kbase = L.k + ((int64_t)i * kH + h) * np * kD;
-  const bf16* vbase = L.vt + ((int64_t)i * kH + h) * kD * np;
-  const float* tbrow = L.tb + ((int64_t)h * np + q0 + (l & 31)) * np;
-
-  // Q^T fragments (B operand): lane = query, 8 consecutive d per k-step.
-  const bf16* qbase = L.q + (((int64_t)i * kH + h) * np + q0) * kD;
-  const bf16x8 qf0 = frag(qbase, kD, 0, 0), qf1 = frag(qbase, kD, 0, 1);
-
-  bf16x8 rk, rv;
+  const tb_t* tbrow = L.tb + ((int64_t)h * np + q0 + (l & 31)) * np;
+  const bf16* kb[G];
+  const bf16* vb[G];
+  const float* mbr[G];
+  bf16x8 qf[G][2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int i = min(i0 + g, n - 1);  // rows past n repeat row n-1 and are not stored
+    kb[g] = L.k + ((int64_t)i * kH + h) * np * kD;
+    vb[g] = L.vt + ((int64_t)i * kH + h) * kD * np;
+    mbr[g] = L.mb + (int64_t)i * np;
+    const bf16* qbase = L.q + (((int64_t)i * kH + h) * np + q0) * kD;
+    qf[g][0] = frag(qbase, kD, 0, 0);
+    qf[g][1] = frag(qbase, kD, 0, 1);
+  }
+  f32x16 o[G];
+  float m[G], lsum[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    o[g] = zero16();
+    m[g] = -INFINITY;
+    lsum[g] = 0.f;
+  }
+  // Per row and stage: K tile 64 keys x 32 d and V^T tile 32 d x 64 keys,
+  // 256 chunks of 8 each; chunk c < 256 is K, c >= 256 is V^T.
+  constexpr int kPer = 512 / kCoreThreads;
+  static_assert(kPer * kCoreThreads == 512, "K/V chunks must split evenly over the block");
+  bf16x8 rkv[G][kPer];
   auto gload = [&](int k0) {
-    // K tile: 64 keys x 32 d -> 256 chunks of 8; V^T tile: 32 d x 64 keys.
-    rk = *(const bf16x8*)(kbase + (int64_t)(k0 + (t >> 2)) * kD + (t & 3) * 8);
-    rv = *(const bf16x8*)(vbase + (int64_t)(t >> 3) * np + k0 + (t & 7) * 8);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int c = 0; c < kPer; ++c) {
+        const int idx = t + kCoreThreads * c, u = idx & 255;
+        rkv[g][c] = idx < 256 ? *(const bf16x8*)(kb[g] + (int64_t)(k0 + (u >> 2)) * kD + (u & 3) * 8)
+                              : *(const bf16x8*)(vb[g] + (int64_t)(u >> 3) * np + k0 + (u & 7) * 8);
+      }
   };
   auto sstore = [&](int buf) {
-    *(bf16x8*)(&ks_lds[buf][(t >> 2) * kKLd + (t & 3) * 8]) = rk;
-    *(bf16x8*)(&vs_lds[buf][(t >> 3) * kVLd + (t & 7) * 8]) = rv;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int c = 0; c < kPer; ++c) {
+        const int idx = t + kCoreThreads * c, u = idx & 255;
+        bf16* dst = idx < 256 ? ks + (buf * G + g) * kKs + (u >> 2) * kKLd + (u & 3) * 8
+                              : vs + (buf * G + g) * kVs + (u >> 3) * kVLd + (u & 7) * 8;
+        *(bf16x8*)dst = rkv[g][c];
+      }
   };
-
-  f32x16 o = zero16();
-  float m = -INFINITY, lsum = 0.f;
   gload(0);
   sstore(0);
   __syncthreads();
   for (int k0 = 0; k0 < nk; k0 += kKT) {
     const int cur = (k0 / kKT) & 1;
-    if (k0 + kKT < nk) gload(k0 + kKT);
-    f32x16 s[2];
+    const bool more = k0 + kKT < nk;
+    // Triangle-bias C tiles for these 64 keys: lane = query, register r -> key drow(r).
+    f32x16 cb[2];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      // C operand: bias^T tile, lane = query, register r -> key drow(r).
-      const int kb = k0 + 32 * sub + 4 * hf;
-      f32x16 c;
+    for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        f32x4 v = *(const f32x4*)(tbrow + kb + 8 * g);
-        if (masked_row) v = v + *(const f32x4*)(mbrow + kb + 8 * g);
-        c[4 * g] = v[0];
-        c[4 * g + 1] = v[1];
-        c[4 * g + 2] = v[2];
-        c[4 * g + 3] = v[3];
+      for (int gq = 0; gq < 4; ++gq) {
+        f32x4 v = load4(tbrow + k0 + 32 * sub + 4 * hf + 8 * gq);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cb[sub][4 * gq + e] = v[e];
       }
-      const bf16* kt = &ks_lds[cur][32 * sub * kKLd];
-      c = mfma32(frag(kt, kKLd, 0, 0), qf0, c);
-      s[sub] = mfma32(frag(kt, kKLd, 0, 1), qf1, c);
-    }
-    float mt = s[0][0];
+    if (more) gload(k0 + kKT);
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[0][r]);
+    for (int g = 0; g < G; ++g) {
+      const bf16* kt = ks + (cur * G + g) * kKs;
+      f32x16 s[2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[1][r]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float mn = fmaxf(m, mt);
-    const float alpha = __builtin_amdgcn_exp2f(m - mn);
-    m = mn;
-    lsum *= alpha;
-    o = o * alpha;
+      for (int sub = 0; sub < 2; ++sub) {
+        f32x16 c = cb[sub];
+        if (MASKED) {
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const bf16* vt = &vs_lds[cur][32 * sub];
+          for (int gq = 0; gq < 4; ++gq) {
+            f32x4 v = *(const f32x4*)(mbr[g] + k0 + 32 * sub + 4 * hf + 8 * gq);
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        bf16x8 pf, vf;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float p = __builtin_amdgcn_exp2f(s[sub][8 * st + e] - mn);
-          lsum += p;
-          pf[e] = (bf16)p;
+            for (int e = 0; e < 4; ++e) c[4 * gq + e] += v[e];
+          }
         }
-        // V^T fragment with the key order of P's D-layout registers.
-        const bf16* vr = vt + (l & 31) * kVLd + 16 * st + 4 * hf;
-        bf16x4 v0 = *(const bf16x4*)vr, v1 = *(const bf16x4*)(vr + 8);
-        vf = bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-        o = mfma32(vf, pf, o);
+        const bf16* ksub = kt + 32 * sub * kKLd;
+        s[sub] = mfma32(frag(ksub, kKLd, 0, 1), qf[g][1], mfma32(frag(ksub, kKLd, 0, 0), qf[g][0], c));
       }
+      float mt = s[0][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[0][r]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[1][r]);
+      mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+      if (__any(mt > m[g] + kLazy)) {  // wave-uniform; rare after the first tiles
+        const float mn = fmaxf(m[g], mt);
+        const float alpha = __builtin_amdgcn_exp2f(m[g] - mn);
+        m[g] = mn;
+        lsum[g] *= alpha;
+        o[g] = o[g] * alpha;
+      }
+      const bf16* vt = vs + (cur * G + g) * kVs;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          bf16x8 pf;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float p = __builtin_amdgcn_exp2f(s[sub][8 * st + e] - m[g]);
+            lsum[g] += p;
+            pf[e] = (bf16)p;
+          }
+          // V^T fragment with the key order of P's D-layout registers.
+          const bf16* vr = vt + (l & 31) * kVLd + 32 * sub + 16 * st + 4 * hf;
+          bf16x4 v0 = *(const bf16x4*)vr, v1 = *(const bf16x4*)(vr + 8);
+          bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          o[g] = mfma32(vf, pf, o[g]);
+        }
     }
-    if (k0 + kKT < nk) sstore(cur ^ 1);
+    if (more) sstore(cur ^ 1);
     __syncthreads();
   }
-  lsum += __shfl_xor(lsum, 32, kWave);
-  const int q = q0 + (l & 31);
-  if (q < n) {
-    const float inv = 1.f / lsum;
-    bf16* dst = L.o + ((int64_t)i * n + q) * kC + h * kD + 4 * hf;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      bf16x4 pk = {(bf16)(o[4 * g] * inv), (bf16)(o[4 * g + 1] * inv), (bf16)(o[4 * g + 2] * inv),
-                   (bf16)(o[4 * g + 3] * inv)};
-      *(bf16x4*)(dst + 8 * g) = pk;
+  for (int g = 0; g < G; ++g) {
+    const float ls = lsum[g] + __shfl_xor(lsum[g], 32, kWave);
+    const int q = q0 + (l & 31);
+    if (i0 + g < n && q < n) {
+      const float inv = 1.f / ls;
+      bf16* dst = L.o + ((int64_t)(i0 + g) * n + q) * kC + h * kD + 4 * hf;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        bf16x4 pk = {(bf16)(o[g][4 * gq] * inv), (bf16)(o[g][4 * gq + 1] * inv), (bf16)(o[g][4 * gq + 2] * inv),
+                     (bf16)(o[g][4 * gq + 3] * inv)};
+        *(bf16x4*)(dst + 8 * gq) = pk;
+      }
     }
   }
 }
 
-// ------------------------------------------------------------------ K3
-template <typename TIn>
-__global__ __launch_bounds__(256) void triattn_out_kernel(const TIn* x, const float* __restrict__ ln_w,
-                                                          const float* __restrict__ ln_b, float eps,
-                                                          const bf16* __restrict__ w_g, const float* __restrict__ b_g,
-                                                          const bf16* __restrict__ w_o, const float* __restrict__ b_o,
-                                                          int starting, void* out, int out_mode, Layout L) {
-  __shared__ __attribute__((aligned(16))) bf16 xg[kTP * kLdsRow];  // LN(x'), then unused
-  __shared__ __attribute__((aligned(16))) bf16 xo[kTP * kLdsRow];  // attention output, then o * gate
-  const int i = blockIdx.y, j0 = blockIdx.x * kTP;
-  const int n = L.n;
-  const int t = threadIdx.x, l = lane_id(), w = t >> 6;
-  auto row_ptr = [&](int p) -> const TIn* {
-    int j = j0 + p;
-    return j < n ? xrow(x, n, starting, i, j) : nullptr;
-  };
-  ln_rows_to_lds<kTP, TIn>(row_ptr, ln_w, ln_b, eps, xg);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    int idx = t + 256 * u, p = idx >> 4, chunk = idx & 15;
-    bf16x8 v = {};
-    if (j0 + p < n) v = *(const bf16x8*)(L.o + ((int64_t)i * n + j0 + p) * kC + chunk * 8);
-    *(bf16x8*)(xo + p * kLdsRow + chunk * 8) = v;
-  }
-  __syncthreads();
+__host__ __device__ inline int core_row_groups(int n) { return (n + kRows - 1) / kRows; }
 
-  // Gate: D[pair][ch], lane = channel c0 + l%32.
-  const int c0 = 32 * w, ch = c0 + (l & 31);
-  {
-    bf16x8 wf[8];
+__global__ __launch_bounds__(kCoreThreads) void triattn_core_kernel(Layout L) {
+  __shared__ __attribute__((aligned(16))) bf16 ks_lds[2 * kRows * kKT * kKLd];
+  __shared__ __attribute__((aligned(16))) bf16 vs_lds[2 * kRows * kD * kVLd];
+  const int n = L.n, np = L.np;
+  const int qtiles = core_qtiles(n);
+  const int cpx = core_cols_per_xcd(n);
+  const int bid = blockIdx.x;
+  const int idx = bid >> 3;
+  const int col = (bid & 7) * cpx + idx % cpx, ig = idx / cpx;
+  if (col >= kH * qtiles) return;  // uniform over the block
+  const int h = col / qtiles, qt = col % qtiles;
+  const int t = threadIdx.x, w = t >> 6;
+  const int i0 = ig * kRows;
+  const int q0 = qt * kCoreQ + 32 * w;  // this wave's 32 queries (< np: np is a multiple of kCoreQ)
+
+  bool masked = false;
+  for (int g = 0; g < kRows && i0 + g < n; ++g) {
+    const float* mbrow = L.mb + (int64_t)(i0 + g) * np;
+    for (int k = t; k < n; k += kCoreThreads) masked |= mbrow[k] != 0.f;
+  }
+  masked = __syncthreads_or(masked);
+  if (masked)
+    core_rows<true>(L, i0, h, q0, ks_lds, vs_lds);
+  else
+    core_rows<false>(L, i0, h, q0, ks_lds, vs_lds);
+}
+
+// ------------------------------------------------------------------ K3
+// Persistent and weight-stationary; a tile is 64 positions (i, j0..j0+63) of
+// the row frame.  Input rows stay in registers from the prefetch to the
+// residual store, so x is read once; results are re-laid out through LDS.
+constexpr int kP3 = 64;
+
+template <typename TIn>
+__global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const float* __restrict__ ln_w,
+                                                             const float* __restrict__ ln_b, float eps,
+                                                             const bf16* __restrict__ w_g,
+                                                             const float* __restrict__ b_g,
+                                                             const bf16* __restrict__ w_o,
+                                                             const float* __restrict__ b_o, int starting, void* out,
+                                                             int out_mode, Layout L) {
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * kP3 * kLdsRow];
+  bf16* xg = smem;                   // LN(x'), pairs x channels
+  bf16* xo = smem + kP3 * kLdsRow;   // attention output, then o * gate
+  float* ybuf = (float*)smem;        // fp32 result rows (aliases both)
+  static_assert(kP3 * kYRow * 4 <= 2 * kP3 * kLdsRow * 2, "ybuf must fit in the tile buffers");
+  const int n = L.n;
+  const int t = threadIdx.x, l = lane_id(), w = t >> 6, c0 = 32 * w, ch = c0 + (l & 31);
+  const int hw = t >> 5, hl = t & 31;
+  const int tiles_x = (n + kP3 - 1) / kP3, total = n * tiles_x;
+  const bool x_in_regs = out_mode == kOutResidual || (const void*)x == out;
+
+  bf16x8 wg[8], wo[8];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) wf[ks] = frag(w_g, kC, c0, ks);
-    const float bg = b_g[ch];
-    float gv[4][16];
+  for (int ks = 0; ks < 8; ++ks) {
+    wg[ks] = frag(w_g, kC, c0, ks);
+    wo[ks] = frag(w_o, kC, c0, ks);
+  }
+  const float bg = b_g[ch], bo = b_o[ch];
+
+  constexpr int kRowsPer = kP3 / 8;
+  f32x4 px[kRowsPer];
+  bf16x4 po[kRowsPer];
+  auto fetch = [&](int tile) {
+    const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int u = 0; u < kRowsPer; ++u) {
+      const int j = j0 + hw + 8 * u;
+      if (j < n) {
+        px[u] = load4(xrow(x, n, starting, i, j) + 4 * hl);
+        po[u] = *(const bf16x4*)(L.o + ((int64_t)i * n + j) * kC + 4 * hl);
+      } else {
+        px[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        po[u] = bf16x4{};
+      }
+    }
+  };
+
+  int tile = blockIdx.x;
+  if (tile < total) fetch(tile);
+  for (; tile < total; tile += gridDim.x) {
+    const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
+    f32x4 xc[kRowsPer];
+#pragma unroll
+    for (int u = 0; u < kRowsPer; ++u) {
+      xc[u] = px[u];
+      f32x4 y = ln128_half(px[u], ln_w, ln_b, hl, eps);
+      bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+      *(bf16x4*)(xg + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
+      *(bf16x4*)(xo + (hw + 8 * u) * kLdsRow + 4 * hl) = po[u];
+    }
+    __syncthreads();
+    if (tile + (int)gridDim.x < total) fetch(tile + gridDim.x);
+
+    // Gate: D[pair][ch], lane = channel.  Each (pair, channel) of xo is owned
+    // by exactly one lane, so the in-place multiply needs no barrier.
+#pragma unroll
+    for (int nt = 0; nt < kP3 / 32; ++nt) {
       f32x16 acc = zero16();
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) acc = mfma32(frag(xg, kLdsRow, nt * 32, ks), wf[ks], acc);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) gv[nt][r] = rbf(sigmoid_f(rbf(acc[r] + bg)));
-    }
-    // Each (pair, channel) of xo is owned by exactly one lane here.
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+      for (int ks = 0; ks < 8; ++ks) acc = mfma32(frag(xg, kLdsRow, nt * 32, ks), wg[ks], acc);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         bf16* e = xo + (nt * 32 + drow(r, l)) * kLdsRow + ch;
-        *e = (bf16)((float)*e * gv[nt][r]);
+        *e = (bf16)((float)*e * rbf(sigmoid_f(rbf(acc[r] + bg))));
       }
-  }
-  __syncthreads();
-  bf16x8 wf[8];
-#pragma unroll
-  for (int ks = 0; ks < 8; ++ks) wf[ks] = frag(w_o, kC, c0, ks);
-  const float bo = b_o[ch];
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    f32x16 acc = zero16();
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) acc = mfma32(frag(xo, kLdsRow, nt * 32, ks), wf[ks], acc);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      int j = j0 + nt * 32 + drow(r, l);
-      if (j >= n) continue;
-      float y = rbf(acc[r] + bo);
-      int64_t pair = starting ? (int64_t)i * n + j : (int64_t)j * n + i;
-      int64_t off = pair * kC + ch;
-      if (out_mode == 0)
-        ((bf16*)out)[off] = (bf16)y;
-      else if (out_mode == 1)
-        ((float*)out)[off] = y;
-      else if (out_mode == 2)
-        ((float*)out)[off] += y;
-      else
-        ((float*)out)[off] = (float)x[off] + y;
     }
+    __syncthreads();
+    f32x16 res[kP3 / 32];
+#pragma unroll
+    for (int nt = 0; nt < kP3 / 32; ++nt) {
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) acc = mfma32(frag(xo, kLdsRow, nt * 32, ks), wo[ks], acc);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) res[nt][r] = rbf(acc[r] + bo);
+    }
+    __syncthreads();  // xg / xo are dead; ybuf aliases them
+#pragma unroll
+    for (int nt = 0; nt < kP3 / 32; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ybuf[(nt * 32 + drow(r, l)) * kYRow + ch] = res[nt][r];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kRowsPer; ++u) {
+      const int p = hw + 8 * u, j = j0 + p;
+      if (j < n) {
+        const f32x4 y = *(const f32x4*)(ybuf + p * kYRow + 4 * hl);
+        const int64_t pair = starting ? (int64_t)i * n + j : (int64_t)j * n + i;
+        store_row4(out, pair * kC + 4 * hl, y, xc[u], out_mode, x_in_regs);
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -322,8 +438,8 @@ Layout make_layout(void* ws, int n) {
   p += e * sizeof(bf16);
   L.o = (bf16*)p;
   p += round_up((int64_t)n * n * kC * sizeof(bf16), 256);
-  L.tb = (float*)p;
-  p += (int64_t)kH * L.np * L.np * sizeof(float);
+  L.tb = (tb_t*)p;
+  p += (int64_t)kH * L.np * L.np * sizeof(tb_t);
   L.mb = (float*)p;
   return L;
 }
@@ -333,19 +449,20 @@ int run(const TIn* x, const float* mask, int n, int starting, float inf, const f
         float eps, const bf16* w_proj, const bf16* w_g, const float* b_g, const bf16* w_o, const float* b_o,
         void* out, int out_mode, void* ws, int stages, hipStream_t st) {
   Layout L = make_layout(ws, n);
-  const int qtiles = (n + kTP - 1) / kTP;
   if (stages & 1) {
     triattn_proj_kernel<TIn><<<dim3(L.np / kTP, L.np), 256, 0, st>>>(x, mask, ln_w, ln_b, eps, w_proj, inf,
                                                                       starting, L);
     if (int rc = check_launch("triattn_proj")) return rc;
   }
   if (stages & 2) {
-    triattn_core_kernel<<<dim3((unsigned)((int64_t)n * kH * qtiles)), 256, 0, st>>>(L);
+    triattn_core_kernel<<<dim3((unsigned)(8ll * core_cols_per_xcd(n) * core_row_groups(n))), kCoreThreads, 0, st>>>(L);
     if (int rc = check_launch("triattn_core")) return rc;
   }
   if (stages & 4) {
-    triattn_out_kernel<TIn><<<dim3(qtiles, n), 256, 0, st>>>(x, ln_w, ln_b, eps, w_g, b_g, w_o, b_o, starting,
-                                                             out, out_mode, L);
+    const int total = n * ((n + kP3 - 1) / kP3);
+    const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
+    triattn_out_kernel<TIn><<<dim3(grid), 256, 0, st>>>(x, ln_w, ln_b, eps, w_g, b_g, w_o, b_o, starting, out,
+                                                        out_mode, L);
     if (int rc = check_launch("triattn_out")) return rc;
   }
   return BMX_OK;
@@ -358,7 +475,7 @@ extern "C" {
 size_t bmx_triattn_workspace_bytes(int64_t n) {
   if (n <= 0) return 0;
   int64_t np = round_up(n, kPad);
-  return (size_t)(3 * qkv_elems((int)np) * 2 + round_up(n * n * kC * 2, 256) + (int64_t)kH * np * np * 4 +
+  return (size_t)(3 * qkv_elems((int)np) * 2 + round_up(n * n * kC * 2, 256) + (int64_t)kH * np * np * (int64_t)sizeof(tb_t) +
                   np * np * 4);
 }
 

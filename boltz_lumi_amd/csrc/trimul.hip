@@ -26,86 +26,103 @@ using namespace bmx;
 
 namespace {
 
-constexpr int kTP = 128;               // pairs per K1 / K3 block
-constexpr int kStageRow = kTP + 8;     // staged plane rows (bf16)
 constexpr int kPlaneTile = 128;        // plane padding granularity
 
 // ------------------------------------------------------------------ K1
-__global__ __launch_bounds__(256) void trimul_proj_kernel(const float* __restrict__ x, const float* __restrict__ mask,
-                                                          const float* __restrict__ ln_w,
-                                                          const float* __restrict__ ln_b, float eps,
-                                                          const bf16* __restrict__ w_in, bf16* __restrict__ a_pl,
-                                                          bf16* __restrict__ b_pl, int n, int np, int outgoing) {
-  // X tile [kTP][kLdsRow] aliases the front of the output staging area
-  // stage[2][kC][kStageRow].
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * kC * kStageRow];
-  bf16* xt = smem;
-  const int rp = blockIdx.y;
-  const int t0 = blockIdx.x * kTP;
-  const int l = lane_id(), w = threadIdx.x >> 6;
+// Persistent and weight-stationary: each wave keeps its [p_in; g_in] rows for
+// 32 channels of a and of b in VGPRs for the life of the block, and the next
+// tile's input rows are prefetched into registers while the current tile is
+// projected, so HBM reads overlap the MFMA work.
+constexpr int kP1 = 64;                // pairs per K1 tile (one plane row segment)
+constexpr int kStage1 = kP1 + 8;       // staged plane rows (bf16)
 
-  auto row_ptr = [&](int p) -> const float* {
-    int t = t0 + p;
-    if (rp >= n || t >= n) return nullptr;
-    int64_t pair = outgoing ? (int64_t)rp * n + t : (int64_t)t * n + rp;
-    return x + pair * kC;
-  };
-  ln_rows_to_lds<kTP, float>(row_ptr, ln_w, ln_b, eps, xt);
-  __syncthreads();
-
-  // Wave w owns channels [32w, 32w+32) of a and of b.  Orientation: D[ch][pair]
-  // (A = weight rows, B = normalised pairs), so lane l holds pair l%32.
-  const int c0 = 32 * w;
-  uint32_t res[2][4][8];  // [a|b][pair tile][packed bf16 pairs of registers]
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    bf16x8 wp[8], wg[8];
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      wp[ks] = frag(w_in, kC, half * kC + c0, ks);
-      wg[ks] = frag(w_in, kC, 2 * kC + half * kC + c0, ks);
-    }
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      f32x16 ap = zero16(), ag = zero16();
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        bf16x8 xf = frag(xt, kLdsRow, nt * 32, ks);
-        ap = mfma32(wp[ks], xf, ap);
-        ag = mfma32(wg[ks], xf, ag);
-      }
-      const int t = t0 + nt * 32 + (l & 31);
-      float m = 0.f;
-      if (rp < n && t < n) m = mask[outgoing ? (int64_t)rp * n + t : (int64_t)t * n + rp];
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float v0 = rbf(rbf(rbf(ap[r]) * rbf(sigmoid_f(rbf(ag[r])))) * m);
-        float v1 = rbf(rbf(rbf(ap[r + 1]) * rbf(sigmoid_f(rbf(ag[r + 1])))) * m);
-        bf16x2 pk = {(bf16)v0, (bf16)v1};
-        res[half][nt][r >> 1] = __builtin_bit_cast(uint32_t, pk);
-      }
-    }
-  }
-  __syncthreads();  // X tile is dead; reuse LDS as the staging area
-#pragma unroll
-  for (int half = 0; half < 2; ++half)
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        bf16x2 pk = __builtin_bit_cast(bf16x2, res[half][nt][r >> 1]);
-        int ch = c0 + drow(r, l);
-        smem[(half * kC + ch) * kStageRow + nt * 32 + (l & 31)] = pk[r & 1];
-      }
-  __syncthreads();
+__global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ mask,
+                                                             const float* __restrict__ ln_w,
+                                                             const float* __restrict__ ln_b, float eps,
+                                                             const bf16* __restrict__ w_in, bf16* __restrict__ a_pl,
+                                                             bf16* __restrict__ b_pl, int n, int np, int outgoing) {
+  __shared__ __attribute__((aligned(16))) bf16 xt[kP1 * kLdsRow];
+  __shared__ __attribute__((aligned(16))) bf16 stage[2 * kC * kStage1];
+  const int l = lane_id(), w = threadIdx.x >> 6, c0 = 32 * w;
+  const int hw = threadIdx.x >> 5, hl = threadIdx.x & 31;
+  const int tiles_x = np / kP1, total = np * tiles_x;
   const int64_t plane = (int64_t)np * np;
+
+  // Weight rows for this wave: p(a), g(a), p(b), g(b) of channels c0..c0+31.
+  bf16x8 wf[4][8];
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    int idx = threadIdx.x + 256 * u;
-    int half = idx >> 11, ch = (idx >> 4) & 127, chunk = idx & 15;
-    bf16x8 v = *(const bf16x8*)(smem + (half * kC + ch) * kStageRow + chunk * 8);
-    bf16* dst = (half ? b_pl : a_pl) + ch * plane + (int64_t)rp * np + t0 + chunk * 8;
-    *(bf16x8*)dst = v;
+  for (int q = 0; q < 4; ++q) {
+    const int row0 = (q & 1) * 2 * kC + (q >> 1) * kC + c0;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) wf[q][ks] = frag(w_in, kC, row0, ks);
+  }
+
+  // Input row p of a tile is pair (rp, t0+p) (outgoing) or (t0+p, rp) (incoming).
+  f32x4 pre[kP1 / 8];
+  auto fetch = [&](int tile) {
+    const int rp = tile / tiles_x, t0 = (tile % tiles_x) * kP1;
+#pragma unroll
+    for (int u = 0; u < kP1 / 8; ++u) {
+      const int tt = t0 + hw + 8 * u;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (rp < n && tt < n) {
+        const int64_t pair = outgoing ? (int64_t)rp * n + tt : (int64_t)tt * n + rp;
+        v = load4(x + pair * kC + 4 * hl);
+      }
+      pre[u] = v;
+    }
+  };
+
+  int tile = blockIdx.x;
+  if (tile < total) fetch(tile);
+  for (; tile < total; tile += gridDim.x) {
+    const int rp = tile / tiles_x, t0 = (tile % tiles_x) * kP1;
+#pragma unroll
+    for (int u = 0; u < kP1 / 8; ++u) {
+      const int tt = t0 + hw + 8 * u;
+      f32x4 y = ln128_half(pre[u], ln_w, ln_b, hl, eps);
+      if (rp >= n || tt >= n) y = f32x4{0.f, 0.f, 0.f, 0.f};
+      bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+      *(bf16x4*)(xt + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
+    }
+    __syncthreads();
+    if (tile + (int)gridDim.x < total) fetch(tile + gridDim.x);
+
+    // D[ch][pair]: A = weight rows, B = normalised pairs; lane l holds pair l%32.
+#pragma unroll
+    for (int nt = 0; nt < kP1 / 32; ++nt) {
+      const int tt = t0 + nt * 32 + (l & 31);
+      float m = 0.f;
+      if (rp < n && tt < n) m = mask[outgoing ? (int64_t)rp * n + tt : (int64_t)tt * n + rp];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        f32x16 ap = zero16(), ag = zero16();
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+          bf16x8 xf = frag(xt, kLdsRow, nt * 32, ks);
+          ap = mfma32(wf[2 * half][ks], xf, ap);
+          ag = mfma32(wf[2 * half + 1][ks], xf, ag);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          // bf16(bf16(p) * bf16(sigmoid(bf16(g)))) * mask, rounded as upstream does
+          const float v = rbf(rbf(rbf(ap[r]) * rbf(sigmoid_f(rbf(ag[r])))) * m);
+          stage[(half * kC + c0 + drow(r, l)) * kStage1 + nt * 32 + (l & 31)] = (bf16)v;
+        }
+      }
+    }
+    __syncthreads();
+    // 2 operands x 128 channels x 8 chunks of 8 positions
+#pragma unroll
+    for (int u = 0; u < 2 * kC * (kP1 / 8) / 256; ++u) {
+      const int idx = threadIdx.x + 256 * u;
+      const int half = idx / (kC * (kP1 / 8)), ch = (idx / (kP1 / 8)) % kC, chunk = idx % (kP1 / 8);
+      const bf16x8 v = *(const bf16x8*)(stage + (half * kC + ch) * kStage1 + chunk * 8);
+      bf16* dst = (half ? b_pl : a_pl) + ch * plane + (int64_t)rp * np + t0 + chunk * 8;
+      *(bf16x8*)dst = v;
+    }
+    __syncthreads();
   }
 }
 
@@ -208,77 +225,115 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
 }
 
 // ------------------------------------------------------------------ K3
-__global__ __launch_bounds__(256) void trimul_out_kernel(const float* x, const bf16* __restrict__ o_pl,
-                                                         const float* __restrict__ in_w, const float* __restrict__ in_b,
-                                                         float eps_in, const float* __restrict__ out_w,
-                                                         const float* __restrict__ out_b, float eps_out,
-                                                         const bf16* __restrict__ w_pout,
-                                                         const bf16* __restrict__ w_gout, void* out,
-                                                         int out_mode, int n, int np) {
-  __shared__ __attribute__((aligned(16))) bf16 xo[kTP * kLdsRow];  // LN_out(O), pairs x channels
-  __shared__ __attribute__((aligned(16))) bf16 xg[kTP * kLdsRow];  // LN_in(x), pairs x channels
-  const int i = blockIdx.y, j0 = blockIdx.x * kTP;
-  const int t = threadIdx.x, l = lane_id(), w = t >> 6;
+// Persistent and weight-stationary like K1.  A tile is 64 pairs (i, j0..j0+63).
+// The input rows stay in registers (row layout: a half-wave per row, 4
+// channels per lane) from the prefetch to the residual store, so x is read
+// from HBM exactly once; the MFMA result is re-laid out through LDS.
+constexpr int kP3 = 64;
+
+__global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, const bf16* __restrict__ o_pl,
+                                                            const float* __restrict__ in_w,
+                                                            const float* __restrict__ in_b, float eps_in,
+                                                            const float* __restrict__ out_w,
+                                                            const float* __restrict__ out_b, float eps_out,
+                                                            const bf16* __restrict__ w_pout,
+                                                            const bf16* __restrict__ w_gout, void* out, int out_mode,
+                                                            int n, int np) {
+  // xo: LN_out(O) and xg: LN_in(x), pairs x channels; ybuf (fp32) aliases both.
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * kP3 * kLdsRow];
+  bf16* xo = smem;
+  bf16* xg = smem + kP3 * kLdsRow;
+  float* ybuf = (float*)smem;
+  static_assert(kP3 * kYRow * 4 <= 2 * kP3 * kLdsRow * 2, "ybuf must fit in the tile buffers");
+  const int t = threadIdx.x, l = lane_id(), w = t >> 6, c0 = 32 * w;
+  const int hw = t >> 5, hl = t & 31;
+  const int tiles_x = (n + kP3 - 1) / kP3, total = n * tiles_x;
   const int64_t plane = (int64_t)np * np;
+  const bool x_in_regs = out_mode == kOutResidual || (const void*)x == out;
 
-  // Product tile O[c][i][j0..j0+127] -> xo[p][c] (transposed through LDS).
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    int idx = t + 256 * u, c = idx >> 4, chunk = idx & 15;
-    bf16x8 v = *(const bf16x8*)(o_pl + c * plane + (int64_t)i * np + j0 + chunk * 8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xo[(chunk * 8 + e) * kLdsRow + c] = v[e];
-  }
-  auto row_ptr = [&](int p) -> const float* {
-    return (j0 + p < n) ? x + ((int64_t)i * n + j0 + p) * kC : nullptr;
-  };
-  ln_rows_to_lds<kTP, float>(row_ptr, in_w, in_b, eps_in, xg);
-  __syncthreads();
-  {
-    const int hw = t >> 5, hl = t & 31;
-#pragma unroll 4
-    for (int u = 0; u < kTP / 8; ++u) {
-      bf16* row = xo + (hw + 8 * u) * kLdsRow + 4 * hl;
-      f32x4 v = {(float)row[0], (float)row[1], (float)row[2], (float)row[3]};
-      f32x4 y = ln128_half(v, out_w, out_b, hl, eps_out);
-      bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
-      *(bf16x4*)row = o;
-    }
-  }
-  __syncthreads();
-
-  // D[pair][ch]: A = normalised pairs, B = weight rows; lane l holds channel c0 + l%32.
-  const int c0 = 32 * w;
   bf16x8 wp[8], wg[8];
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     wp[ks] = frag(w_pout, kC, c0, ks);
     wg[ks] = frag(w_gout, kC, c0, ks);
   }
-  const int ch = c0 + (l & 31);
+
+  constexpr int kRowsPer = kP3 / 8;                  // rows per half-wave
+  constexpr int kOChunks = kC * (kP3 / 8) / 256;     // 16-byte product chunks per thread
+  f32x4 px[kRowsPer];
+  bf16x8 po[kOChunks];
+  auto fetch = [&](int tile) {
+    const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    f32x16 ay = zero16(), ag = zero16();
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      ay = mfma32(frag(xo, kLdsRow, nt * 32, ks), wp[ks], ay);
-      ag = mfma32(frag(xg, kLdsRow, nt * 32, ks), wg[ks], ag);
+    for (int u = 0; u < kRowsPer; ++u) {
+      const int j = j0 + hw + 8 * u;
+      px[u] = j < n ? load4(x + ((int64_t)i * n + j) * kC + 4 * hl) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      int j = j0 + nt * 32 + drow(r, l);
-      if (j >= n) continue;
-      float y = rbf(rbf(ay[r]) * rbf(sigmoid_f(rbf(ag[r]))));
-      int64_t o = ((int64_t)i * n + j) * kC + ch;
-      if (out_mode == 0)
-        ((bf16*)out)[o] = (bf16)y;
-      else if (out_mode == 1)
-        ((float*)out)[o] = y;
-      else if (out_mode == 2)
-        ((float*)out)[o] += y;
-      else
-        ((float*)out)[o] = x[o] + y;
+    for (int u = 0; u < kOChunks; ++u) {
+      const int idx = t + 256 * u, c = idx / (kP3 / 8), chunk = idx % (kP3 / 8);
+      po[u] = *(const bf16x8*)(o_pl + c * plane + (int64_t)i * np + j0 + chunk * 8);
     }
+  };
+
+  int tile = blockIdx.x;
+  if (tile < total) fetch(tile);
+  for (; tile < total; tile += gridDim.x) {
+    const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
+    f32x4 xc[kRowsPer];
+#pragma unroll
+    for (int u = 0; u < kRowsPer; ++u) {
+      xc[u] = px[u];
+      f32x4 y = ln128_half(px[u], in_w, in_b, hl, eps_in);
+      bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+      *(bf16x4*)(xg + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
+    }
+#pragma unroll
+    for (int u = 0; u < kOChunks; ++u) {
+      const int idx = t + 256 * u, c = idx / (kP3 / 8), chunk = idx % (kP3 / 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xo[(chunk * 8 + e) * kLdsRow + c] = po[u][e];
+    }
+    __syncthreads();
+    if (tile + (int)gridDim.x < total) fetch(tile + gridDim.x);
+#pragma unroll
+    for (int u = 0; u < kRowsPer; ++u) {
+      bf16* row = xo + (hw + 8 * u) * kLdsRow + 4 * hl;
+      f32x4 v = {(float)row[0], (float)row[1], (float)row[2], (float)row[3]};
+      f32x4 y = ln128_half(v, out_w, out_b, hl, eps_out);
+      bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+      *(bf16x4*)row = o;
+    }
+    __syncthreads();
+
+    // D[pair][ch]: A = normalised pairs, B = weight rows; lane l holds channel c0 + l%32.
+    f32x16 res[kP3 / 32];
+#pragma unroll
+    for (int nt = 0; nt < kP3 / 32; ++nt) {
+      f32x16 ay = zero16(), ag = zero16();
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        ay = mfma32(frag(xo, kLdsRow, nt * 32, ks), wp[ks], ay);
+        ag = mfma32(frag(xg, kLdsRow, nt * 32, ks), wg[ks], ag);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) res[nt][r] = rbf(rbf(ay[r]) * rbf(sigmoid_f(rbf(ag[r]))));
+    }
+    __syncthreads();  // xo / xg are dead; ybuf aliases them
+#pragma unroll
+    for (int nt = 0; nt < kP3 / 32; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ybuf[(nt * 32 + drow(r, l)) * kYRow + c0 + (l & 31)] = res[nt][r];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kRowsPer; ++u) {
+      const int p = hw + 8 * u, j = j0 + p;
+      if (j < n) {
+        const f32x4 y = *(const f32x4*)(ybuf + p * kYRow + 4 * hl);
+        store_row4(out, ((int64_t)i * n + j) * kC + 4 * hl, y, xc[u], out_mode, x_in_regs);
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -320,8 +375,10 @@ int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, c
   bf16* o_pl = b_pl + plane;
 
   if (stages & 1) {
-    trimul_proj_kernel<<<dim3(np / kTP, np), 256, 0, stream>>>(x, mask, norm_in_w, norm_in_b, eps_in,
-                                                                (const bf16*)w_in, a_pl, b_pl, ni, np, outgoing);
+    const int total = np * (np / kP1);
+    const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
+    trimul_proj_kernel<<<dim3(grid), 256, 0, stream>>>(x, mask, norm_in_w, norm_in_b, eps_in, (const bf16*)w_in,
+                                                       a_pl, b_pl, ni, np, outgoing);
     if (int rc = check_launch("trimul_proj")) return rc;
   }
   if (stages & 2) {
@@ -332,7 +389,9 @@ int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, c
     if (int rc = check_launch("trimul_contract")) return rc;
   }
   if (stages & 4) {
-    trimul_out_kernel<<<dim3((ni + kTP - 1) / kTP, ni), 256, 0, stream>>>(
+    const int total = ni * ((ni + kP3 - 1) / kP3);
+    const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
+    trimul_out_kernel<<<dim3(grid), 256, 0, stream>>>(
         x, o_pl, norm_in_w, norm_in_b, eps_in, norm_out_w, norm_out_b, eps_out, (const bf16*)w_pout,
         (const bf16*)w_gout, out, out_mode, ni, np);
     if (int rc = check_launch("trimul_out")) return rc;
