@@ -1,0 +1,94 @@
+"""Install the gfx950 hot-path forwards on a Boltz-2 model.
+
+Reference: src/boltz_lumi/adapters.py:7-47.  Same mechanism: walk
+``model.named_modules()`` and rebind *instance* forwards with
+``types.MethodType``, selected by class name and module path; idempotent via a
+flag on the model; a no-op unless the model is a Boltz2 and the current device
+is a gfx950 GPU of a ROCm build (the reference checks gfx90a).
+
+Patched (class name, path rule -> replacement):
+  TriangleAttention, TriangleAttentionEndingNode   -> triangle.triangle_attention_forward
+      .layer_norm                                  -> triangle.normalization_forward
+      ._chunk (ending node)                        -> triangle.contiguous_mask_chunk
+  TriangleMultiplication{Outgoing,Incoming}        -> multiplication.normalized_forward
+  Transition named "*.transition_z"                -> pair_transition.transition_forward
+  AdaLN / ConditionedTransitionBlock under
+      "structure_module.score_model."              -> diffusion.adaln_forward / transition_forward
+Out of scope (left to upstream): token-transformer AttentionPairBias and the
+``structure_module.sample`` wrapper (reference adapters.py:39-46).
+"""
+
+from __future__ import annotations
+
+from types import MethodType
+
+from ._guards import gfx950_available
+
+TRIANGLE_ATTENTION = {"TriangleAttention", "TriangleAttentionEndingNode"}
+TRIANGLE_MULTIPLICATION = {"TriangleMultiplicationIncoming", "TriangleMultiplicationOutgoing"}
+SCORE_MODEL = "structure_module.score_model."
+
+FLAG = "_bmx_optimized"
+
+
+def _is_boltz2(model) -> bool:
+    return any(cls.__name__ == "Boltz2" for cls in type(model).__mro__)
+
+
+def install(model, *, require_boltz2: bool = True, require_device: bool = True):
+    """Patch the hot-path modules of ``model`` in place; returns the number of
+    patched modules (0 when nothing applies).
+
+    ``require_boltz2`` / ``require_device`` relax the model-class and
+    gfx950-device gates (used by tests that install on stand-in modules)."""
+    if require_boltz2 and not _is_boltz2(model):
+        return 0
+    if getattr(model, FLAG, False):
+        return 0
+    if require_device and not gfx950_available():
+        return 0
+    from . import _native
+
+    _native.lib()  # fail loudly here, not inside the first forward
+    from .diffusion import adaln_forward, transition_forward
+    from .multiplication import normalized_forward
+    from .pair_transition import transition_forward as pair_transition_forward
+    from .triangle import contiguous_mask_chunk, normalization_forward, triangle_attention_forward
+
+    patched = 0
+    for name, module in model.named_modules():
+        cls = type(module).__name__
+        if cls in TRIANGLE_ATTENTION:
+            module.forward = MethodType(triangle_attention_forward, module)
+            module.layer_norm.forward = MethodType(normalization_forward, module.layer_norm)
+            if cls == "TriangleAttentionEndingNode" and hasattr(type(module), "_chunk"):
+                module._chunk = MethodType(contiguous_mask_chunk, module)
+            patched += 1
+        elif cls in TRIANGLE_MULTIPLICATION:
+            module.forward = MethodType(normalized_forward, module)
+            patched += 1
+        elif cls == "Transition" and name.endswith(".transition_z"):
+            module.forward = MethodType(pair_transition_forward, module)
+            patched += 1
+        elif name.startswith(SCORE_MODEL) and cls == "AdaLN":
+            module.forward = MethodType(adaln_forward, module)
+            patched += 1
+        elif name.startswith(SCORE_MODEL) and cls == "ConditionedTransitionBlock":
+            module.forward = MethodType(transition_forward, module)
+            patched += 1
+    setattr(model, FLAG, True)
+    return patched
+
+
+def uninstall(model) -> int:
+    """Remove the instance-level patches installed by :func:`install`."""
+    removed = 0
+    for _, module in model.named_modules():
+        for owner, attr in ((module, "forward"), (module, "_chunk"), (getattr(module, "layer_norm", None), "forward")):
+            if owner is not None and attr in vars(owner) and isinstance(vars(owner)[attr], MethodType):
+                if vars(owner)[attr].__func__.__module__.startswith(__package__):
+                    del owner.__dict__[attr]
+                    removed += 1
+    if getattr(model, FLAG, False):
+        delattr(model, FLAG)
+    return removed

@@ -1,0 +1,82 @@
+"""Triangle attention forwards patched onto Boltz modules.
+
+Reference: src/boltz_lumi/triangle.py (contiguous_mask_chunk :18-22,
+ordered_triangle_forward :32-104, normalization_forward :107-146).  Here the
+whole ``TriangleAttention.forward`` is replaced: LayerNorm, the q/k/v/gate/
+triangle-bias projections, the attention and the output projection run in
+the three fused gfx950 kernels, so the ``[I, H, N, N]`` scores are never
+materialised and ``chunk_size`` needs no chunk loop.  Every forward falls back
+to the module's own class forward when a guard fails, as the reference does.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from ._guards import bf16_autocast, fp32_contiguous_on, gfx950_tensor, inference
+
+
+def _native_shape_ok(module, x) -> bool:
+    return (
+        getattr(module, "c_in", None) == 128
+        and getattr(module, "c_hidden", None) == 32
+        and getattr(module, "no_heads", None) == 4
+        and x.ndim == 4
+        and x.shape[1] == x.shape[2]
+        and x.shape[-1] == 128
+        and x.shape[1] <= 8192
+    )
+
+
+def triangle_attention_forward(self, x, mask=None, chunk_size=None, use_kernels=False):
+    """Drop-in for ``TriangleAttention{,EndingNode}.forward(x, mask, chunk_size, use_kernels)``.
+
+    Native under bf16 autocast (or for bf16 x) in inference; returns bf16 like
+    the upstream autocast path.  fp32 mode (autocast off, fp32 x) keeps the
+    upstream fp32 math so its 1e-4 tolerance holds."""
+    supported = (
+        not use_kernels
+        and inference(self)
+        and gfx950_tensor(x)
+        and _native_shape_ok(self, x)
+        and (bf16_autocast() or x.dtype == torch.bfloat16)
+        and x.dtype in (torch.float32, torch.bfloat16)
+        and (mask is None or tuple(mask.shape) == tuple(x.shape[:-1]))
+    )
+    if not supported:
+        return type(self).forward(self, x, mask, chunk_size=chunk_size, use_kernels=use_kernels)
+    starting = getattr(self, "starting", True)
+    out = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
+    ws = ops.new_workspace(x.shape[1], x.device)
+    for b in range(x.shape[0]):
+        mb = None if mask is None else mask[b].to(torch.float32).contiguous()
+        ops.triattn(self, x[b].contiguous(), mb, starting, ops.OUT_BF16, out[b], ws)
+    return out
+
+
+def normalization_forward(module, x):
+    """Drop-in for the triangle ``LayerNorm.forward`` (c_in (128,)): the
+    native LN128 with a bf16 result under bf16 autocast (the next op casts to
+    bf16 anyway; reference triangle.py:133-145)."""
+    eligible = (
+        inference(module)
+        and gfx950_tensor(x)
+        and x.dtype == torch.float32
+        and x.shape[-1] == 128
+        and getattr(module, "c_in", None) == (128,)
+        and fp32_contiguous_on(x.device, module.weight, module.bias)
+        and bf16_autocast()
+    )
+    if not eligible:
+        return type(module).forward(module, x)
+    flat = x.contiguous().reshape(-1, 128)
+    return ops.norm(flat, module.weight, module.bias, module.eps, False, bf16_output=True).reshape(x.shape)
+
+
+def contiguous_mask_chunk(self, x, tri_bias, mask_bias, mask, chunk_size, use_kernels=False):
+    """Ending-node ``_chunk`` with a dense ``mask_bias`` (reference triangle.py:18-22)."""
+    if x.shape[-3] > 384:  # upstream const.chunk_size_threshold
+        mask_bias = mask_bias.contiguous()
+    # The patch is an instance attribute; the class attribute is upstream's.
+    return type(self)._chunk(self, x, tri_bias, mask_bias, mask, chunk_size, use_kernels)
