@@ -35,6 +35,8 @@ def parse():
     p.add_argument("--cpu-n", type=int, default=None, help="token count of the CPU sample (default: --n)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--kernel-reps", type=int, default=3, help="repetitions of the per-kernel timing pass")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="first copy 1 GiB device-to-device (a kernel of known traffic for scaling PMC byte counters)")
     return p.parse_args()
 
 
@@ -62,6 +64,19 @@ def kernel_table(n: int):
         "triattn_out": (2 * n2 * 128 * 256, n2 * (512 + 256 + 512), "hbm"),
         "pair_transition": (2 * n2 * 128 * 1536, n2 * 1024, "hbm"),
     }
+
+
+def measured_traffic(kernel: str, n: int):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter
+    summary (FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy), when it was
+    taken at this N; None otherwise."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"hbm_traffic_n{n}.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return data.get("bytes_per_launch", {}).get(kernel) if data.get("n") == n else None
 
 
 def per_kernel_times(layer, s, z, mask, pair_mask, z_out, ws, reps):
@@ -133,6 +148,13 @@ def main():
 
     dev = torch.device("cuda:0")
     n = args.n
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, device=dev)  # 1 GiB of fp32
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     layer = init_weights(layers.PairformerLayer(), 0).to(dev).eval()
     g = torch.Generator().manual_seed(0)
     z = torch.randn(1, n, n, 128, generator=g).to(dev)
@@ -182,7 +204,7 @@ def main():
         "peak": PEAK_BF16_TFLOPS if d["bound"] == "mfma" else PEAK_HBM_GBS,
         "unit": "TFLOP/s" if d["bound"] == "mfma" else "GB/s",
         "frac": d["frac"],
-        "traffic": None,
+        "traffic": measured_traffic(dominant, n),
     }
     out = {
         "metric": "Pairformer layer ms @N=1024 bf16",

@@ -43,6 +43,7 @@ SIGNATURES = {
     "bmx_triattn_fwd": (c_int, [_P, c_int, _P, c_int64, c_int, c_float, _P, _P, c_float, _P, _P, _P, _P, _P, _P, c_int,
                                 _P, c_size_t, c_int, _P]),
     "bmx_pair_transition_fwd": (c_int, [_P, c_int, c_int64, _P, _P, c_float, _P, _P, _P, c_int, _P]),
+    "bmx_pair_bias_fwd": (c_int, [_P, c_int, c_int64, _P, _P, c_float, _P, c_int, _P, _P]),
 }
 
 

@@ -161,9 +161,13 @@ class AttentionPairBias(nn.Module):
         self.proj_o = nn.Linear(c_s, c_s, bias=False)
 
     def pair_bias(self, z):
-        """[B, N, N, c_z] -> [B, H, N, N]."""
+        """[B, N, N, c_z] -> [B, H, N, N]; the 128 -> 16 projection of the trunk
+        runs as one fused gfx950 kernel (LN + fp32 MFMA, head-major output)."""
         if not self.compute_pair_bias:
             return z.movedim(-1, 1)
+        norm, lin = self.proj_z[0], self.proj_z[1]
+        if z.is_cuda and z.shape[-1] == 128 and lin.weight.shape[0] == 16 and z.shape[1] == z.shape[2]:
+            return torch.stack([ops.pair_bias(norm, lin, z[b].contiguous()) for b in range(z.shape[0])])
         return self.proj_z(z).movedim(-1, 1)
 
     def forward(self, s, z, mask, k_in, multiplicity=1):
@@ -171,7 +175,9 @@ class AttentionPairBias(nn.Module):
         q = self.proj_q(s).view(b, -1, self.num_heads, self.head_dim).transpose(1, 2)
         k = self.proj_k(k_in).view(b, -1, self.num_heads, self.head_dim).transpose(1, 2)
         v = self.proj_v(k_in).view(b, -1, self.num_heads, self.head_dim).transpose(1, 2)
-        bias = self.pair_bias(z).repeat_interleave(multiplicity, 0).float()
+        bias = self.pair_bias(z).float()
+        if multiplicity != 1:
+            bias = bias.repeat_interleave(multiplicity, 0)
         g = torch.sigmoid(self.proj_g(s))
         logits = (q.float() @ k.float().transpose(-1, -2)) / math.sqrt(self.head_dim) + bias
         logits = logits + (1 - mask[:, None, None].float()) * -self.inf

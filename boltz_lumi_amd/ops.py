@@ -350,6 +350,25 @@ def pair_transition(module, x, out_mode=OUT_BF16, out=None):
     return out
 
 
+def pair_bias(proj_z_norm, proj_z_linear, z):
+    """fp32 ``Linear(LN(z))`` for 16 heads, returned head-major as [H, N, N]
+    (the layout AttentionPairBias adds to its logits); z is [N, N, 128]."""
+    _cuda(z)
+    _check(z.dim() == 3 and z.shape[-1] == C and z.dtype in (torch.float32, torch.bfloat16) and z.is_contiguous(),
+           "expected contiguous z of shape [N, N, 128]")
+    heads = proj_z_linear.weight.shape[0]
+    _check(heads == 16 and proj_z_linear.weight.shape[1] == C, "expected a 128 -> 16 projection")
+    w = cached_weight(proj_z_linear, "w32", (proj_z_linear.weight,), _f32)
+    lnw = cached_weight(proj_z_norm, "w32", (proj_z_norm.weight,), _f32)
+    lnb = cached_weight(proj_z_norm, "b32", (proj_z_norm.bias,), _f32)
+    out = torch.empty((heads, z.shape[0], z.shape[1]), device=z.device, dtype=torch.float32)
+    rows = z.shape[0] * z.shape[1]
+    if rows:
+        N.call("bmx_pair_bias_fwd", z.data_ptr(), _code(z.dtype), rows, lnw.data_ptr(), lnb.data_ptr(),
+               float(proj_z_norm.eps), w.data_ptr(), heads, out.data_ptr(), _stream(z))
+    return out
+
+
 def adaln_modulate(a, scale, shift, eps):
     """``sigmoid(scale) * LN_noaffine(a) + shift`` in one pass."""
     _cuda(a, scale, shift)

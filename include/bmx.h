@@ -128,6 +128,16 @@ int bmx_triattn_fwd(const void* x, int x_dtype, const float* mask, int64_t n, in
 int bmx_pair_transition_fwd(const void* x, int x_dtype, int64_t rows, const float* ln_w, const float* ln_b, float eps,
                             const void* w12, const void* w3, void* out, int out_mode, bmx_stream_t stream);
 
+/* ---- Sequence-stack pair bias (next to the hot path) ------------------- */
+
+/* bias[h][row] = sum_c LN(z[row])[c] * w[h][c] for heads = 16, fp32 math; out is
+ * [16][rows] fp32 (the [B,H,N,N] attention bias for one batch element).
+ * Replaces AttentionPairBias.proj_z = LayerNorm + Linear(128, 16) + Rearrange of the
+ * Pairformer sequence stack, which the reference leaves to torch (adapters.py:39-45;
+ * math restated at src/boltz_lumi/pair_bias.py:21-36). */
+int bmx_pair_bias_fwd(const void* z, int z_dtype, int64_t rows, const float* ln_w, const float* ln_b, float eps,
+                      const float* w, int heads, float* out, bmx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -88,3 +88,19 @@ def test_transition_s_uses_upstream_math(gpu):
         y = t(x)
         want = t.fc3(torch.nn.functional.silu(t.fc1(t.norm(x))) * t.fc2(t.norm(x)))
     assert torch.allclose(y, want)
+
+
+@pytest.mark.parametrize("n", [1, 37, 130])
+def test_pair_bias_matches_upstream_fp32(gpu, n):
+    g = torch.Generator().manual_seed(n)
+    ref = R.randomize(R.AttentionPairBias(384, 128, 16), generator=g)
+    z = torch.randn(1, n, n, 128, generator=g) * 2 + 0.3
+    with torch.no_grad():
+        want = ref.proj_z(z)  # [1, 16, n, n]
+    mine = layers.AttentionPairBias(384, 128, 16)
+    mine.load_state_dict(ref.state_dict())
+    mine = mine.to(gpu)
+    with torch.inference_mode():
+        got = mine.pair_bias(z.to(gpu))
+    assert got.shape == want.shape
+    assert max_rel(got, want) < 1e-5  # fp32 path
