@@ -37,7 +37,13 @@ enum Dtype : int { kF32 = 0, kBF16 = 1 };
 
 __device__ __forceinline__ float rbf(float x) { return (float)(bf16)x; }
 
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + __expf(-x)); }
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32; ~1 ulp each).  An IEEE division would cost ~10 VALU
+// instructions, which dominated the epilogues of the fused kernels.
+__device__ __forceinline__ float sigmoid_f(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+__device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 
 __device__ __forceinline__ float load_f(const float* p) { return *p; }
 __device__ __forceinline__ float load_f(const bf16* p) { return (float)*p; }

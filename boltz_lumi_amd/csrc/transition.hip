@@ -50,9 +50,7 @@ __global__ __launch_bounds__(256) void pair_transition_kernel(const TIn* x, cons
         // D[pair][hidden]: lane = hidden channel c0 + l%32.
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float u = rbf(a1[r]);
-          float act = rbf(u / (1.f + __expf(-u)));
-          hid[(nt * 32 + drow(r, l)) * kLdsRow + c0 + (l & 31)] = (bf16)(act * rbf(a2[r]));
+          hid[(nt * 32 + drow(r, l)) * kLdsRow + c0 + (l & 31)] = (bf16)(silu_f(a1[r]) * a2[r]);
         }
       }
     }

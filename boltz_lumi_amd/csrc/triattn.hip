@@ -390,7 +390,7 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         bf16* e = xo + (nt * 32 + drow(r, l)) * kLdsRow + ch;
-        *e = (bf16)((float)*e * rbf(sigmoid_f(rbf(acc[r] + bg))));
+        *e = (bf16)((float)*e * sigmoid_f(acc[r] + bg));
       }
     }
     __syncthreads();

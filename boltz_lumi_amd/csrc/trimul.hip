@@ -106,8 +106,8 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          // bf16(bf16(p) * bf16(sigmoid(bf16(g)))) * mask, rounded as upstream does
-          const float v = rbf(rbf(rbf(ap[r]) * rbf(sigmoid_f(rbf(ag[r])))) * m);
+          // p * sigmoid(g) * mask, rounded once to the bf16 operand
+          const float v = ap[r] * sigmoid_f(ag[r]) * m;
           stage[(half * kC + c0 + drow(r, l)) * kStage1 + nt * 32 + (l & 31)] = (bf16)v;
         }
       }
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
         ag = mfma32(frag(xg, kLdsRow, nt * 32, ks), wg[ks], ag);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) res[nt][r] = rbf(rbf(ay[r]) * rbf(sigmoid_f(rbf(ag[r]))));
+      for (int r = 0; r < 16; ++r) res[nt][r] = rbf(ay[r] * sigmoid_f(ag[r]));  // the bf16 module output
     }
     __syncthreads();  // xo / xg are dead; ybuf aliases them
 #pragma unroll
