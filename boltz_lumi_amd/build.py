@@ -37,6 +37,13 @@ FLAGS = [
     "-I", str(PKG.parent / "include"),
 ]
 
+# Per-source additions.  The attention core takes running maxima over MFMA
+# results that are never NaN; without NaN semantics fmaxf needs no
+# canonicalising v_max per operand (half the max instructions).
+FILE_FLAGS = {
+    "triattn": ["-fno-honor-nans"],
+}
+
 
 def sources():
     return sorted(CSRC.glob("*.hip"))
@@ -44,7 +51,7 @@ def sources():
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.stem, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")

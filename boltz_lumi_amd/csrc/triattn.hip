@@ -20,8 +20,9 @@
 //                    write or add into the fp32 residual in place.
 //
 // Workspace (np = round_up(n, 128)):
-//   q[i][h][j][d], k[i][h][j][d], vt[i][h][d][j]  bf16, i < np, j < np
-//   tb[h][q][k] fp32 (k >= n is -inf), mb[i][k] fp32, o[i][j][h*32+d] bf16 (n x n)
+//   q[i][h][j][d], k[i][h][j][d], vt[i][h][d][j']  bf16, i < np, j < np, where
+//     j' = (j & ~31) + vperm(j & 31) permutes keys inside each 32-key block
+//   tb[h][q][k] bf16 (k >= n is -inf), mb[i][k] fp32, o[i][j][h*32+d] bf16 (n x n)
 #include "bmx_common.h"
 
 using namespace bmx;
@@ -43,6 +44,13 @@ struct Layout {
 };
 
 __host__ __device__ inline int64_t qkv_elems(int np) { return (int64_t)np * kH * np * kD; }
+
+// V^T rows keep each 32-key block in the order in which the attention core's
+// P operand holds keys: storage slot 8g + 4a + c holds key 16a + 4g + c, so the
+// 8 keys of lane group g are one contiguous 16-byte read.
+__host__ __device__ inline int vperm(int key_in_block) {
+  return ((key_in_block >> 2) & 3) * 8 + ((key_in_block >> 4) & 1) * 4 + (key_in_block & 3);
+}
 
 template <typename TIn>
 __device__ __forceinline__ const TIn* xrow(const TIn* x, int n, int starting, int i, int j) {
@@ -101,7 +109,8 @@ __global__ __launch_bounds__(256) void triattn_proj_kernel(const TIn* __restrict
         for (int ks = 0; ks < 8; ++ks) acc = mfma32(wf[ks], frag(xt, kLdsRow, nt * 32, ks), acc);
         const int j = j0 + nt * 32 + (l & 31);
         if (kind == 2) {
-          bf16* dst = L.vt + ((int64_t)i * kH + h) * kD * np + j;
+          // keys are stored permuted inside each 32-key block (see vperm)
+          bf16* dst = L.vt + ((int64_t)i * kH + h) * kD * np + (j & ~31) + vperm(j & 31);
 #pragma unroll
           for (int r = 0; r < 16; ++r) dst[(int64_t)drow(r, l) * np] = (bf16)acc[r];
         } else if (l < 32) {
@@ -117,6 +126,11 @@ __global__ __launch_bounds__(256) void triattn_proj_kernel(const TIn* __restrict
 }
 
 // ------------------------------------------------------------------ K2
+// MFMA shape of the attention core: v_mfma_f32_16x16x32_bf16 (lane l, group
+// g = l / 16): A holds A[l%16][8g .. 8g+7], B holds B[8g .. 8g+7][l%16], D
+// register r holds D[4g + r][l%16].  With 16 queries per wave the head dim
+// (32) is one K step and a wave's per-row state is small, so 8 waves x 2 rows
+// fit at 4 waves per SIMD.
 constexpr int kKT = 64;             // keys per pipeline stage
 constexpr int kKLd = kD + 8;        // K tile row (bf16)
 constexpr int kVLd = kKT + 8;       // V^T tile row (bf16)
@@ -125,77 +139,90 @@ constexpr int kVLd = kKT + 8;       // V^T tile row (bf16)
 // 2^kLazy: until then p = exp2(s - m) stays <= 2^kLazy, exact in fp32/bf16.
 constexpr float kLazy = 8.f;
 
-// Blocks are dispatched round-robin over the 8 XCDs.  A "column" is one
-// (head, query tile); every XCD owns a contiguous run of columns, so the
-// triangle-bias rows those columns re-read for every row i stay in that
-// XCD's L2 instead of being fetched again from HBM / MALL.
-constexpr int kCoreWaves = 4;              // waves per attention block
-constexpr int kCoreQ = 32 * kCoreWaves;    // queries per attention block
+constexpr int kCoreWaves = 8;              // waves per attention block
+constexpr int kCoreQ = 16 * kCoreWaves;    // queries per attention block
 constexpr int kCoreThreads = 64 * kCoreWaves;
 
+// Rows i processed together by one block: every triangle-bias tile loaded
+// into registers serves all of them, which divides the bias traffic
+// (N x the [H, N, N] bias per direction) by kRows.
+constexpr int kRows = 2;
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Blocks are dispatched round-robin over the 8 XCDs.  A "column" is one
+// (head, query tile); every XCD owns a contiguous run of columns, so the
+// triangle-bias rows those columns re-read for every row group stay in that
+// XCD's L2 instead of being fetched again from HBM / MALL.
 __host__ __device__ inline int core_qtiles(int n) { return (n + kCoreQ - 1) / kCoreQ; }
 __host__ __device__ inline int core_cols_per_xcd(int n) { return (kH * core_qtiles(n) + 7) / 8; }
-
-// Rows i processed together by one block: every triangle-bias tile loaded
-// into registers serves all of them, which divides the dominant bias
-// traffic (N x the [H, N, N] bias per direction) by kRows.
-constexpr int kRows = 2;
+__host__ __device__ inline int core_row_groups(int n) { return (n + kRows - 1) / kRows; }
 
 template <bool MASKED>
 __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0, bf16* ks, bf16* vs) {
   constexpr int G = kRows;
   constexpr int kKs = kKT * kKLd, kVs = kD * kVLd;  // per-row LDS tile sizes
   const int n = L.n, np = L.np;
-  const int t = threadIdx.x, l = lane_id(), hf = l >> 5;
+  const int t = threadIdx.x, l = lane_id(), g = l >> 4, lq = l & 15;
   const int nk = (n + kKT - 1) / kKT * kKT;
-  const tb_t* tbrow = L.tb + ((int64_t)h * np + q0 + (l & 31)) * np;
+  const tb_t* tbrow = L.tb + ((int64_t)h * np + q0 + lq) * np + 4 * g;
   const bf16* kb[G];
   const bf16* vb[G];
   const float* mbr[G];
-  bf16x8 qf[G][2];
+  bf16x8 qf[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const int i = min(i0 + g, n - 1);  // rows past n repeat row n-1 and are not stored
-    kb[g] = L.k + ((int64_t)i * kH + h) * np * kD;
-    vb[g] = L.vt + ((int64_t)i * kH + h) * kD * np;
-    mbr[g] = L.mb + (int64_t)i * np;
-    const bf16* qbase = L.q + (((int64_t)i * kH + h) * np + q0) * kD;
-    qf[g][0] = frag(qbase, kD, 0, 0);
-    qf[g][1] = frag(qbase, kD, 0, 1);
+  for (int r = 0; r < G; ++r) {
+    const int i = min(i0 + r, n - 1);  // rows past n repeat row n-1 and are not stored
+    kb[r] = L.k + ((int64_t)i * kH + h) * np * kD;
+    vb[r] = L.vt + ((int64_t)i * kH + h) * kD * np;
+    mbr[r] = L.mb + (int64_t)i * np + 4 * g;
+    // Q^T (B operand): query q0 + l%16, head dims 8g .. 8g+7
+    qf[r] = *(const bf16x8*)(L.q + (((int64_t)i * kH + h) * np + q0 + lq) * kD + 8 * g);
   }
-  f32x16 o[G];
-  float m[G], lsum[G];
+  // O^T tiles (d 0..15, 16..31) and the row sum l, which an MFMA with an
+  // all-ones A operand accumulates from the same bf16 P that multiplies V.
+  f32x4 o[G][2], ls[G];
+  // m: the max offset subtracted from this lane's scores.  Unmasked rows
+  // subtract it inside the QK^T MFMA chain (an extra K step with A = e0 and
+  // B = -m in bf16), so m is kept exactly bf16-representable; the offset
+  // cancels in o / l, so rounding it only has to keep p <= 2^(kLazy + 1).
+  float m[G];
+  bf16x8 qm[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    o[g] = zero16();
-    m[g] = -INFINITY;
-    lsum[g] = 0.f;
+  for (int r = 0; r < G; ++r) {
+    o[r][0] = o[r][1] = ls[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m[r] = MASKED ? -INFINITY : 0.f;
+    qm[r] = bf16x8{};
   }
+  bf16x8 ones, e0 = {};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (bf16)1.f;
+  if (g == 0) e0[0] = (bf16)1.f;
+
   // Per row and stage: K tile 64 keys x 32 d and V^T tile 32 d x 64 keys,
   // 256 chunks of 8 each; chunk c < 256 is K, c >= 256 is V^T.
-  constexpr int kPer = 512 / kCoreThreads;
-  static_assert(kPer * kCoreThreads == 512, "K/V chunks must split evenly over the block");
-  bf16x8 rkv[G][kPer];
+  constexpr int kPer = G * 512 / kCoreThreads;
+  static_assert(kPer * kCoreThreads == G * 512, "K/V chunks must split evenly over the block");
+  bf16x8 rkv[kPer];
+  auto chunk_src = [&](int idx, int k0) -> const bf16* {
+    const int r = idx >> 9, c = idx & 511, u = c & 255;
+    return c < 256 ? kb[r] + (int64_t)(k0 + (u >> 2)) * kD + (u & 3) * 8
+                   : vb[r] + (int64_t)(u >> 3) * np + k0 + (u & 7) * 8;
+  };
+  auto chunk_dst = [&](int idx, int buf) -> bf16* {
+    const int r = idx >> 9, c = idx & 511, u = c & 255;
+    return c < 256 ? ks + (buf * G + r) * kKs + (u >> 2) * kKLd + (u & 3) * 8
+                   : vs + (buf * G + r) * kVs + (u >> 3) * kVLd + (u & 7) * 8;
+  };
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int c = 0; c < kPer; ++c) {
-        const int idx = t + kCoreThreads * c, u = idx & 255;
-        rkv[g][c] = idx < 256 ? *(const bf16x8*)(kb[g] + (int64_t)(k0 + (u >> 2)) * kD + (u & 3) * 8)
-                              : *(const bf16x8*)(vb[g] + (int64_t)(u >> 3) * np + k0 + (u & 7) * 8);
-      }
+    for (int c = 0; c < kPer; ++c) rkv[c] = *(const bf16x8*)chunk_src(t + kCoreThreads * c, k0);
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int c = 0; c < kPer; ++c) {
-        const int idx = t + kCoreThreads * c, u = idx & 255;
-        bf16* dst = idx < 256 ? ks + (buf * G + g) * kKs + (u >> 2) * kKLd + (u & 3) * 8
-                              : vs + (buf * G + g) * kVs + (u >> 3) * kVLd + (u & 7) * 8;
-        *(bf16x8*)dst = rkv[g][c];
-      }
+    for (int c = 0; c < kPer; ++c) *(bf16x8*)chunk_dst(t + kCoreThreads * c, buf) = rkv[c];
   };
   gload(0);
   sstore(0);
@@ -203,88 +230,95 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
   for (int k0 = 0; k0 < nk; k0 += kKT) {
     const int cur = (k0 / kKT) & 1;
     const bool more = k0 + kKT < nk;
-    // Triangle-bias C tiles for these 64 keys: lane = query, register r -> key drow(r).
-    f32x16 cb[2];
+    // Triangle-bias C tiles: tile j covers keys 16j..16j+15, register r -> key 16j + 4g + r.
+    f32x4 cb[4];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        f32x4 v = load4(tbrow + k0 + 32 * sub + 4 * hf + 8 * gq);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) cb[sub][4 * gq + e] = v[e];
-      }
+    for (int j = 0; j < 4; ++j) cb[j] = load4(tbrow + k0 + 16 * j);
     if (more) gload(k0 + kKT);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const bf16* kt = ks + (cur * G + g) * kKs;
-      f32x16 s[2];
+    for (int r = 0; r < G; ++r) {
+      const bf16* kt = ks + (cur * G + r) * kKs;
+      f32x4 s[4];
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        f32x16 c = cb[sub];
-        if (MASKED) {
-#pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            f32x4 v = *(const f32x4*)(mbr[g] + k0 + 32 * sub + 4 * hf + 8 * gq);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) c[4 * gq + e] += v[e];
-          }
-        }
-        const bf16* ksub = kt + 32 * sub * kKLd;
-        s[sub] = mfma32(frag(ksub, kKLd, 0, 1), qf[g][1], mfma32(frag(ksub, kKLd, 0, 0), qf[g][0], c));
+      for (int j = 0; j < 4; ++j) {
+        f32x4 c = cb[j];
+        if (MASKED) c = c + *(const f32x4*)(mbr[r] + k0 + 16 * j);
+        s[j] = mfma16(*(const bf16x8*)(kt + (16 * j + lq) * kKLd + 8 * g), qf[r], c);
+        if (!MASKED) s[j] = mfma16(e0, qm[r], s[j]);  // s - m
       }
-      float mt = s[0][0];
+      // This lane's max over its 16 keys; the max over all keys of a query
+      // (4 lanes) is only needed when some lane crosses the lazy threshold.
+      float mt = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[0][r]);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[1][r]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-      if (__any(mt > m[g] + kLazy)) {  // wave-uniform; rare after the first tiles
-        const float mn = fmaxf(m[g], mt);
-        const float alpha = __builtin_amdgcn_exp2f(m[g] - mn);
-        m[g] = mn;
-        lsum[g] *= alpha;
-        o[g] = o[g] * alpha;
-      }
-      const bf16* vt = vs + (cur * G + g) * kVs;
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          bf16x8 pf;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            float p = __builtin_amdgcn_exp2f(s[sub][8 * st + e] - m[g]);
-            lsum[g] += p;
-            pf[e] = (bf16)p;
-          }
-          // V^T fragment with the key order of P's D-layout registers.
-          const bf16* vr = vt + (l & 31) * kVLd + 32 * sub + 16 * st + 4 * hf;
-          bf16x4 v0 = *(const bf16x4*)vr, v1 = *(const bf16x4*)(vr + 8);
-          bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-          o[g] = mfma32(vf, pf, o[g]);
+      for (int j = 1; j < 4; ++j) mt = fmaxf(mt, fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
+      auto query_max = [](float v) {
+        v = fmaxf(v, __shfl_xor(v, 16, kWave));
+        return fmaxf(v, __shfl_xor(v, 32, kWave));
+      };
+      if (MASKED) {
+        if (__any(mt > m[r] + kLazy)) {  // wave-uniform; rare after the first stages
+          const float mn = fmaxf(m[r], query_max(mt));
+          const float alpha = __builtin_amdgcn_exp2f(m[r] - mn);
+          m[r] = mn;
+          o[r][0] = o[r][0] * alpha;
+          o[r][1] = o[r][1] * alpha;
+          ls[r] = ls[r] * alpha;
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] = s[j] - m[r];
+      } else if (k0 == 0 || __any(mt > kLazy)) {
+        mt = query_max(mt);
+        // first stage: start from the tile max; later: raise the offset by the excess
+        const float mn = (float)(bf16)(k0 == 0 ? mt : m[r] + fmaxf(mt, 0.f));
+        const float delta = m[r] - mn;
+        if (k0 != 0) {
+          const float alpha = __builtin_amdgcn_exp2f(delta);
+          o[r][0] = o[r][0] * alpha;
+          o[r][1] = o[r][1] * alpha;
+          ls[r] = ls[r] * alpha;
+        }
+        m[r] = mn;
+        if (g == 0) qm[r][0] = (bf16)(-mn);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] = s[j] + delta;
+      }
+      const bf16* vt = vs + (cur * G + r) * kVs;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        // P^T operand for keys 32st..32st+31: element e <-> key 32st + 16(e/4) + 4g + e%4
+        bf16x8 pf;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pf[e] = (bf16)__builtin_amdgcn_exp2f(s[2 * st][e]);
+          pf[4 + e] = (bf16)__builtin_amdgcn_exp2f(s[2 * st + 1][e]);
+        }
+        ls[r] = mfma16(ones, pf, ls[r]);
+#pragma unroll
+        for (int mt2 = 0; mt2 < 2; ++mt2) {
+          // V^T rows d = 16 mt2 + l%16 hold the same key order (stored permuted)
+          const bf16x8 vf = *(const bf16x8*)(vt + (16 * mt2 + lq) * kVLd + 32 * st + 8 * g);
+          o[r][mt2] = mfma16(vf, pf, o[r][mt2]);
+        }
+      }
     }
     if (more) sstore(cur ^ 1);
     __syncthreads();
   }
+  const int q = q0 + lq;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float ls = lsum[g] + __shfl_xor(lsum[g], 32, kWave);
-    const int q = q0 + (l & 31);
-    if (i0 + g < n && q < n) {
-      const float inv = 1.f / ls;
-      bf16* dst = L.o + ((int64_t)(i0 + g) * n + q) * kC + h * kD + 4 * hf;
+  for (int r = 0; r < G; ++r) {
+    if (i0 + r < n && q < n) {
+      const float inv = __builtin_amdgcn_rcpf(ls[r][0]);
+      bf16* dst = L.o + ((int64_t)(i0 + r) * n + q) * kC + h * kD + 4 * g;
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        bf16x4 pk = {(bf16)(o[g][4 * gq] * inv), (bf16)(o[g][4 * gq + 1] * inv), (bf16)(o[g][4 * gq + 2] * inv),
-                     (bf16)(o[g][4 * gq + 3] * inv)};
-        *(bf16x4*)(dst + 8 * gq) = pk;
+      for (int mt2 = 0; mt2 < 2; ++mt2) {
+        const bf16x4 pk = {(bf16)(o[r][mt2][0] * inv), (bf16)(o[r][mt2][1] * inv), (bf16)(o[r][mt2][2] * inv),
+                           (bf16)(o[r][mt2][3] * inv)};
+        *(bf16x4*)(dst + 16 * mt2) = pk;
       }
     }
   }
 }
-
-__host__ __device__ inline int core_row_groups(int n) { return (n + kRows - 1) / kRows; }
 
 __global__ __launch_bounds__(kCoreThreads) void triattn_core_kernel(Layout L) {
   __shared__ __attribute__((aligned(16))) bf16 ks_lds[2 * kRows * kKT * kKLd];
@@ -299,11 +333,11 @@ __global__ __launch_bounds__(kCoreThreads) void triattn_core_kernel(Layout L) {
   const int h = col / qtiles, qt = col % qtiles;
   const int t = threadIdx.x, w = t >> 6;
   const int i0 = ig * kRows;
-  const int q0 = qt * kCoreQ + 32 * w;  // this wave's 32 queries (< np: np is a multiple of kCoreQ)
+  const int q0 = qt * kCoreQ + 16 * w;  // this wave's 16 queries (< np: np is a multiple of kCoreQ)
 
   bool masked = false;
-  for (int g = 0; g < kRows && i0 + g < n; ++g) {
-    const float* mbrow = L.mb + (int64_t)(i0 + g) * np;
+  for (int r = 0; r < kRows && i0 + r < n; ++r) {
+    const float* mbrow = L.mb + (int64_t)(i0 + r) * np;
     for (int k = t; k < n; k += kCoreThreads) masked |= mbrow[k] != 0.f;
   }
   masked = __syncthreads_or(masked);
