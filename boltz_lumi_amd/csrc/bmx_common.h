@@ -53,6 +53,14 @@ __device__ __forceinline__ void store_f(T* p, float v) {
   *p = (T)v;
 }
 
+// 16-byte load through a global (addrspace 1) pointer.  When a source pointer
+// is picked at run time the compiler can lose its address space and emit a
+// flat load, which also counts against lgkmcnt: every later LDS wait then
+// waits for the global load as well, serialising a prefetch with compute.
+__device__ __forceinline__ bf16x8 gload8(const bf16* p) {
+  return *(const __attribute__((address_space(1))) bf16x8*)p;
+}
+
 // 4 consecutive values as fp32.
 __device__ __forceinline__ f32x4 load4(const float* p) { return *(const f32x4*)p; }
 __device__ __forceinline__ f32x4 load4(const bf16* p) {

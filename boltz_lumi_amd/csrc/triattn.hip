@@ -12,17 +12,17 @@
 //  K1 triattn_proj   LN(x') -> q (pre-scaled by log2(e)/sqrt(d)), k, v^T and the
 //                    triangle bias tb[h][q][k] = log2(e) * linear(x')[q,k,h] on
 //                    MFMA; mask bias mb[i][k] = log2(e) * inf * (mask'[i][k] - 1).
-//  K2 triattn_core   one block per (row i, head h, 128 queries); per 32-key
-//                    tile S^T = K Q^T + (tb + mb)^T with the bias as the MFMA C
-//                    operand, online softmax in base 2 (fp32), O^T += V^T P^T
-//                    with P kept in registers (bf16).
+//  K2 triattn_core   one block per (2 rows i, head h, 128 queries); per 64-key
+//                    stage S^T = K Q^T + tb^T (+ mb for masked rows) with the
+//                    bias as the MFMA C operand, online softmax in base 2
+//                    (fp32), O^T += V^T P^T with P kept in registers (bf16).
 //  K3 triattn_out    o * sigmoid(linear_g(LN(x')) + b_g) -> linear_o + b_o, then
 //                    write or add into the fp32 residual in place.
 //
 // Workspace (np = round_up(n, 128)):
 //   q[i][h][j][d], k[i][h][j][d], vt[i][h][d][j']  bf16, i < np, j < np, where
 //     j' = (j & ~31) + vperm(j & 31) permutes keys inside each 32-key block
-//   tb[h][q][k] bf16 (k >= n is -inf), mb[i][k] fp32, o[i][j][h*32+d] bf16 (n x n)
+//   tb[h][q][k] fp32 (k >= n is -inf), mb[i][k] fp32, o[i][j][h*32+d] bf16 (n x n)
 #include "bmx_common.h"
 
 using namespace bmx;
@@ -32,9 +32,10 @@ namespace {
 constexpr int kH = 4, kD = 32, kTP = 128, kPad = 256;  // row padding: a multiple of both kTP and the attention query tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kProjRows = 3 * kC + 32;  // q, k, v, then H triangle-bias rows (+ zero rows)
-// Triangle-bias storage type.  bf16 halves the bias traffic of the attention
-// core; upstream's bf16 path rounds the bias to bf16 as well.
-using tb_t = bf16;
+// Triangle-bias storage type.  fp32 feeds the QK^T MFMA's C operand with no
+// conversion; the bias rows a block re-reads stay in its XCD's L2 (2 MB of
+// bias per XCD at N = 1024), so the extra bytes cost L2 bandwidth only.
+using tb_t = float;
 
 struct Layout {
   int n, np;
@@ -218,7 +219,7 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
   };
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int c = 0; c < kPer; ++c) rkv[c] = *(const bf16x8*)chunk_src(t + kCoreThreads * c, k0);
+    for (int c = 0; c < kPer; ++c) rkv[c] = gload8(chunk_src(t + kCoreThreads * c, k0));
   };
   auto sstore = [&](int buf) {
 #pragma unroll
@@ -235,52 +236,63 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
 #pragma unroll
     for (int j = 0; j < 4; ++j) cb[j] = load4(tbrow + k0 + 16 * j);
     if (more) gload(k0 + kKT);
+    // S^T for all rows first, so the scheduler can overlap one row's MFMAs
+    // with another row's max / exp work inside one basic block.
+    f32x4 s[G][4];
+    float mt[G];
 #pragma unroll
     for (int r = 0; r < G; ++r) {
       const bf16* kt = ks + (cur * G + r) * kKs;
-      f32x4 s[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         f32x4 c = cb[j];
         if (MASKED) c = c + *(const f32x4*)(mbr[r] + k0 + 16 * j);
-        s[j] = mfma16(*(const bf16x8*)(kt + (16 * j + lq) * kKLd + 8 * g), qf[r], c);
-        if (!MASKED) s[j] = mfma16(e0, qm[r], s[j]);  // s - m
+        s[r][j] = mfma16(*(const bf16x8*)(kt + (16 * j + lq) * kKLd + 8 * g), qf[r], c);
+        if (!MASKED) s[r][j] = mfma16(e0, qm[r], s[r][j]);  // s - m
       }
       // This lane's max over its 16 keys; the max over all keys of a query
       // (4 lanes) is only needed when some lane crosses the lazy threshold.
-      float mt = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+      mt[r] = fmaxf(fmaxf(s[r][0][0], s[r][0][1]), fmaxf(s[r][0][2], s[r][0][3]));
 #pragma unroll
-      for (int j = 1; j < 4; ++j) mt = fmaxf(mt, fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
-      auto query_max = [](float v) {
-        v = fmaxf(v, __shfl_xor(v, 16, kWave));
-        return fmaxf(v, __shfl_xor(v, 32, kWave));
-      };
-      if (MASKED) {
-        if (__any(mt > m[r] + kLazy)) {  // wave-uniform; rare after the first stages
-          const float mn = fmaxf(m[r], query_max(mt));
-          const float alpha = __builtin_amdgcn_exp2f(m[r] - mn);
-          m[r] = mn;
-          o[r][0] = o[r][0] * alpha;
-          o[r][1] = o[r][1] * alpha;
-          ls[r] = ls[r] * alpha;
-        }
+      for (int j = 1; j < 4; ++j)
+        mt[r] = fmaxf(mt[r], fmaxf(fmaxf(s[r][j][0], s[r][j][1]), fmaxf(s[r][j][2], s[r][j][3])));
+    }
+    bool grow = false;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s[j] = s[j] - m[r];
-      } else if (k0 == 0 || __any(mt > kLazy)) {
-        mt = query_max(mt);
-        // first stage: start from the tile max; later: raise the offset by the excess
-        const float mn = (float)(bf16)(k0 == 0 ? mt : m[r] + fmaxf(mt, 0.f));
+    for (int r = 0; r < G; ++r) grow |= MASKED ? mt[r] > m[r] + kLazy : mt[r] > kLazy;
+    auto query_max = [](float v) {
+      v = fmaxf(v, __shfl_xor(v, 16, kWave));
+      return fmaxf(v, __shfl_xor(v, 32, kWave));
+    };
+    if ((!MASKED && k0 == 0) || __any(grow)) {  // wave-uniform; rare after the first stages
+#pragma unroll
+      for (int r = 0; r < G; ++r) {
+        const float qmax = query_max(mt[r]);
+        float mn;
+        if (MASKED)
+          mn = fmaxf(m[r], qmax);
+        else  // first stage: start from the tile max; later: raise the offset by the excess
+          mn = (float)(bf16)(k0 == 0 ? qmax : m[r] + fmaxf(qmax, 0.f));
         const float delta = m[r] - mn;
-        if (k0 != 0) {
+        if (MASKED || k0 != 0) {
           const float alpha = __builtin_amdgcn_exp2f(delta);
           o[r][0] = o[r][0] * alpha;
           o[r][1] = o[r][1] * alpha;
           ls[r] = ls[r] * alpha;
         }
         m[r] = mn;
-        if (g == 0) qm[r][0] = (bf16)(-mn);
+        if (!MASKED) {
+          if (g == 0) qm[r][0] = (bf16)(-mn);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s[j] = s[j] + delta;
+          for (int j = 0; j < 4; ++j) s[r][j] = s[r][j] + delta;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      if (MASKED) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[r][j] = s[r][j] - m[r];
       }
       const bf16* vt = vs + (cur * G + r) * kVs;
 #pragma unroll
@@ -289,8 +301,8 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
         bf16x8 pf;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pf[e] = (bf16)__builtin_amdgcn_exp2f(s[2 * st][e]);
-          pf[4 + e] = (bf16)__builtin_amdgcn_exp2f(s[2 * st + 1][e]);
+          pf[e] = (bf16)__builtin_amdgcn_exp2f(s[r][2 * st][e]);
+          pf[4 + e] = (bf16)__builtin_amdgcn_exp2f(s[r][2 * st + 1][e]);
         }
         ls[r] = mfma16(ones, pf, ls[r]);
 #pragma unroll
