@@ -101,27 +101,42 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Per-lane LayerNorm affine for channels 4*hl .. 4*hl+3; a null weight or
+// bias acts as 1 or 0.  Load it once, outside any row loop: a conditional load
+// inside an unrolled row loop gets its own basic block and a vmcnt(0) wait,
+// which also waits for every prefetch in flight.
+struct LnAffine {
+  f32x4 w, b;
+};
+__device__ __forceinline__ LnAffine ln_affine(const float* w, const float* b, int hl) {
+  LnAffine a;
+  a.w = w ? load4(w + 4 * hl) : f32x4{1.f, 1.f, 1.f, 1.f};
+  a.b = b ? load4(b + 4 * hl) : f32x4{0.f, 0.f, 0.f, 0.f};
+  return a;
+}
+
 // LayerNorm over 128 channels of one row held by a half-wave: 4 values per
 // lane (channels 4*hl .. 4*hl+3).  Two-pass mean/variance in fp32.
-__device__ __forceinline__ f32x4 ln128_half(f32x4 v, const float* w, const float* b, int hl, float eps) {
+__device__ __forceinline__ f32x4 ln128_half(f32x4 v, const LnAffine& a, float eps) {
   float s = v[0] + v[1] + v[2] + v[3];
   float mean = half_sum(s) * (1.f / kC);
   f32x4 d = v - mean;
   float q = d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + d[3] * d[3];
   float inv = rsqrtf(half_sum(q) * (1.f / kC) + eps);
-  f32x4 y = d * inv;
-  if (w) y = y * load4(w + 4 * hl);
-  if (b) y = y + load4(b + 4 * hl);
-  return y;
+  return d * inv * a.w + a.b;
 }
 
 // Normalise TP rows of 128 channels into an LDS tile lds[TP][kLdsRow] (bf16).
 // row_ptr(p) returns the row's base pointer or nullptr for padding rows,
-// which are written as zeros.  256 threads: each half-wave takes TP/8 rows.
+// which are written as zeros.  Padding rows read the valid row `safe`
+// instead, so every load is unconditional: a load under a branch gets its own
+// basic block and a full vmcnt wait, serialising the tile's HBM reads.
+// 256 threads: each half-wave takes TP/8 rows.
 template <int TP, typename TIn, typename RowPtr>
-__device__ __forceinline__ void ln_rows_to_lds(RowPtr row_ptr, const float* w, const float* b, float eps,
-                                               bf16* lds) {
+__device__ __forceinline__ void ln_rows_to_lds(RowPtr row_ptr, const TIn* safe, const float* w, const float* b,
+                                               float eps, bf16* lds) {
   const int hw = threadIdx.x >> 5, hl = threadIdx.x & 31;
+  const LnAffine aff = ln_affine(w, b, hl);
   constexpr int kPer = TP / 8;
   f32x4 v[kPer];
   bool ok[kPer];
@@ -129,11 +144,11 @@ __device__ __forceinline__ void ln_rows_to_lds(RowPtr row_ptr, const float* w, c
   for (int u = 0; u < kPer; ++u) {
     const TIn* src = row_ptr(hw + 8 * u);
     ok[u] = src != nullptr;
-    v[u] = ok[u] ? load4(src + 4 * hl) : f32x4{0.f, 0.f, 0.f, 0.f};
+    v[u] = load4((ok[u] ? src : safe) + 4 * hl);
   }
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
-    f32x4 y = ln128_half(v[u], w, b, hl, eps);
+    f32x4 y = ln128_half(v[u], aff, eps);
     if (!ok[u]) y = f32x4{0.f, 0.f, 0.f, 0.f};
     bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
     *(bf16x4*)(lds + (hw + 8 * u) * kLdsRow + 4 * hl) = o;

@@ -21,10 +21,11 @@ __global__ __launch_bounds__(256) void ln128_rows_kernel(const TIn* __restrict__
                                                          const float* __restrict__ b, TOut* __restrict__ out,
                                                          int64_t rows, float eps) {
   const int hl = threadIdx.x & 31;
+  const LnAffine aff = ln_affine(w, b, hl);
   const int64_t stride = (int64_t)gridDim.x * (blockDim.x >> 5);
   for (int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5); row < rows; row += stride) {
     f32x4 v = load4(x + row * kC + 4 * hl);
-    f32x4 y = ln128_half(v, w, b, hl, eps);
+    f32x4 y = ln128_half(v, aff, eps);
     TOut* o = out + row * kC + 4 * hl;
 #pragma unroll
     for (int u = 0; u < 4; ++u) o[u] = (TOut)y[u];
@@ -46,10 +47,11 @@ __global__ __launch_bounds__(256) void ln128_cf_kernel(const TIn* __restrict__ x
   }
   __syncthreads();
   const int hw = t >> 5, hl = t & 31;
+  const LnAffine aff = ln_affine(w, b, hl);
   for (int r = hw; r < 64; r += 8) {
     if (r0 + r >= rows) break;
     f32x4 v = {tile[r][4 * hl], tile[r][4 * hl + 1], tile[r][4 * hl + 2], tile[r][4 * hl + 3]};
-    f32x4 y = ln128_half(v, w, b, hl, eps);
+    f32x4 y = ln128_half(v, aff, eps);
     TOut* o = out + (r0 + r) * kC + 4 * hl;
 #pragma unroll
     for (int u = 0; u < 4; ++u) o[u] = (TOut)y[u];

@@ -33,6 +33,7 @@ __global__ __launch_bounds__(256) void pair_bias_kernel(const TIn* __restrict__ 
   __shared__ __attribute__((aligned(16))) float xs[kTile * kXRow];
   const int t = threadIdx.x, l = lane_id(), wv = t >> 6, g = l >> 4;
   const int hw = t >> 5, hl = t & 31;
+  const LnAffine aff = ln_affine(ln_w, ln_b, hl);
   const int64_t r0 = (int64_t)blockIdx.x * kTile;
 
   // Weight fragments: head l%16, k = 4*s + g for the 32 k-steps.
@@ -43,12 +44,13 @@ __global__ __launch_bounds__(256) void pair_bias_kernel(const TIn* __restrict__ 
   f32x4 v[kTile / 8];
 #pragma unroll
   for (int u = 0; u < kTile / 8; ++u) {
-    const int64_t row = r0 + hw + 8 * u;
-    v[u] = row < rows ? load4(z + row * kC + 4 * hl) : f32x4{0.f, 0.f, 0.f, 0.f};
+    // rows past the end re-read the last row (unconditional loads) and are not stored
+    const int64_t row = min(r0 + hw + 8 * u, rows - 1);
+    v[u] = load4(z + row * kC + 4 * hl);
   }
 #pragma unroll
   for (int u = 0; u < kTile / 8; ++u)
-    *(f32x4*)(xs + (hw + 8 * u) * kXRow + 4 * hl) = ln128_half(v[u], ln_w, ln_b, hl, eps);
+    *(f32x4*)(xs + (hw + 8 * u) * kXRow + 4 * hl) = ln128_half(v[u], aff, eps);
   __syncthreads();
 
   // D[head][pair] = W[head][k] * X^T[k][pair]; wave wv owns pairs 16*wv .. +15.

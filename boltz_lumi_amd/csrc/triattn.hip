@@ -74,7 +74,7 @@ __global__ __launch_bounds__(256) void triattn_proj_kernel(const TIn* __restrict
     int j = j0 + p;
     return (i < n && j < n) ? xrow(x, n, starting, i, j) : nullptr;
   };
-  ln_rows_to_lds<kTP, TIn>(row_ptr, ln_w, ln_b, eps, xt);
+  ln_rows_to_lds<kTP, TIn>(row_ptr, x, ln_w, ln_b, eps, xt);
   if (t < kTP) {
     int j = j0 + t;
     float mb = 0.f;
@@ -381,6 +381,7 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
   const int n = L.n;
   const int t = threadIdx.x, l = lane_id(), w = t >> 6, c0 = 32 * w, ch = c0 + (l & 31);
   const int hw = t >> 5, hl = t & 31;
+  const LnAffine aff = ln_affine(ln_w, ln_b, hl);
   const int tiles_x = (n + kP3 - 1) / kP3, total = n * tiles_x;
   const bool x_in_regs = out_mode == kOutResidual || (const void*)x == out;
 
@@ -418,7 +419,7 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
 #pragma unroll
     for (int u = 0; u < kRowsPer; ++u) {
       xc[u] = px[u];
-      f32x4 y = ln128_half(px[u], ln_w, ln_b, hl, eps);
+      f32x4 y = ln128_half(px[u], aff, eps);
       bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
       *(bf16x4*)(xg + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
       *(bf16x4*)(xo + (hw + 8 * u) * kLdsRow + 4 * hl) = po[u];

@@ -46,6 +46,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
   __shared__ __attribute__((aligned(16))) bf16 stage[2 * kC * kStage1];
   const int l = lane_id(), w = threadIdx.x >> 6, c0 = 32 * w;
   const int hw = threadIdx.x >> 5, hl = threadIdx.x & 31;
+  const LnAffine aff = ln_affine(ln_w, ln_b, hl);
   const int tiles_x = np / kP1, total = np * tiles_x;
   const int64_t plane = (int64_t)np * np;
 
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
 #pragma unroll
     for (int u = 0; u < kP1 / 8; ++u) {
       const int tt = t0 + hw + 8 * u;
-      f32x4 y = ln128_half(pre[u], ln_w, ln_b, hl, eps);
+      f32x4 y = ln128_half(pre[u], aff, eps);
       if (rp >= n || tt >= n) y = f32x4{0.f, 0.f, 0.f, 0.f};
       bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
       *(bf16x4*)(xt + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
@@ -247,6 +248,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
   static_assert(kP3 * kYRow * 4 <= 2 * kP3 * kLdsRow * 2, "ybuf must fit in the tile buffers");
   const int t = threadIdx.x, l = lane_id(), w = t >> 6, c0 = 32 * w;
   const int hw = t >> 5, hl = t & 31;
+  const LnAffine aff_in = ln_affine(in_w, in_b, hl), aff_out = ln_affine(out_w, out_b, hl);
   const int tiles_x = (n + kP3 - 1) / kP3, total = n * tiles_x;
   const int64_t plane = (int64_t)np * np;
   const bool x_in_regs = out_mode == kOutResidual || (const void*)x == out;
@@ -284,7 +286,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
 #pragma unroll
     for (int u = 0; u < kRowsPer; ++u) {
       xc[u] = px[u];
-      f32x4 y = ln128_half(px[u], in_w, in_b, hl, eps_in);
+      f32x4 y = ln128_half(px[u], aff_in, eps_in);
       bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
       *(bf16x4*)(xg + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
     }
@@ -300,7 +302,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
     for (int u = 0; u < kRowsPer; ++u) {
       bf16* row = xo + (hw + 8 * u) * kLdsRow + 4 * hl;
       f32x4 v = {(float)row[0], (float)row[1], (float)row[2], (float)row[3]};
-      f32x4 y = ln128_half(v, out_w, out_b, hl, eps_out);
+      f32x4 y = ln128_half(v, aff_out, eps_out);
       bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
       *(bf16x4*)row = o;
     }
