@@ -84,10 +84,24 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 // D-fragment row of register r for this lane (see header comment).
 __device__ __forceinline__ int drow(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
-// Sum / max across the 32 lanes of a half-wave.
+// v from the lane selected by a DPP control word (full row / bank masks).
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+// Sum across the 32 lanes of a half-wave; every lane gets the same bits.
+// Lanes within 16 exchange through DPP (VALU, no LDS round trip): quad_perm
+// xor 1, quad_perm xor 2, row_half_mirror (i <-> 7-i in 8), row_mirror
+// (i <-> 15-i in 16).  The last step crosses the two 16-lane rows with
+// ds_swizzle in bitmask mode (xor 16).  A __shfl_xor butterfly costs one
+// ds_bpermute and a full LDS wait per step.
 __device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  v += dpp<0x140>(v);  // row_mirror
+  v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // xor 16
   return v;
 }
 __device__ __forceinline__ float wave_sum(float v) {
