@@ -29,7 +29,7 @@ using namespace bmx;
 
 namespace {
 
-constexpr int kH = 4, kD = 32, kTP = 128, kPad = 256;  // row padding: a multiple of both kTP and the attention query tile
+constexpr int kH = 4, kD = 32, kPad = 256;  // row padding: a multiple of the projection and attention tiles
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kProjRows = 3 * kC + 32;  // q, k, v, then H triangle-bias rows (+ zero rows)
 // Triangle-bias storage type.  fp32 feeds the QK^T MFMA's C operand with no
@@ -59,70 +59,119 @@ __device__ __forceinline__ const TIn* xrow(const TIn* x, int n, int starting, in
   return x + pair * kC;
 }
 
-// ------------------------------------------------------------------ K1
-template <typename TIn>
-__global__ __launch_bounds__(256) void triattn_proj_kernel(const TIn* __restrict__ x, const float* __restrict__ mask,
-                                                           const float* __restrict__ ln_w,
-                                                           const float* __restrict__ ln_b, float eps,
-                                                           const bf16* __restrict__ w_proj, float inf, int starting,
-                                                           Layout L) {
-  __shared__ __attribute__((aligned(16))) bf16 xt[kTP * kLdsRow];
-  const int i = blockIdx.y, j0 = blockIdx.x * kTP;
-  const int n = L.n, np = L.np;
-  const int t = threadIdx.x, l = lane_id(), w = t >> 6;
-  auto row_ptr = [&](int p) -> const TIn* {
-    int j = j0 + p;
-    return (i < n && j < n) ? xrow(x, n, starting, i, j) : nullptr;
-  };
-  ln_rows_to_lds<kTP, TIn>(row_ptr, x, ln_w, ln_b, eps, xt);
-  if (t < kTP) {
-    int j = j0 + t;
-    float mb = 0.f;
-    if (i < n && j < n && mask) {
-      float m = starting ? mask[(int64_t)i * n + j] : mask[(int64_t)j * n + i];
-      mb = inf * (m - 1.f) * kLog2e;
-    }
-    L.mb[(int64_t)i * np + j] = mb;
-  }
-  __syncthreads();
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
 
+// ------------------------------------------------------------------ K1
+// Persistent and weight-stationary.  Wave w keeps head w's q, k and v weight
+// rows (3 x 32 rows, 32x32x16 operands) and the 4 triangle-bias rows (16x16x32
+// A operands) in VGPRs for the block's lifetime.  A tile is 64 positions
+// (i, j0..j0+63) of the row frame over the padded np x np range, so padding
+// rows and keys get their zero / -inf values from the same code; the next
+// tile's input rows are prefetched into registers during the current tile's
+// MFMAs.
+constexpr int kP1 = 64;
+
+template <typename TIn>
+__global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restrict__ x, const float* __restrict__ mask,
+                                                              const float* __restrict__ ln_w,
+                                                              const float* __restrict__ ln_b, float eps,
+                                                              const bf16* __restrict__ w_proj, float inf, int starting,
+                                                              Layout L) {
+  __shared__ __attribute__((aligned(16))) bf16 xt[kP1 * kLdsRow];
+  const int n = L.n, np = L.np;
+  const int t = threadIdx.x, l = lane_id(), w = t >> 6, h = w, g = l >> 4, lq = l & 15;
+  const int hw = t >> 5, hl = t & 31;
+  const LnAffine aff = ln_affine(ln_w, ln_b, hl);
+  const int tiles_x = np / kP1, total = np * tiles_x;
   const float qscale = kLog2e / sqrtf((float)kD);
-  // 13 weight tiles of 32 rows: 0-3 q heads, 4-7 k heads, 8-11 v heads, 12 tri-bias.
-  for (int tile = w; tile < 13; tile += 4) {
-    bf16x8 wf[8];
+
+  // Weight rows: q, k, v of head h are rows 32h, 128 + 32h, 256 + 32h; the
+  // triangle-bias rows 384..387 (then zero rows) as A[l%16][32 ks + 8g ..].
+  bf16x8 wq[8], wk[8], wv[8], wb[4];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) wf[ks] = frag(w_proj, kC, tile * 32, ks);
-    const int kind = tile >> 2, h = tile & 3;
+  for (int ks = 0; ks < 8; ++ks) {
+    wq[ks] = frag(w_proj, kC, 32 * h, ks);
+    wk[ks] = frag(w_proj, kC, kC + 32 * h, ks);
+    wv[ks] = frag(w_proj, kC, 2 * kC + 32 * h, ks);
+  }
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      f32x16 acc = zero16();
-      if (kind < 2) {
-        // D[pair][d]: lane = d, register = pair.
+  for (int ks = 0; ks < 4; ++ks) wb[ks] = *(const bf16x8*)(w_proj + (3 * kC + lq) * kC + 32 * ks + 8 * g);
+
+  // Input rows (clamped into range: every load is unconditional, padding rows
+  // are zeroed after the LayerNorm).
+  constexpr int kRowsPer = kP1 / 8;
+  f32x4 px[kRowsPer];
+  auto fetch = [&](int tile) {
+    const int i = min(tile / tiles_x, n - 1), j0 = (tile % tiles_x) * kP1;
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) acc = mfma32(frag(xt, kLdsRow, nt * 32, ks), wf[ks], acc);
-        bf16* dst = (kind == 0 ? L.q : L.k) + (((int64_t)i * kH + h) * np + j0) * kD + (l & 31);
+    for (int u = 0; u < kRowsPer; ++u) px[u] = load4(xrow(x, n, starting, i, min(j0 + hw + 8 * u, n - 1)) + 4 * hl);
+  };
+
+  int tile = blockIdx.x;
+  if (tile < total) fetch(tile);
+  for (; tile < total; tile += gridDim.x) {
+    const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP1;
+#pragma unroll
+    for (int u = 0; u < kRowsPer; ++u) {
+      f32x4 y = ln128_half(px[u], aff, eps);
+      if (i >= n || j0 + hw + 8 * u >= n) y = f32x4{0.f, 0.f, 0.f, 0.f};
+      const bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+      *(bf16x4*)(xt + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
+    }
+    if (t < kP1) {
+      // mask bias mb[i][j] = log2(e) * inf * (mask'[i][j] - 1); 0 outside n x n
+      const int j = j0 + t;
+      const bool in = i < n && j < n;
+      const int ic = min(i, n - 1), jc = min(j, n - 1);
+      const float mv = mask ? (starting ? mask[(int64_t)ic * n + jc] : mask[(int64_t)jc * n + ic]) : 1.f;
+      L.mb[(int64_t)i * np + j] = in ? inf * (mv - 1.f) * kLog2e : 0.f;
+    }
+    __syncthreads();
+    if (tile + (int)gridDim.x < total) fetch(tile + gridDim.x);
+
+#pragma unroll
+    for (int nt = 0; nt < kP1 / 32; ++nt) {
+      bf16x8 xf[8];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) xf[ks] = frag(xt, kLdsRow, nt * 32, ks);
+      // q, k: D[pair][d], lane -> d, register r -> pair 8(r/4) + 4(l/32) + r%4;
+      // each store writes 2 contiguous 64-byte rows.
+      const int64_t qk_off = (((int64_t)i * kH + h) * np + j0 + nt * 32 + 4 * (l >> 5)) * kD + (l & 31);
+#pragma unroll
+      for (int kind = 0; kind < 2; ++kind) {
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) acc = mfma32(xf[ks], kind == 0 ? wq[ks] : wk[ks], acc);
+        bf16* dst = (kind == 0 ? L.q : L.k) + qk_off;
         const float sc = kind == 0 ? qscale : 1.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dst[(nt * 32 + drow(r, l)) * kD] = (bf16)(acc[r] * sc);
-      } else {
-        // D[channel][pair]: lane = pair, register = channel.
+        for (int r = 0; r < 16; ++r) dst[(8 * (r >> 2) + (r & 3)) * kD] = (bf16)(acc[r] * sc);
+      }
+      // v^T: D[d][pair], lane -> pair, register -> d; keys are stored permuted
+      // inside each 32-key block (see vperm), still 64 contiguous bytes per row.
+      f32x16 av = zero16();
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) acc = mfma32(wf[ks], frag(xt, kLdsRow, nt * 32, ks), acc);
-        const int j = j0 + nt * 32 + (l & 31);
-        if (kind == 2) {
-          // keys are stored permuted inside each 32-key block (see vperm)
-          bf16* dst = L.vt + ((int64_t)i * kH + h) * kD * np + (j & ~31) + vperm(j & 31);
+      for (int ks = 0; ks < 8; ++ks) av = mfma32(wv[ks], xf[ks], av);
+      bf16* vdst = L.vt + ((int64_t)i * kH + h) * kD * np + (int64_t)(4 * (l >> 5)) * np + j0 + nt * 32 + vperm(l & 31);
 #pragma unroll
-          for (int r = 0; r < 16; ++r) dst[(int64_t)drow(r, l) * np] = (bf16)acc[r];
-        } else if (l < 32) {
+      for (int r = 0; r < 16; ++r) vdst[(int64_t)(8 * (r >> 2) + (r & 3)) * np] = (bf16)av[r];
+    }
+    {
+      // Triangle bias for pairs j0 + 16w .. +15: D[head][pair] on 16x16x32,
+      // lanes of group 0 hold heads 0..3 in registers 0..3.
+      f32x4 ab = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int r = 0; r < kH; ++r) {
-            float v = j < n ? acc[r] * kLog2e : -INFINITY;
-            L.tb[((int64_t)r * np + i) * np + j] = (tb_t)v;
-          }
-        }
+      for (int ks = 0; ks < 4; ++ks)
+        ab = mfma16(wb[ks], *(const bf16x8*)(xt + (16 * w + lq) * kLdsRow + 32 * ks + 8 * g), ab);
+      const int j = j0 + 16 * w + lq;
+      if (g == 0) {
+#pragma unroll
+        for (int r = 0; r < kH; ++r) L.tb[((int64_t)r * np + i) * np + j] = (tb_t)(j < n ? ab[r] * kLog2e : -INFINITY);
       }
     }
+    __syncthreads();
   }
 }
 
@@ -148,10 +197,6 @@ constexpr int kCoreThreads = 64 * kCoreWaves;
 // into registers serves all of them, which divides the bias traffic
 // (N x the [H, N, N] bias per direction) by kRows.
 constexpr int kRows = 2;
-
-__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
 
 // Blocks are dispatched round-robin over the 8 XCDs.  A "column" is one
 // (head, query tile); every XCD owns a contiguous run of columns, so the
@@ -497,8 +542,9 @@ int run(const TIn* x, const float* mask, int n, int starting, float inf, const f
         void* out, int out_mode, void* ws, int stages, hipStream_t st) {
   Layout L = make_layout(ws, n);
   if (stages & 1) {
-    triattn_proj_kernel<TIn><<<dim3(L.np / kTP, L.np), 256, 0, st>>>(x, mask, ln_w, ln_b, eps, w_proj, inf,
-                                                                      starting, L);
+    const int total = L.np * (L.np / kP1);
+    const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
+    triattn_proj_kernel<TIn><<<dim3(grid), 256, 0, st>>>(x, mask, ln_w, ln_b, eps, w_proj, inf, starting, L);
     if (int rc = check_launch("triattn_proj")) return rc;
   }
   if (stages & 2) {
