@@ -22,7 +22,8 @@
 // Workspace (np = round_up(n, 128)):
 //   q[i][h][j][d], k[i][h][j][d], vt[i][h][d][j']  bf16, i < np, j < np, where
 //     j' = (j & ~31) + vperm(j & 31) permutes keys inside each 32-key block
-//   tb[h][q][k] fp32 (k >= n is -inf), mb[i][k] fp32, o[i][j][h*32+d] bf16 (n x n)
+//   tb: H x np x np fp32 in C-operand order (tb_offset; k >= n is -inf), mb[i][k] fp32,
+//   o[i][j][h*32+d] bf16 (n x n)
 #include "bmx_common.h"
 
 using namespace bmx;
@@ -51,6 +52,16 @@ __host__ __device__ inline int64_t qkv_elems(int np) { return (int64_t)np * kH *
 // 8 keys of lane group g are one contiguous 16-byte read.
 __host__ __device__ inline int vperm(int key_in_block) {
   return ((key_in_block >> 2) & 3) * 8 + ((key_in_block >> 4) & 1) * 4 + (key_in_block & 3);
+}
+
+// The triangle bias is stored in the attention core's C-operand order: for
+// head h, query block qb (16 queries) and key block kb (16 keys), one 1 KB
+// run holds lane l's 4 keys 16 kb + 4 (l / 16) + 0..3 of query 16 qb + l % 16,
+// so every bias load of the core reads 64 lanes x 16 contiguous bytes.
+// (32-bit: H * np * np < 2^31 for n <= 8192.)
+__host__ __device__ inline int tb_offset(int np, int h, int q, int k) {
+  const int nb = np / 16;
+  return ((h * nb + q / 16) * nb + k / 16) * 256 + (((k & 15) >> 2) * 16 + (q & 15)) * 4 + (k & 3);
 }
 
 template <typename TIn>
@@ -167,8 +178,10 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
         ab = mfma16(wb[ks], *(const bf16x8*)(xt + (16 * w + lq) * kLdsRow + 32 * ks + 8 * g), ab);
       const int j = j0 + 16 * w + lq;
       if (g == 0) {
+        tb_t* dst = L.tb + tb_offset(np, 0, i, j);
+        const int head_stride = np * np;  // tb_offset(np, h + 1, ..) - tb_offset(np, h, ..)
 #pragma unroll
-        for (int r = 0; r < kH; ++r) L.tb[((int64_t)r * np + i) * np + j] = (tb_t)(j < n ? ab[r] * kLog2e : -INFINITY);
+        for (int r = 0; r < kH; ++r) dst[r * head_stride] = (tb_t)(j < n ? ab[r] * kLog2e : -INFINITY);
       }
     }
     __syncthreads();
@@ -213,7 +226,7 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
   const int n = L.n, np = L.np;
   const int t = threadIdx.x, l = lane_id(), g = l >> 4, lq = l & 15;
   const int nk = (n + kKT - 1) / kKT * kKT;
-  const tb_t* tbrow = L.tb + ((int64_t)h * np + q0 + lq) * np + 4 * g;
+  const tb_t* tbrow = L.tb + tb_offset(np, h, q0, 0) + 4 * l;  // + 256 per 16-key block
   const bf16* kb[G];
   const bf16* vb[G];
   const float* mbr[G];
@@ -279,7 +292,7 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
     // Triangle-bias C tiles: tile j covers keys 16j..16j+15, register r -> key 16j + 4g + r.
     f32x4 cb[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) cb[j] = load4(tbrow + k0 + 16 * j);
+    for (int j = 0; j < 4; ++j) cb[j] = load4(tbrow + 16 * (k0 + 16 * j));
     if (more) gload(k0 + kKT);
     // S^T for all rows first, so the scheduler can overlap one row's MFMAs
     // with another row's max / exp work inside one basic block.
@@ -377,7 +390,9 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
   }
 }
 
-__global__ __launch_bounds__(kCoreThreads) void triattn_core_kernel(Layout L) {
+// Two 8-wave blocks per CU need <= 128 VGPRs; one register more would leave a
+// single block per CU, which measured 1.5-2.3x slower, so the budget is pinned.
+__global__ __launch_bounds__(kCoreThreads) __attribute__((amdgpu_waves_per_eu(4))) void triattn_core_kernel(Layout L) {
   __shared__ __attribute__((aligned(16))) bf16 ks_lds[2 * kRows * kKT * kKLd];
   __shared__ __attribute__((aligned(16))) bf16 vs_lds[2 * kRows * kD * kVLd];
   const int n = L.n, np = L.np;
