@@ -42,6 +42,7 @@ SIGNATURES = {
     "bmx_triattn_proj_rows": (c_int, []),
     "bmx_triattn_fwd": (c_int, [_P, c_int, _P, c_int64, c_int, c_float, _P, _P, c_float, _P, _P, _P, _P, _P, _P, c_int,
                                 _P, c_size_t, c_int, _P]),
+    "bmx_pack_mfma_weights": (c_int, [_P, c_int64, c_int64, _P, _P]),
     "bmx_pair_transition_fwd": (c_int, [_P, c_int, c_int64, _P, _P, c_float, _P, _P, _P, c_int, _P]),
     "bmx_pair_bias_fwd": (c_int, [_P, c_int, c_int64, _P, _P, c_float, _P, c_int, _P, _P]),
 }

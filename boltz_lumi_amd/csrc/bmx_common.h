@@ -197,6 +197,12 @@ __device__ __forceinline__ bf16x8 frag(const bf16* base, int ld, int row0, int k
   return *(const bf16x8*)(base + (row0 + (l & 31)) * ld + 16 * ks + 8 * (l >> 5));
 }
 
+// The same fragment from a matrix packed by bmx_pack_mfma_weights (cols
+// columns, row0 a multiple of 32): one contiguous 1 KB run per fragment.
+__device__ __forceinline__ bf16x8 pfrag(const bf16* packed, int cols, int row0, int ks) {
+  return *(const bf16x8*)(packed + (((int64_t)(row0 >> 5) * (cols >> 4) + ks) * 64 + lane_id()) * 8);
+}
+
 }  // namespace bmx
 
 // ---------------------------------------------------------------------------

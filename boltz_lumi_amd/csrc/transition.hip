@@ -1,5 +1,8 @@
 // Fused pair transition for gfx950: LN -> fc1 | fc2 (128 -> 512 each) ->
-// bf16(bf16(silu(fc1)) * fc2) -> fc3 (512 -> 128), one kernel per 128 pairs.
+// bf16(silu(fc1) * fc2) -> fc3 (512 -> 128), one block per 128 pairs.  The
+// weights arrive packed in MFMA A-operand order (bmx_pack_mfma_weights):
+// every tile streams all 384 KB of them, and packed operands are contiguous
+// 1 KB loads.
 //
 // Replaces the reference's transition_forward (pair_transition.py:8-28:
 // module.norm, fc1, fc2, the HIP silu_mul of kernels/pair_hip.cu:42-64, fc3).
@@ -71,8 +74,8 @@ __global__ __launch_bounds__(256) void pair_transition_kernel(const TIn* x, cons
   auto load_w12 = [&](int hc) {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      f1[ks] = frag(w12, kC, hc * kC + c0, ks);
-      f2[ks] = frag(w12, kC, kHidden + hc * kC + c0, ks);
+      f1[ks] = pfrag(w12, kC, hc * kC + c0, ks);
+      f2[ks] = pfrag(w12, kC, kHidden + hc * kC + c0, ks);
     }
   };
   load_w12(0);
@@ -84,7 +87,7 @@ __global__ __launch_bounds__(256) void pair_transition_kernel(const TIn* x, cons
   for (int hc = 0; hc < kHidden / kC; ++hc) {
     bf16x8 f3[8];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) f3[ks] = frag(w3 + hc * kC, kHidden, c0, ks);
+    for (int ks = 0; ks < 8; ++ks) f3[ks] = pfrag(w3, kHidden, c0, 8 * hc + ks);
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       f32x16 a1 = zero16(), a2 = zero16();

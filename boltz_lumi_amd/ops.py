@@ -79,6 +79,22 @@ def _f32(t):
     return t.detach().to(torch.float32).contiguous()
 
 
+def pack_mfma_weights(w):
+    """bf16 copy of the row-major matrix ``w`` in MFMA A-operand order
+    (``bmx_pack_mfma_weights``): each 32-row x 16-column operand tile becomes
+    one contiguous 1 KB run."""
+    _cuda(w)
+    w = w.detach().to(torch.bfloat16).contiguous()
+    rows, cols = w.shape
+    out = torch.empty_like(w)
+    N.call("bmx_pack_mfma_weights", w.data_ptr(), rows, cols, out.data_ptr(), _stream(w))
+    return out
+
+
+def _bf16_packed(*ws):
+    return pack_mfma_weights(_bf16(*ws))
+
+
 def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
@@ -338,8 +354,8 @@ def pair_transition(module, x, out_mode=OUT_BF16, out=None):
            "expected contiguous fp32/bf16 x with 128 channels")
     _check(module.fc1.weight.shape == (4 * C, C) and module.fc3.weight.shape == (C, 4 * C),
            "expected a 128 -> 512 -> 128 transition")
-    w12 = cached_weight(module, "w12", (module.fc1.weight, module.fc2.weight), _bf16)
-    w3 = cached_weight(module, "w3", (module.fc3.weight,), _bf16)
+    w12 = cached_weight(module, "w12p", (module.fc1.weight, module.fc2.weight), _bf16_packed)
+    w3 = cached_weight(module, "w3p", (module.fc3.weight,), _bf16_packed)
     lnw = cached_weight(module, "ln_w", (module.norm.weight,), _f32)
     lnb = cached_weight(module, "ln_b", (module.norm.bias,), _f32)
     out = _out_tensor(x, out, out_mode)

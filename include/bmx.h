@@ -122,8 +122,17 @@ int bmx_triattn_fwd(const void* x, int x_dtype, const float* mask, int64_t n, in
                     const float* b_g, const void* w_o, const float* b_o, void* out, int out_mode, void* workspace,
                     size_t workspace_bytes, int stages, bmx_stream_t stream);
 
+/* Pack a row-major bf16 matrix W[rows][cols] (rows % 32 == 0, cols % 16 == 0) into MFMA
+ * A-operand order: element (r, c) goes to ((r/32 * cols/16 + c/16) * 64 + lane) * 8 + c%8
+ * with lane = 32 * ((c%16)/8) + r%32, so each 32x16 operand tile is one contiguous 1 KB run.
+ * dst holds rows * cols bf16 and must not overlap src.  Weight preparation for the
+ * kernels that stream weights per tile (bmx_pair_transition_fwd); it replaces the reference's
+ * cached bf16 weight concatenation (src/boltz_lumi/multiplication.py:29-45) for those. */
+int bmx_pack_mfma_weights(const void* src, int64_t rows, int64_t cols, void* dst, bmx_stream_t stream);
+
 /* Transition(128, 512).forward on `rows` rows of 128 channels.
- * w12: bf16 [1024][128] = [fc1.weight; fc2.weight]; w3: bf16 [128][512] = fc3.weight.
+ * w12: [fc1.weight; fc2.weight] (bf16 [1024][128]) and w3: fc3.weight (bf16 [128][512]),
+ * each packed by bmx_pack_mfma_weights.
  * Replaces transition_forward (src/boltz_lumi/pair_transition.py:8-28). */
 int bmx_pair_transition_fwd(const void* x, int x_dtype, int64_t rows, const float* ln_w, const float* ln_b, float eps,
                             const void* w12, const void* w3, void* out, int out_mode, bmx_stream_t stream);

@@ -64,6 +64,11 @@ def test_argument_validation_needs_no_gpu(lib):
     assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
     rc = lib.bmx_pair_transition_fwd(None, 1, 8, None, None, 1e-5, None, None, None, 2, None)
     assert rc == N.BMX_EINVAL and b"residual" in lib.bmx_last_error()
+    rc = lib.bmx_pack_mfma_weights(None, 48, 128, None, None)
+    assert rc == N.BMX_EINVAL and b"multiple of 32" in lib.bmx_last_error()
+    rc = lib.bmx_pack_mfma_weights(None, 32, 128, None, None)
+    assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
+    assert lib.bmx_pack_mfma_weights(None, 0, 128, None, None) == N.BMX_OK
 
 
 def test_call_raises_with_message(lib):

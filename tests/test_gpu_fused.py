@@ -116,6 +116,21 @@ def test_pair_transition_matches_oracle(gpu, rows, dtype):
     assert want.abs().max() > 0 and e["max_rel"] < TOL, e
 
 
+@pytest.mark.parametrize("rows,cols", [(32, 16), (1024, 128), (128, 512)])
+def test_pack_mfma_weights_layout(gpu, rows, cols):
+    """Element (r, c) of the packed copy sits at ((r/32 * cols/16 + c/16) * 64
+    + 32 * ((c%16)/8) + r%32) * 8 + c%8: checked by placing every element by
+    that formula on the CPU."""
+    w = torch.arange(rows * cols, dtype=torch.float32).reshape(rows, cols) % 251
+    want = torch.empty(rows * cols)
+    r = torch.arange(rows)[:, None].expand(rows, cols)
+    c = torch.arange(cols)[None, :].expand(rows, cols)
+    lane = 32 * ((c % 16) // 8) + r % 32
+    want[(((r // 32) * (cols // 16) + c // 16) * 64 + lane) * 8 + c % 8] = w
+    got = ops.pack_mfma_weights(w.to(gpu)).float().cpu().flatten()
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_adaln_modulate_matches_oracle(gpu, dtype):
     g = torch.Generator().manual_seed(3)
