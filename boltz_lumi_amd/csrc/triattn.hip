@@ -22,7 +22,7 @@
 // Workspace (np = round_up(n, 128)):
 //   q[i][h][j][d], k[i][h][j][d], vt[i][h][d][j']  bf16, i < np, j < np, where
 //     j' = (j & ~31) + vperm(j & 31) permutes keys inside each 32-key block
-//   tb: H x np x np fp32 in C-operand order (tb_offset; k >= n is -inf), mb[i][k] fp32,
+//   tb: H x np x np bf16 in B-operand order (tb_offset; k >= n is kPadBias), mb[i][k] fp32,
 //   o[i][j][h*32+d] bf16 (n x n)
 #include "bmx_common.h"
 
@@ -33,10 +33,14 @@ namespace {
 constexpr int kH = 4, kD = 32, kPad = 256;  // row padding: a multiple of the projection and attention tiles
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kProjRows = 3 * kC + 32;  // q, k, v, then H triangle-bias rows (+ zero rows)
-// Triangle-bias storage type.  fp32 feeds the QK^T MFMA's C operand with no
-// conversion; the bias rows a block re-reads stay in its XCD's L2 (2 MB of
-// bias per XCD at N = 1024), so the extra bytes cost L2 bandwidth only.
-using tb_t = float;
+// Triangle-bias storage type: bf16, as upstream's bf16 path rounds the bias.
+// The attention core adds it with an MFMA (identity A operand, bias as the B
+// operand), so it needs no conversion to fp32.
+using tb_t = bf16;
+// Bias of padding keys (k >= n).  Finite, because the identity MFMA multiplies
+// every bias entry by 0 for the other 15 keys of its tile (0 * -inf = NaN);
+// exp2 of it is still exactly 0.
+constexpr float kPadBias = -1e30f;
 
 struct Layout {
   int n, np;
@@ -54,14 +58,15 @@ __host__ __device__ inline int vperm(int key_in_block) {
   return ((key_in_block >> 2) & 3) * 8 + ((key_in_block >> 4) & 1) * 4 + (key_in_block & 3);
 }
 
-// The triangle bias is stored in the attention core's C-operand order: for
-// head h, query block qb (16 queries) and key block kb (16 keys), one 1 KB
-// run holds lane l's 4 keys 16 kb + 4 (l / 16) + 0..3 of query 16 qb + l % 16,
-// so every bias load of the core reads 64 lanes x 16 contiguous bytes.
+// The triangle bias is stored in the attention core's B-operand order: for
+// head h, query block qb (16 queries) and key block kb (16 keys), one 512-byte
+// run holds, for lane L = 16 (k % 16 / 8) + q % 16 (L < 32), the 8 keys
+// 16 kb + 8 (L / 16) + 0..7 of query 16 qb + L % 16, so a bias load of the
+// core reads 32 lanes x 16 contiguous bytes.
 // (32-bit: H * np * np < 2^31 for n <= 8192.)
 __host__ __device__ inline int tb_offset(int np, int h, int q, int k) {
   const int nb = np / 16;
-  return ((h * nb + q / 16) * nb + k / 16) * 256 + (((k & 15) >> 2) * 16 + (q & 15)) * 4 + (k & 3);
+  return ((h * nb + q / 16) * nb + k / 16) * 256 + (((k & 15) >> 3) * 16 + (q & 15)) * 8 + (k & 7);
 }
 
 template <typename TIn>
@@ -181,7 +186,7 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
         tb_t* dst = L.tb + tb_offset(np, 0, i, j);
         const int head_stride = np * np;  // tb_offset(np, h + 1, ..) - tb_offset(np, h, ..)
 #pragma unroll
-        for (int r = 0; r < kH; ++r) dst[r * head_stride] = (tb_t)(j < n ? ab[r] * kLog2e : -INFINITY);
+        for (int r = 0; r < kH; ++r) dst[r * head_stride] = (tb_t)(j < n ? ab[r] * kLog2e : kPadBias);
       }
     }
     __syncthreads();
@@ -226,7 +231,7 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
   const int n = L.n, np = L.np;
   const int t = threadIdx.x, l = lane_id(), g = l >> 4, lq = l & 15;
   const int nk = (n + kKT - 1) / kKT * kKT;
-  const tb_t* tbrow = L.tb + tb_offset(np, h, q0, 0) + 4 * l;  // + 256 per 16-key block
+  const tb_t* tbrow = L.tb + tb_offset(np, h, q0, 0) + 8 * (l & 31);  // + 256 per 16-key block
   const bf16* kb[G];
   const bf16* vb[G];
   const float* mbr[G];
@@ -244,21 +249,21 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
   // all-ones A operand accumulates from the same bf16 P that multiplies V.
   f32x4 o[G][2], ls[G];
   // m: the max offset subtracted from this lane's scores.  Unmasked rows
-  // subtract it inside the QK^T MFMA chain (an extra K step with A = e0 and
-  // B = -m in bf16), so m is kept exactly bf16-representable; the offset
-  // cancels in o / l, so rounding it only has to keep p <= 2^(kLazy + 1).
+  // start the QK^T MFMA from C = -m (mneg), so the subtraction is free.
   float m[G];
-  bf16x8 qm[G];
+  f32x4 mneg[G];
 #pragma unroll
   for (int r = 0; r < G; ++r) {
     o[r][0] = o[r][1] = ls[r] = f32x4{0.f, 0.f, 0.f, 0.f};
     m[r] = MASKED ? -INFINITY : 0.f;
-    qm[r] = bf16x8{};
+    mneg[r] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  bf16x8 ones, e0 = {};
+  // ident: A operand with A[key][kk] = (kk == key) for kk < 16, so that one
+  // MFMA with the bias tile as B adds bias^T to S^T.
+  bf16x8 ones, ident = {};
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones[e] = (bf16)1.f;
-  if (g == 0) e0[0] = (bf16)1.f;
+  if (g == (lq >> 3)) ident[lq & 7] = (bf16)1.f;
 
   // Per row and stage: K tile 64 keys x 32 d and V^T tile 32 d x 64 keys,
   // 256 chunks of 8 each; chunk c < 256 is K, c >= 256 is V^T.
@@ -289,10 +294,12 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
   for (int k0 = 0; k0 < nk; k0 += kKT) {
     const int cur = (k0 / kKT) & 1;
     const bool more = k0 + kKT < nk;
-    // Triangle-bias C tiles: tile j covers keys 16j..16j+15, register r -> key 16j + 4g + r.
-    f32x4 cb[4];
+    // Triangle-bias B tiles: tile j covers keys 16j..16j+15; lanes of groups
+    // 0 and 1 hold keys 16j + 8g .. +7 of their query.  Groups 2 and 3 load
+    // the same bytes, which ident multiplies by zero (the bias is finite).
+    bf16x8 cb[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) cb[j] = load4(tbrow + 16 * (k0 + 16 * j));
+    for (int j = 0; j < 4; ++j) cb[j] = *(const bf16x8*)(tbrow + 16 * (k0 + 16 * j));
     if (more) gload(k0 + kKT);
     // S^T for all rows first, so the scheduler can overlap one row's MFMAs
     // with another row's max / exp work inside one basic block.
@@ -303,10 +310,9 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
       const bf16* kt = ks + (cur * G + r) * kKs;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        f32x4 c = cb[j];
-        if (MASKED) c = c + *(const f32x4*)(mbr[r] + k0 + 16 * j);
+        const f32x4 c = MASKED ? *(const f32x4*)(mbr[r] + k0 + 16 * j) : mneg[r];
         s[r][j] = mfma16(*(const bf16x8*)(kt + (16 * j + lq) * kKLd + 8 * g), qf[r], c);
-        if (!MASKED) s[r][j] = mfma16(e0, qm[r], s[r][j]);  // s - m
+        s[r][j] = mfma16(ident, cb[j], s[r][j]);  // + bias
       }
       // This lane's max over its 16 keys; the max over all keys of a query
       // (4 lanes) is only needed when some lane crosses the lazy threshold.
@@ -330,7 +336,7 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
         if (MASKED)
           mn = fmaxf(m[r], qmax);
         else  // first stage: start from the tile max; later: raise the offset by the excess
-          mn = (float)(bf16)(k0 == 0 ? qmax : m[r] + fmaxf(qmax, 0.f));
+          mn = k0 == 0 ? qmax : m[r] + fmaxf(qmax, 0.f);
         const float delta = m[r] - mn;
         if (MASKED || k0 != 0) {
           const float alpha = __builtin_amdgcn_exp2f(delta);
@@ -340,7 +346,7 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
         }
         m[r] = mn;
         if (!MASKED) {
-          if (g == 0) qm[r][0] = (bf16)(-mn);
+          mneg[r] = f32x4{-mn, -mn, -mn, -mn};
 #pragma unroll
           for (int j = 0; j < 4; ++j) s[r][j] = s[r][j] + delta;
         }
