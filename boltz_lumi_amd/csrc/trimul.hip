@@ -63,15 +63,12 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
   f32x4 pre[kP1 / 8];
   auto fetch = [&](int tile) {
     const int rp = tile / tiles_x, t0 = (tile % tiles_x) * kP1;
+    const int rc = min(rp, n - 1);  // padding rows / columns re-read row n-1 and are zeroed after the LN
 #pragma unroll
     for (int u = 0; u < kP1 / 8; ++u) {
-      const int tt = t0 + hw + 8 * u;
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (rp < n && tt < n) {
-        const int64_t pair = outgoing ? (int64_t)rp * n + tt : (int64_t)tt * n + rp;
-        v = load4(x + pair * kC + 4 * hl);
-      }
-      pre[u] = v;
+      const int tc = min(t0 + hw + 8 * u, n - 1);
+      const int64_t pair = outgoing ? (int64_t)rc * n + tc : (int64_t)tc * n + rc;
+      pre[u] = load4(x + pair * kC + 4 * hl);
     }
   };
 
@@ -94,8 +91,10 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
 #pragma unroll
     for (int nt = 0; nt < kP1 / 32; ++nt) {
       const int tt = t0 + nt * 32 + (l & 31);
-      float m = 0.f;
-      if (rp < n && tt < n) m = mask[outgoing ? (int64_t)rp * n + tt : (int64_t)tt * n + rp];
+      // rows / columns past n (plane padding) are written as zeros
+      const int rc = min(rp, n - 1), tc = min(tt, n - 1);
+      const float mv = mask[outgoing ? (int64_t)rc * n + tc : (int64_t)tc * n + rc];
+      const float m = (rp < n && tt < n) ? mv : 0.f;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         f32x16 ap = zero16(), ag = zero16();
@@ -262,6 +261,15 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
 
   constexpr int kRowsPer = kP3 / 8;                  // rows per half-wave
   constexpr int kOChunks = kC * (kP3 / 8) / 256;     // 16-byte product chunks per thread
+  static_assert(kOChunks == 2 * (kP3 / 32), "one chunk per (pair block, k step)");
+  // ident[ks]: B operand I[k][n] = (16 ks + k == n) for the transposing MFMA;
+  // lane (half h, column n) holds k = 8h .. 8h+7.
+  bf16x8 ident[2] = {};
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int e = (l & 31) - 16 * ks - 8 * (l >> 5);
+    if (e >= 0 && e < 8) ident[ks][e] = (bf16)1.f;
+  }
   f32x4 px[kRowsPer];
   bf16x8 po[kOChunks];
   auto fetch = [&](int tile) {
@@ -271,10 +279,13 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
       const int j = j0 + hw + 8 * u;
       px[u] = j < n ? load4(x + ((int64_t)i * n + j) * kC + 4 * hl) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // A operands of the transposing MFMA: pair block pb (32 pairs), k step ks
+    // (16 pairs): channel c0 + l%32, pairs 32 pb + 16 ks + 8 (l/32) .. +7.
 #pragma unroll
     for (int u = 0; u < kOChunks; ++u) {
-      const int idx = t + 256 * u, c = idx / (kP3 / 8), chunk = idx % (kP3 / 8);
-      po[u] = *(const bf16x8*)(o_pl + c * plane + (int64_t)i * np + j0 + chunk * 8);
+      const int pb = u >> 1, ks = u & 1;
+      po[u] = *(const bf16x8*)(o_pl + (c0 + (l & 31)) * plane + (int64_t)i * np + j0 + 32 * pb + 16 * ks +
+                               8 * (l >> 5));
     }
   };
 
@@ -290,11 +301,19 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
       bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
       *(bf16x4*)(xg + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
     }
+    // Transpose O (channel-major planes) into xo[pair][channel] with an
+    // identity B operand: D[ch][pair] = O[ch][k] * I[k][pair] puts 4
+    // consecutive channels of one pair in each register group, written as
+    // one 8-byte LDS store (a 2-byte scatter here costs 4-8-way bank conflicts).
 #pragma unroll
-    for (int u = 0; u < kOChunks; ++u) {
-      const int idx = t + 256 * u, c = idx / (kP3 / 8), chunk = idx % (kP3 / 8);
+    for (int pb = 0; pb < kP3 / 32; ++pb) {
+      f32x16 d = mfma32(po[2 * pb], ident[0], zero16());
+      d = mfma32(po[2 * pb + 1], ident[1], d);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xo[(chunk * 8 + e) * kLdsRow + c] = po[u][e];
+      for (int q = 0; q < 4; ++q) {
+        const bf16x4 v = {(bf16)d[4 * q], (bf16)d[4 * q + 1], (bf16)d[4 * q + 2], (bf16)d[4 * q + 3]};
+        *(bf16x4*)(xo + (32 * pb + (l & 31)) * kLdsRow + c0 + 8 * q + 4 * (l >> 5)) = v;
+      }
     }
     __syncthreads();
     if (tile + (int)gridDim.x < total) fetch(tile + gridDim.x);
