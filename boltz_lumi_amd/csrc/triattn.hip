@@ -199,9 +199,15 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
 // register r holds D[4g + r][l%16].  With 16 queries per wave the head dim
 // (32) is one K step and a wave's per-row state is small, so 8 waves x 2 rows
 // fit at 4 waves per SIMD.
-constexpr int kKT = 64;             // keys per pipeline stage
-constexpr int kKLd = kD + 8;        // K tile row (bf16)
-constexpr int kVLd = kKT + 8;       // V^T tile row (bf16)
+constexpr int kKT = 64;  // keys per pipeline stage
+
+// Stage buffers are filled by LDS DMA (global_load_lds_dwordx4: one wave
+// instruction copies 1 KB, lane l to byte 16 l), so the K and V^T tiles are
+// dense and XOR-swizzled in 16-byte chunks instead of padded; the MFMA operand
+// reads of 16 consecutive lanes then hit 16 distinct 4-bank groups:
+//   K tile   (64 keys x 32 d)  key k, d chunk c (8 dims)  -> chunk 4k + (c ^ ((k >> 2) & 3))
+//   V^T tile (32 d x 64 keys)  dim d, key chunk c (8 keys) -> chunk 8d + (c ^ ((d >> 1) & 7))
+constexpr int kTileBytes = kKT * kD * 2;  // one K or V^T tile of one row
 
 // Rescale the running output only when a query's max grows by more than
 // 2^kLazy: until then p = exp2(s - m) stays <= 2^kLazy, exact in fp32/bf16.
@@ -224,27 +230,79 @@ __host__ __device__ inline int core_qtiles(int n) { return (n + kCoreQ - 1) / kC
 __host__ __device__ inline int core_cols_per_xcd(int n) { return (kH * core_qtiles(n) + 7) / 8; }
 __host__ __device__ inline int core_row_groups(int n) { return (n + kRows - 1) / kRows; }
 
+// LDS stage buffer, per block: K and V^T tiles of the kRows rows, every wave's
+// triangle-bias B tiles for the stage (4 tiles x 512 B), and the rows' mask
+// bias (masked blocks only).
+constexpr int kBiasWaveBytes = 4 * 512;
+constexpr int kOffK = 0, kOffV = kRows * kTileBytes, kOffBias = 2 * kRows * kTileBytes;
+constexpr int kOffMb = kOffBias + kCoreWaves * kBiasWaveBytes;
+constexpr int kStageBytes = kOffMb + kRows * kKT * 4;
+
+// One LDS DMA: 64 lanes x 16 bytes from per-lane global addresses to
+// lds_addr + 16 * lane.  Issued as inline asm so that the compiler does not
+// wait for it before unrelated LDS reads: the kernel waits for its DMAs
+// explicitly (s_waitcnt vmcnt) before the barrier that publishes them.
+__device__ __forceinline__ void lds_dma16(const void* src, unsigned lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
+}
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
 template <bool MASKED>
-__device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0, bf16* ks, bf16* vs) {
+__device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0, char* lds) {
   constexpr int G = kRows;
-  constexpr int kKs = kKT * kKLd, kVs = kD * kVLd;  // per-row LDS tile sizes
   const int n = L.n, np = L.np;
-  const int t = threadIdx.x, l = lane_id(), g = l >> 4, lq = l & 15;
+  const int t = threadIdx.x, l = lane_id(), g = l >> 4, lq = l & 15, w = t >> 6;
   const int nk = (n + kKT - 1) / kKT * kKT;
-  const tb_t* tbrow = L.tb + tb_offset(np, h, q0, 0) + 8 * (l & 31);  // + 256 per 16-key block
+  const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
   const bf16* kb[G];
   const bf16* vb[G];
-  const float* mbr[G];
   bf16x8 qf[G];
 #pragma unroll
   for (int r = 0; r < G; ++r) {
     const int i = min(i0 + r, n - 1);  // rows past n repeat row n-1 and are not stored
     kb[r] = L.k + ((int64_t)i * kH + h) * np * kD;
     vb[r] = L.vt + ((int64_t)i * kH + h) * kD * np;
-    mbr[r] = L.mb + (int64_t)i * np + 4 * g;
     // Q^T (B operand): query q0 + l%16, head dims 8g .. 8g+7
     qf[r] = *(const bf16x8*)(L.q + (((int64_t)i * kH + h) * np + q0 + lq) * kD + 8 * g);
   }
+
+  // DMA jobs of one stage.  K / V^T: 4 quarters per (row, kind), job
+  // 8 r + 4 kind + quarter, wave w takes jobs w and w + 8.  Bias: every wave
+  // copies its own 16 queries' 4 tiles (2 KB, contiguous in the bias layout).
+  // Mask bias: wave 0's first 32 lanes copy 64 keys of both rows.
+  static_assert(kCoreWaves == 8 && G == 2, "DMA job split assumes 8 waves and 2 rows");
+  int64_t kv_off[2];
+  unsigned kv_lds[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int job = w + 8 * u, r = job >> 3, kind = (job >> 2) & 1, quarter = job & 3;
+    if (kind == 0) {
+      const int key = 16 * quarter + (l >> 2), c = (l & 3) ^ ((key >> 2) & 3);
+      kv_off[u] = (kb[r] - L.k) + (int64_t)key * kD + 8 * c;
+    } else {
+      const int d = 8 * quarter + (l >> 3), c = (l & 7) ^ ((d >> 1) & 7);
+      kv_off[u] = (vb[r] - L.vt) + (int64_t)d * np + 8 * c;
+    }
+    kv_lds[u] = (kind == 0 ? kOffK : kOffV) + r * kTileBytes + 1024 * quarter;
+  }
+  const bf16* tb_src = L.tb + tb_offset(np, h, q0, 0) + 8 * l;  // + 256 per 16-key block
+  const int i_mb = min(i0 + (l >> 4), n - 1);
+  const float* mb_src = L.mb + (int64_t)i_mb * np + 4 * lq;
+  auto dma_stage = [&](int k0, int buf) {
+    const unsigned base = lds0 + buf * kStageBytes;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int job = w + 8 * u, kind = (job >> 2) & 1;
+      const bf16* src = kind == 0 ? L.k + kv_off[u] + (int64_t)k0 * kD : L.vt + kv_off[u] + k0;
+      lds_dma16(src, __builtin_amdgcn_readfirstlane(base + kv_lds[u]));
+    }
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb)
+      lds_dma16(tb_src + 16 * (k0 + 32 * hb),
+                __builtin_amdgcn_readfirstlane(base + kOffBias + w * kBiasWaveBytes + 1024 * hb));
+    if (MASKED && w == 0 && l < 32) lds_dma16(mb_src + k0, __builtin_amdgcn_readfirstlane(base + kOffMb));
+  };
+
   // O^T tiles (d 0..15, 16..31) and the row sum l, which an MFMA with an
   // all-ones A operand accumulates from the same bf16 P that multiplies V.
   f32x4 o[G][2], ls[G];
@@ -265,54 +323,32 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
   for (int e = 0; e < 8; ++e) ones[e] = (bf16)1.f;
   if (g == (lq >> 3)) ident[lq & 7] = (bf16)1.f;
 
-  // Per row and stage: K tile 64 keys x 32 d and V^T tile 32 d x 64 keys,
-  // 256 chunks of 8 each; chunk c < 256 is K, c >= 256 is V^T.
-  constexpr int kPer = G * 512 / kCoreThreads;
-  static_assert(kPer * kCoreThreads == G * 512, "K/V chunks must split evenly over the block");
-  bf16x8 rkv[kPer];
-  auto chunk_src = [&](int idx, int k0) -> const bf16* {
-    const int r = idx >> 9, c = idx & 511, u = c & 255;
-    return c < 256 ? kb[r] + (int64_t)(k0 + (u >> 2)) * kD + (u & 3) * 8
-                   : vb[r] + (int64_t)(u >> 3) * np + k0 + (u & 7) * 8;
-  };
-  auto chunk_dst = [&](int idx, int buf) -> bf16* {
-    const int r = idx >> 9, c = idx & 511, u = c & 255;
-    return c < 256 ? ks + (buf * G + r) * kKs + (u >> 2) * kKLd + (u & 3) * 8
-                   : vs + (buf * G + r) * kVs + (u >> 3) * kVLd + (u & 7) * 8;
-  };
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int c = 0; c < kPer; ++c) rkv[c] = gload8(chunk_src(t + kCoreThreads * c, k0));
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int c = 0; c < kPer; ++c) *(bf16x8*)chunk_dst(t + kCoreThreads * c, buf) = rkv[c];
-  };
-  gload(0);
-  sstore(0);
+  // Per-lane LDS read offsets (bytes) inside a stage buffer.
+  const int k_rd = kOffK + (4 * lq + (g ^ ((lq >> 2) & 3))) * 16;  // + 1024 j (16 keys) + r tile
+  const int b_rd = kOffBias + w * kBiasWaveBytes + 16 * (l & 31);   // + 512 j
+
+  dma_stage(0, 0);
+  wait_vm0();
   __syncthreads();
   for (int k0 = 0; k0 < nk; k0 += kKT) {
     const int cur = (k0 / kKT) & 1;
     const bool more = k0 + kKT < nk;
-    // Triangle-bias B tiles: tile j covers keys 16j..16j+15; lanes of groups
-    // 0 and 1 hold keys 16j + 8g .. +7 of their query.  Groups 2 and 3 load
-    // the same bytes, which ident multiplies by zero (the bias is finite).
-    bf16x8 cb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) cb[j] = *(const bf16x8*)(tbrow + 16 * (k0 + 16 * j));
-    if (more) gload(k0 + kKT);
+    if (more) dma_stage(k0 + kKT, cur ^ 1);
+    const char* sb = lds + cur * kStageBytes;
     // S^T for all rows first, so the scheduler can overlap one row's MFMAs
     // with another row's max / exp work inside one basic block.
     f32x4 s[G][4];
     float mt[G];
 #pragma unroll
     for (int r = 0; r < G; ++r) {
-      const bf16* kt = ks + (cur * G + r) * kKs;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f32x4 c = MASKED ? *(const f32x4*)(mbr[r] + k0 + 16 * j) : mneg[r];
-        s[r][j] = mfma16(*(const bf16x8*)(kt + (16 * j + lq) * kKLd + 8 * g), qf[r], c);
-        s[r][j] = mfma16(ident, cb[j], s[r][j]);  // + bias
+        const f32x4 c = MASKED ? *(const f32x4*)(sb + kOffMb + r * kKT * 4 + (16 * j + 4 * g) * 4) : mneg[r];
+        s[r][j] = mfma16(*(const bf16x8*)(sb + k_rd + r * kTileBytes + 1024 * j), qf[r], c);
+        // Triangle-bias B tile j: lanes of groups 0 and 1 hold keys 16j + 8g .. +7
+        // of their query; groups 2 and 3 read the same bytes, which ident
+        // multiplies by zero (the bias is finite).
+        s[r][j] = mfma16(ident, *(const bf16x8*)(sb + b_rd + 512 * j), s[r][j]);
       }
       // This lane's max over its 16 keys; the max over all keys of a query
       // (4 lanes) is only needed when some lane crosses the lazy threshold.
@@ -358,7 +394,6 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
 #pragma unroll
         for (int j = 0; j < 4; ++j) s[r][j] = s[r][j] - m[r];
       }
-      const bf16* vt = vs + (cur * G + r) * kVs;
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         // P^T operand for keys 32st..32st+31: element e <-> key 32st + 16(e/4) + 4g + e%4
@@ -372,12 +407,14 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
 #pragma unroll
         for (int mt2 = 0; mt2 < 2; ++mt2) {
           // V^T rows d = 16 mt2 + l%16 hold the same key order (stored permuted)
-          const bf16x8 vf = *(const bf16x8*)(vt + (16 * mt2 + lq) * kVLd + 32 * st + 8 * g);
+          const int d = 16 * mt2 + lq, c = 4 * st + g;
+          const bf16x8 vf =
+              *(const bf16x8*)(sb + kOffV + r * kTileBytes + (8 * d + (c ^ ((d >> 1) & 7))) * 16);
           o[r][mt2] = mfma16(vf, pf, o[r][mt2]);
         }
       }
     }
-    if (more) sstore(cur ^ 1);
+    wait_vm0();  // this wave's DMAs of the next stage
     __syncthreads();
   }
   const int q = q0 + lq;
@@ -399,8 +436,7 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
 // Two 8-wave blocks per CU need <= 128 VGPRs; one register more would leave a
 // single block per CU, which measured 1.5-2.3x slower, so the budget is pinned.
 __global__ __launch_bounds__(kCoreThreads) __attribute__((amdgpu_waves_per_eu(4))) void triattn_core_kernel(Layout L) {
-  __shared__ __attribute__((aligned(16))) bf16 ks_lds[2 * kRows * kKT * kKLd];
-  __shared__ __attribute__((aligned(16))) bf16 vs_lds[2 * kRows * kD * kVLd];
+  __shared__ __attribute__((aligned(16))) char stage_lds[2 * kStageBytes];
   const int n = L.n, np = L.np;
   const int qtiles = core_qtiles(n);
   const int cpx = core_cols_per_xcd(n);
@@ -420,9 +456,9 @@ __global__ __launch_bounds__(kCoreThreads) __attribute__((amdgpu_waves_per_eu(4)
   }
   masked = __syncthreads_or(masked);
   if (masked)
-    core_rows<true>(L, i0, h, q0, ks_lds, vs_lds);
+    core_rows<true>(L, i0, h, q0, stage_lds);
   else
-    core_rows<false>(L, i0, h, q0, ks_lds, vs_lds);
+    core_rows<false>(L, i0, h, q0, stage_lds);
 }
 
 // ------------------------------------------------------------------ K3
