@@ -26,7 +26,7 @@ using namespace bmx;
 
 namespace {
 
-constexpr int kPlaneTile = 128;        // plane padding granularity
+constexpr int kPlaneTile = 256;        // plane padding granularity (the contraction's 256 x 256 tiles)
 
 // ------------------------------------------------------------------ K1
 // Persistent and weight-stationary: each wave keeps its [p_in; g_in] rows for
@@ -128,19 +128,27 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
 
 // ------------------------------------------------------------------ K2
 // Batched NT GEMM over channels: O_c[m][n] = sum_k A_c[m][k] * B_c[n][k].
+// Operand tiles are copied global -> LDS by the DMA path (global_load_lds,
+// 1 KB per wave instruction, lane l to byte 16 l), so the LDS tiles are dense
+// rows of BK bf16 with 16-byte chunks XOR-swizzled by (row / 2) % 8: the
+// fragment reads of 16 consecutive rows hit 16 distinct 4-bank groups.  The
+// DMA of stage k+1 runs during stage k's MFMAs with no staging registers.
+__device__ __forceinline__ void lds_dma16(const void* src, unsigned lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
+}
+
 template <int BM, int BN, int BK, int WM, int WN>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_kernel(
     const bf16* __restrict__ A, const bf16* __restrict__ B, bf16* __restrict__ O, int np, int tiles_n,
     int tiles_per_ch) {
   constexpr int kWavesN = BN / WN;
-  constexpr int kThreads = (BM / WM) * kWavesN * 64;
-  constexpr int kLd = BK + 8;
+  constexpr int kWaves = (BM / WM) * kWavesN;
   constexpr int kMi = WM / 32, kNi = WN / 32;
-  constexpr int kChunksA = BM * BK / 8 / kThreads;
-  constexpr int kChunksB = BN * BK / 8 / kThreads;
-  static_assert(kChunksA * kThreads * 8 == BM * BK && kChunksB * kThreads * 8 == BN * BK, "tile/thread mismatch");
-  __shared__ __attribute__((aligned(16))) bf16 As[2][BM * kLd];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2][BN * kLd];
+  static_assert(BK == 64, "one LDS row is 8 chunks of 16 bytes");
+  constexpr int kTileA = BM * BK * 2, kTileB = BN * BK * 2, kStage = kTileA + kTileB;
+  constexpr int kDmaA = kTileA / 1024 / kWaves, kDmaB = kTileB / 1024 / kWaves;  // wave instructions per stage
+  static_assert(kDmaA * kWaves * 1024 == kTileA && kDmaB * kWaves * 1024 == kTileB, "tile/wave mismatch");
+  __shared__ __attribute__((aligned(16))) char smem[2 * kStage];
 
   // Blocks are dispatched round-robin over the 8 XCDs; give every XCD whole
   // channels so the channel's operand planes stay in that XCD's L2.
@@ -155,31 +163,26 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
 
   const int t = threadIdx.x, l = lane_id(), wv = t >> 6;
   const int wm0 = (wv / kWavesN) * WM, wn0 = (wv % kWavesN) * WN;
+  const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
 
-  bf16x8 ra[kChunksA], rb[kChunksB];
-  auto gload = [&](int k0) {
+  // DMA instruction u of this wave copies tile rows 8 q .. 8 q + 7 (q = wave
+  // + kWaves u): lane l -> row 8 q + l / 8, stored chunk l % 8 holding k-chunk
+  // (l % 8) ^ ((row / 2) % 8).
+  auto dma_stage = [&](int k0, int buf) {
+    const unsigned base = lds0 + buf * kStage;
 #pragma unroll
-    for (int u = 0; u < kChunksA; ++u) {
-      int i = t + kThreads * u, row = i / (BK / 8), col = (i % (BK / 8)) * 8;
-      ra[u] = *(const bf16x8*)(Ac + (int64_t)row * np + k0 + col);
-    }
-#pragma unroll
-    for (int u = 0; u < kChunksB; ++u) {
-      int i = t + kThreads * u, row = i / (BK / 8), col = (i % (BK / 8)) * 8;
-      rb[u] = *(const bf16x8*)(Bc + (int64_t)row * np + k0 + col);
+    for (int u = 0; u < kDmaA + kDmaB; ++u) {
+      const bool is_a = u < kDmaA;
+      const int q = wv + kWaves * (is_a ? u : u - kDmaA);
+      const int row = 8 * q + (l >> 3), chunk = (l & 7) ^ ((row >> 1) & 7);
+      const bf16* src = (is_a ? Ac : Bc) + (int64_t)row * np + k0 + 8 * chunk;
+      lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (is_a ? 0 : kTileA) + 1024 * q));
     }
   };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < kChunksA; ++u) {
-      int i = t + kThreads * u, row = i / (BK / 8), col = (i % (BK / 8)) * 8;
-      *(bf16x8*)(&As[buf][row * kLd + col]) = ra[u];
-    }
-#pragma unroll
-    for (int u = 0; u < kChunksB; ++u) {
-      int i = t + kThreads * u, row = i / (BK / 8), col = (i % (BK / 8)) * 8;
-      *(bf16x8*)(&Bs[buf][row * kLd + col]) = rb[u];
-    }
+  // Fragment (row0 + l % 32, k-step ks) of a tile at byte offset tile_off.
+  auto sfrag = [&](const char* sb, int tile_off, int row0, int ks) -> bf16x8 {
+    const int row = row0 + (l & 31), chunk = 2 * ks + (l >> 5);
+    return *(const bf16x8*)(sb + tile_off + row * (BK * 2) + ((chunk ^ ((row >> 1) & 7)) * 16));
   };
 
   f32x16 acc[kMi][kNi];
@@ -189,25 +192,26 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
     for (int j = 0; j < kNi; ++j) acc[i][j] = zero16();
 
   const int kt_count = np / BK;
-  gload(0);
-  sstore(0);
+  dma_stage(0, 0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's DMAs
   __syncthreads();
   for (int kt = 0; kt < kt_count; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < kt_count) gload((kt + 1) * BK);
+    if (kt + 1 < kt_count) dma_stage((kt + 1) * BK, cur ^ 1);
+    const char* sb = smem + cur * kStage;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8 af[kMi], bfr[kNi];
 #pragma unroll
-      for (int i = 0; i < kMi; ++i) af[i] = frag(As[cur], kLd, wm0 + 32 * i, ks);
+      for (int i = 0; i < kMi; ++i) af[i] = sfrag(sb, 0, wm0 + 32 * i, ks);
 #pragma unroll
-      for (int j = 0; j < kNi; ++j) bfr[j] = frag(Bs[cur], kLd, wn0 + 32 * j, ks);
+      for (int j = 0; j < kNi; ++j) bfr[j] = sfrag(sb, kTileA, wn0 + 32 * j, ks);
 #pragma unroll
       for (int i = 0; i < kMi; ++i)
 #pragma unroll
         for (int j = 0; j < kNi; ++j) acc[i][j] = mfma32(af[i], bfr[j], acc[i][j]);
     }
-    if (kt + 1 < kt_count) sstore(cur ^ 1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // the next stage's DMAs
     __syncthreads();
   }
 
@@ -403,9 +407,9 @@ int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, c
     if (int rc = check_launch("trimul_proj")) return rc;
   }
   if (stages & 2) {
-    constexpr int BM = 128, BN = 128, BK = 64;
+    constexpr int BM = 256, BN = 256, BK = 64, WM = 64, WN = 128;
     const int tiles_n = np / BN, tiles_per_ch = (np / BM) * tiles_n;
-    trimul_contract_kernel<BM, BN, BK, 64, 64><<<dim3(kC * tiles_per_ch), 256, 0, stream>>>(
+    trimul_contract_kernel<BM, BN, BK, WM, WN><<<dim3(kC * tiles_per_ch), (BM / WM) * (BN / WN) * 64, 0, stream>>>(
         a_pl, b_pl, o_pl, np, tiles_n, tiles_per_ch);
     if (int rc = check_launch("trimul_contract")) return rc;
   }

@@ -95,7 +95,7 @@ int bmx_bias_softmax(const void* scores, const void* bias, const float* mask, vo
  * 2 = contraction / attention core, 4 = output; 7 runs the whole module.  The
  * workspace carries the intermediates between separately launched stages. */
 
-/* Workspace needed by bmx_trimul_fwd (bytes; 3 * 128 * np^2 bf16, np = round_up(n,128)). */
+/* Workspace needed by bmx_trimul_fwd (bytes; 3 * 128 * np^2 bf16, np = round_up(n,256)). */
 size_t bmx_trimul_workspace_bytes(int64_t n);
 
 /* TriangleMultiplication{Outgoing,Incoming}.forward for one batch element.

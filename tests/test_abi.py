@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol(lib):
 def test_workspace_queries(lib):
     assert lib.bmx_trimul_workspace_bytes(0) == 0
     assert lib.bmx_trimul_workspace_bytes(1024) == 3 * 128 * 1024 * 1024 * 2
-    assert lib.bmx_trimul_workspace_bytes(100) == 3 * 128 * 128 * 128 * 2
+    assert lib.bmx_trimul_workspace_bytes(100) == 3 * 128 * 256 * 256 * 2  # planes padded to 256
     assert lib.bmx_triattn_workspace_bytes(1024) > 3 * 1024 * 1024 * 128 * 2
     assert lib.bmx_triattn_proj_rows() == 3 * 128 + 32
 
