@@ -62,7 +62,7 @@ def kernel_table(n: int):
         "triattn_proj": (2 * n2 * 128 * 388, n2 * (512 + 4 + 3 * 256 + 16), "hbm"),
         "triattn_core": (4 * 4 * 32 * n3, n2 * 4 * 3 * 64 + n2 * 256, "mfma"),
         "triattn_out": (2 * n2 * 128 * 256, n2 * (512 + 256 + 512), "hbm"),
-        "pair_transition": (2 * n2 * 128 * 1536, n2 * 1024, "hbm"),
+        "pair_transition": (2 * n2 * 128 * (1536 + 16), n2 * (1024 + 64), "hbm"),  # + the fused pair bias
     }
 
 
@@ -97,8 +97,12 @@ def per_kernel_times(layer, s, z, mask, pair_mask, z_out, ws, reps):
         for stage, name in ((1, "triattn_proj"), (2, "triattn_core"), (4, "triattn_out")):
             plan.append((name, lambda m=mod, st_=starting, st=stage:
                          ops.triattn(m, zo, mb, st_, ops.OUT_ACCUMULATE, zo, ws, stages=st)))
-    plan.append(("pair_transition", lambda: ops.pair_transition(layer.transition_z, zo, ops.OUT_ACCUMULATE, zo)))
-    plan.append(("sequence_stack", lambda: layer.sequence_stack(s, z_out, mask)))
+    # the transition's epilogue also writes the sequence stack's pair bias, as in PairformerLayer.forward
+    bias = torch.empty((1, 16) + zo.shape[:2], device=zo.device)
+    pb = (layer.attention.proj_z[0], layer.attention.proj_z[1], bias[0])
+    plan.append(("pair_transition", lambda: ops.pair_transition(layer.transition_z, zo, ops.OUT_ACCUMULATE, zo,
+                                                                pair_bias=pb)))
+    plan.append(("sequence_stack", lambda: layer.sequence_stack(s, z_out, mask, pair_bias=bias)))
     totals = {}
     counts = {}
     for _ in range(reps):

@@ -45,6 +45,11 @@ SIGNATURES = {
     "bmx_pack_mfma_weights": (c_int, [_P, c_int64, c_int64, _P, _P]),
     "bmx_pair_transition_fwd": (c_int, [_P, c_int, c_int64, _P, _P, c_float, _P, _P, _P, c_int, _P]),
     "bmx_pair_bias_fwd": (c_int, [_P, c_int, c_int64, _P, _P, c_float, _P, c_int, _P, _P]),
+    "bmx_pair_bias_fold_bytes": (c_size_t, []),
+    "bmx_pair_bias_fold": (c_int, [_P, _P, _P, c_int, _P, _P]),
+    "bmx_pair_transition_bias_fwd": (c_int, [_P, c_int, c_int64, _P, _P, c_float, _P, _P, _P, c_int, _P, c_float, _P,
+                                             _P]),
+    "bmx_seq_attention_fwd": (c_int, [_P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int, c_int, c_float, _P, _P]),
 }
 
 

@@ -19,10 +19,6 @@ constexpr int kHeads = 16;
 constexpr int kTile = 64;          // pairs per block: 4 waves x 16
 constexpr int kXRow = kC + 4;      // fp32 LDS row
 
-__device__ __forceinline__ f32x4 mfma16f32(float a, float b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
 // 16x16x4 f32 fragments (lane l, group g = l / 16): A holds A[l%16][k=g],
 // B holds B[k=g][l%16], D register r holds D[4*g + r][l%16].
 // Persistent: a block keeps the weights in VGPRs and walks tiles of 64 pairs
@@ -72,6 +68,131 @@ __global__ __launch_bounds__(256) void pair_bias_kernel(const TIn* __restrict__ 
   }
 }
 
+// ------------------------------------------------------------------
+// Pair-biased attention of the sequence stack, fp32, one pass:
+//   out[i][h*24+d] = sigmoid(g[i][h*24+d]) * sum_j softmax_j(q_i.k_j / sqrt(24) + bias[h][i][j]
+//                                                            + (1 - mask[j]) * -inf) v_j[d]
+// (upstream AttentionPairBias, math as pair_bias.py:21-36; the [16, N, N]
+// logits never reach HBM).
+//
+// Both products run on fp32 MFMA (v_mfma_f32_16x16x4f32; lane l, group
+// gi = l / 16: A holds A[l%16][k = gi], B holds B[k = gi][l%16], D register r
+// holds D[4 gi + r][l%16]).  A block owns 16 queries of one head; its 4 waves
+// split the keys (wave w takes the 64-key steps w, w + 4, ...) and merge
+// their softmax states through LDS at the end.  Per 16-key tile:
+//   S[key][q]   = K Q^T        A = K rows, B = Q^T; the 24 head dims are
+//                              the k index 6 gi + s of six MFMA steps;
+//   O^T[d][q]  += V^T P^T      B = P^T is the S tile itself (register s of
+//                              lane (q, gi) is key 4 gi + s, the k index of
+//                              step s), A = V^T in two 16-row d tiles (rows
+//                              24..31 are zero).
+// Every lane then holds whole columns (one query) of S and O^T, so the
+// running max and the rescale need only the xor-16 / xor-32 exchanges.
+constexpr int kAttnD = 24, kAttnQ = 16, kAttnWaves = 4, kAttnStep = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+__global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                            const float* __restrict__ v,
+                                                            const float* __restrict__ bias,
+                                                            const float* __restrict__ mask,
+                                                            const float* __restrict__ g, int n, int64_t ld,
+                                                            float inf, float rscale, bool vec,
+                                                            float* __restrict__ out) {
+  constexpr int D = kAttnD, HD = kHeads * D;
+  __shared__ float part_o[kAttnWaves][32][kAttnQ];
+  __shared__ float part_m[kAttnWaves][kAttnQ], part_l[kAttnWaves][kAttnQ];
+  const int h = blockIdx.y, q0 = blockIdx.x * kAttnQ;
+  const int w = threadIdx.x >> 6, l = lane_id(), gi = l >> 4, c = l & 15;
+  const int qc = min(q0 + c, n - 1);  // rows past the end re-read the last one and are not stored
+  float qf[6];
+#pragma unroll
+  for (int s = 0; s < 6; ++s) qf[s] = q[(int64_t)qc * ld + h * D + 6 * gi + s];
+  const float* brow = bias + ((int64_t)h * n + qc) * n;
+  const int dv1 = 16 + (c & 7);  // second d tile: rows 16..23 real, 24..31 zero
+  f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = o0;
+  float m = -3.4e38f, lsum = 0.f;
+  for (int key0 = w * kAttnStep; key0 < n; key0 += kAttnWaves * kAttnStep) {
+    const bool full = vec && key0 + kAttnStep <= n;
+    f32x4 st[4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int kr = min(key0 + 16 * t + c, n - 1);
+      const float* krow = k + (int64_t)kr * ld + h * D + 6 * gi;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 6; ++s) acc = mfma16f32(krow[s], qf[s], acc);
+      const int kb = key0 + 16 * t + 4 * gi;  // this lane's keys kb .. kb + 3
+      f32x4 b4, m4;
+      if (full) {
+        b4 = *(const f32x4*)(brow + kb);
+        m4 = *(const f32x4*)(mask + kb);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          b4[r] = brow[min(kb + r, n - 1)];
+          m4[r] = mask[min(kb + r, n - 1)];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = (acc[r] * rscale + b4[r]) + (1.f - m4[r]) * -inf;
+        st[t][r] = kb + r < n ? x : -INFINITY;
+        tmax = fmaxf(tmax, st[t][r]);
+      }
+    }
+    const float mn = fmaxf(m, col_max(tmax));
+    const float alpha = __builtin_amdgcn_exp2f((m - mn) * kLog2e);
+    m = mn;
+    lsum *= alpha;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o0[r] *= alpha, o1[r] *= alpha;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float p = __builtin_amdgcn_exp2f((st[t][s] - mn) * kLog2e);
+        lsum += p;
+        const int kr = min(key0 + 16 * t + 4 * gi + s, n - 1);
+        const float* vrow = v + (int64_t)kr * ld + h * D;
+        const float a1 = vrow[dv1];
+        o0 = mfma16f32(vrow[c], p, o0);
+        o1 = mfma16f32(c < 8 ? a1 : 0.f, p, o1);
+      }
+    }
+  }
+  // This wave's state for its 16 queries: O^T rows 4 gi + r (tile 0) and
+  // 16 + 4 gi + r (tile 1), the max m, and the key sum over the four lane groups.
+  lsum = col_sum(lsum);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    part_o[w][4 * gi + r][c] = o0[r];
+    part_o[w][16 + 4 * gi + r][c] = o1[r];
+  }
+  if (gi == 0) part_m[w][c] = m, part_l[w][c] = lsum;
+  __syncthreads();
+  // Merge: thread (query qi, dim group) finishes 24 / 16 dims per 16 threads.
+  const int qi = threadIdx.x & 15, i = q0 + qi;
+  if (i < n) {
+    float mm = part_m[0][qi];
+#pragma unroll
+    for (int u = 1; u < kAttnWaves; ++u) mm = fmaxf(mm, part_m[u][qi]);
+    float wt[kAttnWaves], ll = 0.f;
+#pragma unroll
+    for (int u = 0; u < kAttnWaves; ++u) {
+      wt[u] = __builtin_amdgcn_exp2f((part_m[u][qi] - mm) * kLog2e);
+      ll += wt[u] * part_l[u][qi];
+    }
+    for (int d = threadIdx.x >> 4; d < D; d += 16) {
+      float acc = 0.f;
+#pragma unroll
+      for (int u = 0; u < kAttnWaves; ++u) acc += wt[u] * part_o[u][d][qi];
+      const float gate = sigmoid_f(g[(int64_t)i * ld + h * D + d]);
+      out[(int64_t)i * HD + h * D + d] = gate * (acc / ll);
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -92,6 +213,24 @@ int bmx_pair_bias_fwd(const void* z, int z_dtype, int64_t rows, const float* ln_
   else
     pair_bias_kernel<bf16><<<grid, 256, 0, stream>>>((const bf16*)z, ln_w, ln_b, eps, w, out, rows);
   return check_launch("bmx_pair_bias_fwd");
+}
+
+int bmx_seq_attention_fwd(const float* q, const float* k, const float* v, const float* bias, const float* mask,
+                          const float* g, int64_t n, int64_t ld, int heads, int head_dim, float inf, float* out,
+                          hipStream_t stream) {
+  BMX_REQUIRE(n >= 0 && n <= (1 << 20), "bmx_seq_attention_fwd: n must be in [0, 2^20]");
+  BMX_REQUIRE(heads == kHeads && head_dim == kAttnD, "bmx_seq_attention_fwd: built for %d heads x %d dims (got %d x %d)",
+              kHeads, kAttnD, heads, head_dim);
+  BMX_REQUIRE(ld >= kHeads * kAttnD, "bmx_seq_attention_fwd: row stride ld must be >= %d", kHeads * kAttnD);
+  BMX_REQUIRE(inf > 0.f, "bmx_seq_attention_fwd: inf must be positive");
+  if (n == 0) return BMX_OK;
+  BMX_REQUIRE(q && k && v && bias && mask && g && out, "bmx_seq_attention_fwd: null pointer");
+  // 16-byte bias / mask loads where every row start is aligned; scalar loads otherwise
+  const bool vec = n % 4 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)mask % 16 == 0;
+  const dim3 grid((unsigned)((n + kAttnQ - 1) / kAttnQ), kHeads);
+  seq_attention_kernel<<<grid, 256, 0, stream>>>(q, k, v, bias, mask, g, (int)n, ld, inf, 1.f / sqrtf((float)kAttnD),
+                                                 vec, out);
+  return check_launch("bmx_seq_attention_fwd");
 }
 
 }  // extern "C"

@@ -142,6 +142,21 @@ class Transition(nn.Module):
         x = self.norm(x)
         return self.fc3(self.silu(self.fc1(x)) * self.fc2(x))
 
+    def residual(self, x, inplace=False):
+        """``x + self(x)`` for the unfused sizes: fc1 | fc2 as one GEMM and the
+        residual add in the fc3 GEMM's epilogue (fp32 x; written into x when
+        ``inplace`` and x is contiguous)."""
+        if self.fused or x.dtype != torch.float32 or self.fc3.weight.dtype != x.dtype or torch.is_grad_enabled():
+            return x + self(x)
+        w12 = ops.cached_weight(self, "w12", (self.fc1.weight, self.fc2.weight), lambda a, b: torch.cat([a, b], 0))
+        h = F.linear(self.norm(x), w12)
+        h = F.silu(h[..., :self.hidden]).mul_(h[..., self.hidden:])
+        x2 = x.reshape(-1, x.shape[-1])
+        if inplace and x.is_contiguous():
+            x2.addmm_(h.reshape(-1, self.hidden), self.fc3.weight.t())
+            return x
+        return torch.addmm(x2, h.reshape(-1, self.hidden), self.fc3.weight.t()).view(x.shape)
+
 
 class AttentionPairBias(nn.Module):
     """Upstream ``attentionv2.AttentionPairBias`` (sequence stack, fp32)."""
@@ -167,10 +182,49 @@ class AttentionPairBias(nn.Module):
             return z.movedim(-1, 1)
         norm, lin = self.proj_z[0], self.proj_z[1]
         if z.is_cuda and z.shape[-1] == 128 and lin.weight.shape[0] == 16 and z.shape[1] == z.shape[2]:
-            return torch.stack([ops.pair_bias(norm, lin, z[b].contiguous()) for b in range(z.shape[0])])
+            out = torch.empty((z.shape[0], 16, z.shape[1], z.shape[2]), device=z.device, dtype=torch.float32)
+            for b in range(z.shape[0]):
+                ops.pair_bias(norm, lin, z[b].contiguous(), out=out[b])
+            return out
         return self.proj_z(z).movedim(-1, 1)
 
+    def fused_bias_ok(self, z):
+        """Whether ``pair_bias(z)`` is the fused 128 -> 16 kernel's (so a
+        producer of z may compute it in its own epilogue instead)."""
+        return (self.compute_pair_bias and z.is_cuda and z.shape[-1] == 128 and z.shape[1] == z.shape[2]
+                and self.proj_z[1].weight.shape == (16, 128))
+
+    def attend(self, s, z, mask, k_in, multiplicity=1, bias=None):
+        """``g * attention`` before ``proj_o`` ([B, N, c_s]) from the fused
+        gfx950 kernel, or None where it does not apply (CPU, grad, another
+        head shape or dtype).  With ``k_in is s`` the four input projections
+        run as one GEMM whose column slices the kernel reads in place.
+        ``bias``, when given, is ``pair_bias(z)`` computed already."""
+        if not (s.is_cuda and s.dtype == torch.float32 and k_in.dtype == torch.float32 and self.num_heads == 16
+                and self.head_dim == 24 and not torch.is_grad_enabled()):
+            return None
+        if k_in is s:
+            w = ops.cached_weight(self, "qkvg", (self.proj_q.weight, self.proj_k.weight, self.proj_v.weight,
+                                                 self.proj_g.weight), lambda *ws: torch.cat(ws, 0).float())
+            bq = ops.cached_weight(self, "qkvg_bias", (self.proj_q.bias,),
+                                   lambda b: torch.cat([b.float(), b.new_zeros(3 * self.c_s)]))
+            proj = F.linear(s, w, bq)
+            q, k, v, g = proj.split(self.c_s, dim=-1)
+        else:
+            q, k, v, g = self.proj_q(s), self.proj_k(k_in), self.proj_v(k_in), self.proj_g(s)
+        bias = self.pair_bias(z).float() if bias is None else bias
+        m = mask.float()
+        o = torch.empty(s.shape[:-1] + (self.c_s,), device=s.device, dtype=torch.float32)
+        for i in range(s.shape[0]):
+            # the bias of batch element i // multiplicity (upstream repeat_interleave)
+            ops.seq_attention(q[i], k[i], v[i], bias[i // multiplicity].contiguous(), m[i].contiguous(), g[i],
+                              self.inf, out=o[i])
+        return o
+
     def forward(self, s, z, mask, k_in, multiplicity=1):
+        o = self.attend(s, z, mask, k_in, multiplicity)
+        if o is not None:
+            return self.proj_o(o)
         b = s.shape[0]
         q = self.proj_q(s).view(b, -1, self.num_heads, self.head_dim).transpose(1, 2)
         k = self.proj_k(k_in).view(b, -1, self.num_heads, self.head_dim).transpose(1, 2)
@@ -204,10 +258,12 @@ class PairformerLayer(nn.Module):
         self.transition_z = Transition(token_z, token_z * 4)
         self.s_post_norm = nn.LayerNorm(token_s) if post_layer_norm else nn.Identity()
 
-    def pair_stack(self, z, pair_mask, z_out=None, workspace=None):
+    def pair_stack(self, z, pair_mask, z_out=None, workspace=None, bias_out=None):
         """z_out = z + tri_mul_out + tri_mul_in + tri_att_start + tri_att_end + transition_z,
         each added in order into the fp32 stream (eval dropout is identity).
-        z is read once and never written; z_out may be preallocated."""
+        z is read once and never written; z_out may be preallocated.  With
+        ``bias_out`` [B, 16, N, N] the transition's epilogue also writes the
+        sequence stack's pair bias of z_out (``attention.pair_bias(z_out)``)."""
         _require_cuda(z, "PairformerLayer")
         if z.dtype != torch.float32:
             raise RuntimeError("the pair stream is fp32")
@@ -222,21 +278,33 @@ class PairformerLayer(nn.Module):
             ops.trimul(self.tri_mul_in, zo, mb, False, ops.OUT_ACCUMULATE, zo, ws)
             ops.triattn(self.tri_att_start, zo, mb, True, ops.OUT_ACCUMULATE, zo, ws)
             ops.triattn(self.tri_att_end, zo, mb, False, ops.OUT_ACCUMULATE, zo, ws)
-            ops.pair_transition(self.transition_z, zo, ops.OUT_ACCUMULATE, zo)
+            pb = None if bias_out is None else (self.attention.proj_z[0], self.attention.proj_z[1], bias_out[b])
+            ops.pair_transition(self.transition_z, zo, ops.OUT_ACCUMULATE, zo, pair_bias=pb)
         return z_out
 
-    def sequence_stack(self, s, z, mask):
+    def sequence_stack(self, s, z, mask, pair_bias=None):
+        """s + attention, then + transition_s (upstream order, fp32); on the
+        fused path each residual add rides in the epilogue of its output GEMM.
+        ``pair_bias``: ``attention.pair_bias(z)`` if already computed."""
         with torch.autocast("cuda", enabled=False):
             s = s.float()
             s_normed = self.pre_norm_s(s)
-            s = s + self.attention(s=s_normed, z=z, mask=mask.float(), k_in=s_normed)
-            s = s + self.transition_s(s)
+            o = self.attention.attend(s_normed, z, mask.float(), s_normed, bias=pair_bias)
+            if o is None:
+                s = s + self.attention(s=s_normed, z=z, mask=mask.float(), k_in=s_normed)
+            else:
+                s = torch.addmm(s.reshape(-1, s.shape[-1]), o.reshape(-1, o.shape[-1]),
+                                self.attention.proj_o.weight.float().t()).view(s.shape)
+            s = self.transition_s.residual(s, inplace=o is not None)
             return self.s_post_norm(s)
 
     def forward(self, s, z, mask, pair_mask, chunk_size_tri_attn=None, use_kernels=False, z_out=None,
                 workspace=None):
-        z = self.pair_stack(z, pair_mask, z_out, workspace)
-        return self.sequence_stack(s, z, mask), z
+        bias = None
+        if self.attention.fused_bias_ok(z) and not torch.is_grad_enabled():
+            bias = torch.empty((z.shape[0], 16, z.shape[1], z.shape[2]), device=z.device, dtype=torch.float32)
+        z = self.pair_stack(z, pair_mask, z_out, workspace, bias_out=bias)
+        return self.sequence_stack(s, z, mask, pair_bias=bias), z
 
 
 class PairformerModule(nn.Module):

@@ -347,8 +347,13 @@ def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=No
     return out
 
 
-def pair_transition(module, x, out_mode=OUT_BF16, out=None):
-    """Fused Transition(128, 512) over the rows of x [..., 128]."""
+def pair_transition(module, x, out_mode=OUT_BF16, out=None, pair_bias=None):
+    """Fused Transition(128, 512) over the rows of x [..., 128].
+
+    ``pair_bias=(proj_z_norm, proj_z_linear, bias_out)`` also writes the
+    sequence stack's pair bias of the result (``pair_bias`` below applied to
+    ``out``) into ``bias_out`` [16, rows] in the same pass; it needs an fp32
+    ``out_mode``."""
     _cuda(x)
     _check(x.shape[-1] == C and x.dtype in (torch.float32, torch.bfloat16) and x.is_contiguous(),
            "expected contiguous fp32/bf16 x with 128 channels")
@@ -360,15 +365,39 @@ def pair_transition(module, x, out_mode=OUT_BF16, out=None):
     lnb = cached_weight(module, "ln_b", (module.norm.bias,), _f32)
     out = _out_tensor(x, out, out_mode)
     rows = x.numel() // C
+    if pair_bias is None:
+        if rows:
+            N.call("bmx_pair_transition_fwd", x.data_ptr(), _code(x.dtype), rows, lnw.data_ptr(), lnb.data_ptr(),
+                   float(module.norm.eps), w12.data_ptr(), w3.data_ptr(), out.data_ptr(), out_mode, _stream(x))
+        return out
+    norm, lin, bias_out = pair_bias
+    _check(out_mode != OUT_BF16, "the fused pair bias needs an fp32 out_mode")
+    _check(lin.weight.shape == (16, C), "expected a 128 -> 16 projection")
+    _check(bias_out.numel() == 16 * rows and bias_out.dtype == torch.float32 and bias_out.is_contiguous(),
+           "bias_out must be a contiguous fp32 tensor of 16 x rows")
+    fold = cached_weight(lin, "pair_bias_fold", (norm.weight, norm.bias, lin.weight), pair_bias_fold)
     if rows:
-        N.call("bmx_pair_transition_fwd", x.data_ptr(), _code(x.dtype), rows, lnw.data_ptr(), lnb.data_ptr(),
-               float(module.norm.eps), w12.data_ptr(), w3.data_ptr(), out.data_ptr(), out_mode, _stream(x))
+        N.call("bmx_pair_transition_bias_fwd", x.data_ptr(), _code(x.dtype), rows, lnw.data_ptr(), lnb.data_ptr(),
+               float(module.norm.eps), w12.data_ptr(), w3.data_ptr(), out.data_ptr(), out_mode, fold.data_ptr(),
+               float(norm.eps), bias_out.data_ptr(), _stream(x))
     return out
 
 
-def pair_bias(proj_z_norm, proj_z_linear, z):
-    """fp32 ``Linear(LN(z))`` for 16 heads, returned head-major as [H, N, N]
-    (the layout AttentionPairBias adds to its logits); z is [N, N, 128]."""
+def pair_bias_fold(ln_w, ln_b, w):
+    """Folded pair-bias weights (``bmx_pair_bias_fold``): the LayerNorm affine
+    folded into the 128 -> 16 projection, in the fused epilogue's operand order."""
+    _cuda(ln_w, ln_b, w)
+    _check(ln_w.shape == (C,) and ln_b.shape == (C,) and w.shape == (16, C), "expected a 128 -> 16 projection")
+    ln_w, ln_b, w = (_f32(t) for t in (ln_w, ln_b, w))
+    out = torch.empty(N.lib().bmx_pair_bias_fold_bytes(), dtype=torch.uint8, device=w.device)
+    N.call("bmx_pair_bias_fold", ln_w.data_ptr(), ln_b.data_ptr(), w.data_ptr(), 16, out.data_ptr(), _stream(w))
+    return out
+
+
+def pair_bias(proj_z_norm, proj_z_linear, z, out=None):
+    """fp32 ``Linear(LN(z))`` for 16 heads, returned (or written into ``out``)
+    head-major as [H, N, N] (the layout AttentionPairBias adds to its logits);
+    z is [N, N, 128]."""
     _cuda(z)
     _check(z.dim() == 3 and z.shape[-1] == C and z.dtype in (torch.float32, torch.bfloat16) and z.is_contiguous(),
            "expected contiguous z of shape [N, N, 128]")
@@ -377,11 +406,40 @@ def pair_bias(proj_z_norm, proj_z_linear, z):
     w = cached_weight(proj_z_linear, "w32", (proj_z_linear.weight,), _f32)
     lnw = cached_weight(proj_z_norm, "w32", (proj_z_norm.weight,), _f32)
     lnb = cached_weight(proj_z_norm, "b32", (proj_z_norm.bias,), _f32)
-    out = torch.empty((heads, z.shape[0], z.shape[1]), device=z.device, dtype=torch.float32)
+    shape = (heads, z.shape[0], z.shape[1])
+    if out is None:
+        out = torch.empty(shape, device=z.device, dtype=torch.float32)
+    _check(out.shape == shape and out.dtype == torch.float32 and out.is_contiguous(),
+           "out must be a contiguous fp32 [16, N, N]")
     rows = z.shape[0] * z.shape[1]
     if rows:
         N.call("bmx_pair_bias_fwd", z.data_ptr(), _code(z.dtype), rows, lnw.data_ptr(), lnb.data_ptr(),
                float(proj_z_norm.eps), w.data_ptr(), heads, out.data_ptr(), _stream(z))
+    return out
+
+
+def seq_attention(q, k, v, bias, mask, g, inf, out=None):
+    """Pair-biased softmax attention of the sequence stack, fp32, for one batch
+    element: q, k, v and the gate logits g are [N, 384] (16 heads x 24) with
+    unit column stride and one common row stride (e.g. column slices of a
+    fused [N, 1536] projection), bias [16, N, N], mask [N].  Returns (or
+    writes into ``out``) ``sigmoid(g) * softmax(q k^T / sqrt(24) + bias +
+    (1 - mask) * -inf) v`` as a contiguous [N, 384]."""
+    _cuda(q, k, v, bias, mask, g)
+    n = q.shape[0]
+    ld = q.stride(0) if n > 1 else 384
+    for t in (q, k, v, g):
+        _check(t.shape == (n, 384) and t.dtype == torch.float32 and t.stride(1) == 1
+               and (n <= 1 or t.stride(0) == ld), "expected fp32 [N, 384] q / k / v / g with one row stride")
+    _check(bias.shape == (16, n, n) and bias.dtype == torch.float32 and bias.is_contiguous(),
+           "expected a contiguous fp32 [16, N, N] bias")
+    _check(mask.shape == (n,) and mask.dtype == torch.float32 and mask.is_contiguous(), "expected an fp32 [N] mask")
+    if out is None:
+        out = torch.empty((n, 384), device=q.device, dtype=torch.float32)
+    _check(out.shape == (n, 384) and out.dtype == torch.float32 and out.is_contiguous(),
+           "out must be a contiguous fp32 [N, 384]")
+    N.call("bmx_seq_attention_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), mask.data_ptr(),
+           g.data_ptr(), n, ld, 16, 24, float(inf), out.data_ptr(), _stream(q))
     return out
 
 

@@ -137,6 +137,26 @@ int bmx_pack_mfma_weights(const void* src, int64_t rows, int64_t cols, void* dst
 int bmx_pair_transition_fwd(const void* x, int x_dtype, int64_t rows, const float* ln_w, const float* ln_b, float eps,
                             const void* w12, const void* w3, void* out, int out_mode, bmx_stream_t stream);
 
+/* Bytes of the folded pair-bias weights written by bmx_pair_bias_fold (8256). */
+size_t bmx_pair_bias_fold_bytes(void);
+
+/* Fold the sequence stack's pair-bias LayerNorm affine (ln_w, ln_b: [128]) and projection
+ * w ([16][128]) into the operand order of bmx_pair_transition_bias_fwd: bf16 high and low parts
+ * of W'[h][c] = ln_w[c] * w[h][c] and b[h] = sum_c ln_b[c] * w[h][c].  Weight preparation, once
+ * per weight version, like bmx_pack_mfma_weights (AttentionPairBias.proj_z of pair_bias.py:21-36). */
+int bmx_pair_bias_fold(const float* ln_w, const float* ln_b, const float* w, int heads, void* folded,
+                       bmx_stream_t stream);
+
+/* bmx_pair_transition_fwd (fp32 out_mode 1-3) followed, in the same pass, by the Pairformer
+ * sequence stack's pair bias of the updated rows: pb_out[h][row] = sum_c LN(out[row])[c] * w[h][c]
+ * (fp32 result, eps pb_eps, 16 heads, pb_out [16][rows]), i.e. bmx_pair_bias_fwd on `out`
+ * without reading it back; pb_folded is bmx_pair_bias_fold's output.  The composition upstream
+ * PairformerLayer runs (transition_z, then AttentionPairBias.proj_z on the new z;
+ * pair_transition.py:8-28 and pair_bias.py:21-36). */
+int bmx_pair_transition_bias_fwd(const void* x, int x_dtype, int64_t rows, const float* ln_w, const float* ln_b,
+                                 float eps, const void* w12, const void* w3, void* out, int out_mode,
+                                 const void* pb_folded, float pb_eps, float* pb_out, bmx_stream_t stream);
+
 /* ---- Sequence-stack pair bias (next to the hot path) ------------------- */
 
 /* bias[h][row] = sum_c LN(z[row])[c] * w[h][c] for heads = 16, fp32 math; out is
@@ -146,6 +166,18 @@ int bmx_pair_transition_fwd(const void* x, int x_dtype, int64_t rows, const floa
  * math restated at src/boltz_lumi/pair_bias.py:21-36). */
 int bmx_pair_bias_fwd(const void* z, int z_dtype, int64_t rows, const float* ln_w, const float* ln_b, float eps,
                       const float* w, int heads, float* out, bmx_stream_t stream);
+
+/* out[i][h*24+d] = sigmoid(g[i][h*24+d]) * sum_j softmax_j(q_i.k_j / sqrt(24) + bias[h][i][j]
+ *                                                          + (1 - mask[j]) * -inf) v_j[d],  fp32,
+ * for heads = 16, head_dim = 24.  q, k, v and the gate logits g are [n] rows of 384 values at
+ * row stride ld (>= 384; e.g. column slices of one fused [n, 1536] projection), bias is
+ * [16][n][n], mask [n], out [n][384] contiguous.
+ * Replaces the logits / softmax / PV / gate part of AttentionPairBias.forward of the
+ * sequence stack (math as src/boltz_lumi/pair_bias.py:21-36), which the reference leaves to
+ * torch (adapters.py:39-45); the [16, n, n] logits never reach HBM. */
+int bmx_seq_attention_fwd(const float* q, const float* k, const float* v, const float* bias, const float* mask,
+                          const float* g, int64_t n, int64_t ld, int heads, int head_dim, float inf, float* out,
+                          bmx_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -69,6 +69,14 @@ def test_argument_validation_needs_no_gpu(lib):
     rc = lib.bmx_pack_mfma_weights(None, 32, 128, None, None)
     assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
     assert lib.bmx_pack_mfma_weights(None, 0, 128, None, None) == N.BMX_OK
+    rc = N.lib().bmx_pair_transition_bias_fwd(None, 0, 8, None, None, ctypes.c_float(1e-5), None, None, None, 0,
+                                              None, ctypes.c_float(1e-5), None, None)
+    assert rc == N.BMX_EINVAL and b"out_mode" in lib.bmx_last_error()
+    rc = lib.bmx_pair_bias_fold(None, None, None, 8, None, None)
+    assert rc == N.BMX_EINVAL and b"16 heads" in lib.bmx_last_error()
+    rc = lib.bmx_seq_attention_fwd(None, None, None, None, None, None, 8, 100, 16, 24, 1e6, None, None)
+    assert rc == N.BMX_EINVAL and b"row stride" in lib.bmx_last_error()
+    assert lib.bmx_pair_bias_fold_bytes() == 2 * 4 * 64 * 8 * 2 + 16 * 4
 
 
 def test_call_raises_with_message(lib):

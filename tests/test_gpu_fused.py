@@ -6,6 +6,8 @@ with relative L2 reported beside it.  Cases mirror the reference's matrices
 boundaries, masks zero / ones / partial / fractional, both directions.
 """
 
+import copy
+
 import pytest
 import torch
 
@@ -114,6 +116,35 @@ def test_pair_transition_matches_oracle(gpu, rows, dtype):
         got = ops.pair_transition(td, x.to(gpu))
     e = errors(got, want)
     assert want.abs().max() > 0 and e["max_rel"] < TOL, e
+
+
+@pytest.mark.parametrize("rows,mode", [(1, ops.OUT_RESIDUAL), (117, ops.OUT_ACCUMULATE),
+                                       (128 * 5 + 3, ops.OUT_RESIDUAL), (128 * 8, ops.OUT_F32)])
+def test_pair_transition_with_pair_bias(gpu, rows, mode):
+    """The fused epilogue's pair bias equals the oracle's proj_z applied to
+    the kernel's own fp32 output (LN + 128 -> 16 in fp32), and equals the
+    stand-alone pair-bias kernel on that output; the transition output is
+    bitwise the plain entry point's."""
+    g = torch.Generator().manual_seed(17 + rows)
+    t = R.randomize(R.Transition(128, 512), std=0.05, generator=g)
+    apb = R.randomize(R.AttentionPairBias(384, 128, 16), generator=g)
+    norm, lin = apb.proj_z[0], apb.proj_z[1]
+    x = torch.randn(rows, 128, generator=g)
+    td, nd, ld = t.to(gpu), copy.deepcopy(norm).to(gpu), copy.deepcopy(lin).to(gpu)
+    xd = x.to(gpu)
+    with torch.inference_mode():
+        plain_out = xd.clone()
+        plain = ops.pair_transition(td, plain_out if mode == ops.OUT_ACCUMULATE else xd, mode,
+                                    plain_out if mode == ops.OUT_ACCUMULATE else None)
+        out = xd.clone() if mode == ops.OUT_ACCUMULATE else torch.empty_like(xd)
+        bias = torch.empty(16, rows, device=gpu)
+        got = ops.pair_transition(td, out if mode == ops.OUT_ACCUMULATE else xd, mode, out, pair_bias=(nd, ld, bias))
+        alone = ops.pair_bias(nd, ld, got.view(rows, 1, 128)).view(16, rows)
+    assert torch.equal(got, plain)
+    with torch.no_grad():
+        want = lin(norm(got.cpu())).t()  # oracle proj_z on the kernel's output, [16, rows]
+    assert (bias.cpu() - want).abs().max() / want.abs().max() < 1e-5  # fp32 epilogue
+    assert (bias - alone).abs().max() / alone.abs().max() < 1e-5
 
 
 @pytest.mark.parametrize("rows,cols", [(32, 16), (1024, 128), (128, 512)])

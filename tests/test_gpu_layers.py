@@ -104,3 +104,84 @@ def test_pair_bias_matches_upstream_fp32(gpu, n):
         got = mine.pair_bias(z.to(gpu))
     assert got.shape == want.shape
     assert max_rel(got, want) < 1e-5  # fp32 path
+
+
+def _seq_attention_fp64(q, k, v, bias, mask, g, inf):
+    """Upstream AttentionPairBias logits / softmax / PV / gate in float64 on
+    the CPU (g holds the gate logits)."""
+    qh, kh, vh = (t.double().view(t.shape[0], 16, 24).transpose(0, 1) for t in (q, k, v))
+    logits = qh @ kh.transpose(-1, -2) / 24 ** 0.5 + bias.double()
+    logits = logits + (1 - mask.double()[None, None]) * -inf
+    o = (torch.softmax(logits, -1) @ vh).transpose(0, 1).reshape(q.shape[0], 384)
+    return torch.sigmoid(g.double()) * o
+
+
+@pytest.mark.parametrize("n,masked", [(1, False), (37, True), (64, False), (256, False), (301, True), (640, True)])
+def test_seq_attention_matches_fp64(gpu, n, masked):
+    g = torch.Generator().manual_seed(1000 + n)
+    q, k, v, gate = (torch.randn(n, 384, generator=g) for _ in range(4))
+    bias = torch.randn(16, n, n, generator=g) * 2
+    mask = torch.ones(n)
+    if masked:
+        mask[torch.randperm(n, generator=g)[: n // 3]] = 0
+        mask[0] = 1
+    want = _seq_attention_fp64(q, k, v, bias, mask, gate, 1e6)
+    got = ops.seq_attention(*(t.to(gpu) for t in (q, k, v, bias, mask, gate)), 1e6)
+    assert max_rel(got, want) < 1e-4  # fp32 kernel
+    if masked:  # masked keys carry no weight: dropping them changes nothing
+        keep = mask.bool()
+        want_kept = _seq_attention_fp64(q, k[keep], v[keep], bias[:, :, keep], mask[keep], gate, 1e6)
+        assert max_rel(got, want_kept) < 1e-4
+
+
+def test_seq_attention_strided_rows_and_unaligned_bias(gpu):
+    # q / k / v / g as column slices of one [n, 1536] projection (row stride
+    # 1536), and a bias base off 16-byte alignment (scalar bias loads)
+    n = 64
+    g = torch.Generator().manual_seed(7)
+    proj = torch.randn(n, 4 * 384, generator=g)
+    q, k, v, gate = proj.split(384, dim=1)
+    flat = torch.randn(16 * n * n + 1, generator=g)
+    bias = flat[1:].view(16, n, n)
+    mask = torch.ones(n)
+    want = _seq_attention_fp64(q, k, v, bias, mask, gate, 1e6)
+    qd, kd, vd, gd = proj.to(gpu).split(384, dim=1)
+    got = ops.seq_attention(qd, kd, vd, flat.to(gpu)[1:].view(16, n, n), mask.to(gpu), gd, 1e6)
+    assert max_rel(got, want) < 1e-4
+
+
+@pytest.mark.parametrize("n,same_k,multiplicity", [(33, False, 1), (200, True, 1), (70, True, 2)])
+def test_attention_pair_bias_forward_matches_upstream(gpu, n, same_k, multiplicity):
+    g = torch.Generator().manual_seed(50 + n)
+    ref = R.randomize(R.AttentionPairBias(384, 128, 16), generator=g)
+    bz = 2 // multiplicity
+    s = torch.randn(2, n, 384, generator=g)
+    k_in = s if same_k else torch.randn(2, n, 384, generator=g)
+    z = torch.randn(bz, n, n, 128, generator=g)
+    mask = torch.ones(2, n)
+    mask[1, -5:] = 0
+    with torch.no_grad():
+        want = ref(s, z, mask, k_in, multiplicity=multiplicity)
+    mine = layers.AttentionPairBias(384, 128, 16)
+    mine.load_state_dict(ref.state_dict())
+    mine = mine.to(gpu)
+    sd = s.to(gpu)
+    kd = sd if same_k else k_in.to(gpu)
+    with torch.inference_mode():
+        assert mine.attend(sd, z.to(gpu), mask.to(gpu), kd, multiplicity) is not None  # the fused path
+        got = mine(sd, z.to(gpu), mask.to(gpu), kd, multiplicity=multiplicity)
+    assert max_rel(got, want) < 1e-4
+
+
+def test_transition_residual_matches_upstream(gpu):
+    g = torch.Generator().manual_seed(3)
+    t = layers.Transition(384, 1536)
+    for p in t.parameters():
+        p.data = torch.randn(p.shape, generator=g) * 0.05
+    x = torch.randn(2, 50, 384, generator=g)
+    with torch.no_grad():
+        want = x.double() + t.double()(x.double())
+    t = t.float().to(gpu)
+    with torch.inference_mode():
+        got = t.residual(x.to(gpu))
+    assert max_rel(got, want) < 1e-5
