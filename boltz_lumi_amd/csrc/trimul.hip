@@ -60,10 +60,19 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
   }
 
   // Input row p of a tile is pair (rp, t0+p) (outgoing) or (t0+p, rp) (incoming).
+  // The tile's mask values (pair nt*32 + l%32 for this lane) are fetched with
+  // its rows: a mask load next to its use is sunk under the padding test and
+  // gets a vmcnt(0) wait, which would also wait for the whole prefetch.
   f32x4 pre[kP1 / 8];
+  float mpre[kP1 / 32];
   auto fetch = [&](int tile) {
     const int rp = tile / tiles_x, t0 = (tile % tiles_x) * kP1;
     const int rc = min(rp, n - 1);  // padding rows / columns re-read row n-1 and are zeroed after the LN
+#pragma unroll
+    for (int nt = 0; nt < kP1 / 32; ++nt) {  // first, so that a wait for them leaves the rows in flight
+      const int tc = min(t0 + nt * 32 + (l & 31), n - 1);
+      mpre[nt] = mask[outgoing ? (int64_t)rc * n + tc : (int64_t)tc * n + rc];
+    }
 #pragma unroll
     for (int u = 0; u < kP1 / 8; ++u) {
       const int tc = min(t0 + hw + 8 * u, n - 1);
@@ -72,7 +81,24 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
     }
   };
 
-  int tile = blockIdx.x;
+  // Tile k's operand rows leave the stage for the planes in iteration k+1,
+  // right after its LayerNorm and before the next prefetch: vmcnt counts
+  // stores in issue order, so stores issued before a prefetch have a whole
+  // MFMA phase to retire before the next wait for that prefetch.
+  auto store_planes = [&](int tile) {
+    const int rp = tile / tiles_x, t0 = (tile % tiles_x) * kP1;
+    // 2 operands x 128 channels x 8 chunks of 8 positions
+#pragma unroll
+    for (int u = 0; u < 2 * kC * (kP1 / 8) / 256; ++u) {
+      const int idx = threadIdx.x + 256 * u;
+      const int half = idx / (kC * (kP1 / 8)), ch = (idx / (kP1 / 8)) % kC, chunk = idx % (kP1 / 8);
+      const bf16x8 v = *(const bf16x8*)(stage + (half * kC + ch) * kStage1 + chunk * 8);
+      bf16* dst = (half ? b_pl : a_pl) + ch * plane + (int64_t)rp * np + t0 + chunk * 8;
+      *(bf16x8*)dst = v;
+    }
+  };
+
+  int tile = blockIdx.x, prev = -1;
   if (tile < total) fetch(tile);
   for (; tile < total; tile += gridDim.x) {
     const int rp = tile / tiles_x, t0 = (tile % tiles_x) * kP1;
@@ -84,7 +110,11 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
       bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
       *(bf16x4*)(xt + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
     }
-    __syncthreads();
+    float mcur[kP1 / 32];
+#pragma unroll
+    for (int nt = 0; nt < kP1 / 32; ++nt) mcur[nt] = mpre[nt];
+    if (prev >= 0) store_planes(prev);
+    __syncthreads();  // xt written; the stage has been read
     if (tile + (int)gridDim.x < total) fetch(tile + gridDim.x);
 
     // D[ch][pair]: A = weight rows, B = normalised pairs; lane l holds pair l%32.
@@ -92,9 +122,7 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
     for (int nt = 0; nt < kP1 / 32; ++nt) {
       const int tt = t0 + nt * 32 + (l & 31);
       // rows / columns past n (plane padding) are written as zeros
-      const int rc = min(rp, n - 1), tc = min(tt, n - 1);
-      const float mv = mask[outgoing ? (int64_t)rc * n + tc : (int64_t)tc * n + rc];
-      const float m = (rp < n && tt < n) ? mv : 0.f;
+      const float m = (rp < n && tt < n) ? mcur[nt] : 0.f;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         f32x16 ap = zero16(), ag = zero16();
@@ -112,18 +140,10 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
         }
       }
     }
-    __syncthreads();
-    // 2 operands x 128 channels x 8 chunks of 8 positions
-#pragma unroll
-    for (int u = 0; u < 2 * kC * (kP1 / 8) / 256; ++u) {
-      const int idx = threadIdx.x + 256 * u;
-      const int half = idx / (kC * (kP1 / 8)), ch = (idx / (kP1 / 8)) % kC, chunk = idx % (kP1 / 8);
-      const bf16x8 v = *(const bf16x8*)(stage + (half * kC + ch) * kStage1 + chunk * 8);
-      bf16* dst = (half ? b_pl : a_pl) + ch * plane + (int64_t)rp * np + t0 + chunk * 8;
-      *(bf16x8*)dst = v;
-    }
-    __syncthreads();
+    __syncthreads();  // stage written; xt has been read
+    prev = tile;
   }
+  if (prev >= 0) store_planes(prev);
 }
 
 // ------------------------------------------------------------------ K2
@@ -231,8 +251,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
 // ------------------------------------------------------------------ K3
 // Persistent and weight-stationary like K1.  A tile is 64 pairs (i, j0..j0+63).
 // The input rows stay in registers (row layout: a half-wave per row, 4
-// channels per lane) from the prefetch to the residual store, so x is read
-// from HBM exactly once; the MFMA result is re-laid out through LDS.
+// channels per lane) from the prefetch to the residual add, so x is read
+// from HBM exactly once; the MFMA result is re-laid out through LDS (ybuf),
+// where the residual is added.  Tile k's rows are stored from ybuf in
+// iteration k+1, before the next prefetch is issued: vmcnt counts stores in
+// issue order, so the wait for that prefetch does not wait for fresh stores.
 constexpr int kP3 = 64;
 
 __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, const bf16* __restrict__ o_pl,
@@ -243,12 +266,11 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
                                                             const bf16* __restrict__ w_pout,
                                                             const bf16* __restrict__ w_gout, void* out, int out_mode,
                                                             int n, int np) {
-  // xo: LN_out(O) and xg: LN_in(x), pairs x channels; ybuf (fp32) aliases both.
+  // xo: LN_out(O) and xg: LN_in(x), pairs x channels; ybuf: the tile's fp32 output rows.
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kP3 * kLdsRow];
+  __shared__ __attribute__((aligned(16))) float ybuf[kP3 * kYRow];
   bf16* xo = smem;
   bf16* xg = smem + kP3 * kLdsRow;
-  float* ybuf = (float*)smem;
-  static_assert(kP3 * kYRow * 4 <= 2 * kP3 * kLdsRow * 2, "ybuf must fit in the tile buffers");
   const int t = threadIdx.x, l = lane_id(), w = t >> 6, c0 = 32 * w;
   const int hw = t >> 5, hl = t & 31;
   const LnAffine aff_in = ln_affine(in_w, in_b, hl), aff_out = ln_affine(out_w, out_b, hl);
@@ -293,7 +315,25 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
     }
   };
 
-  int tile = blockIdx.x;
+  // Rows of ybuf (residual already added where it is held in registers) to
+  // the output; thread (half-wave row, 4 channels) as in the residual add.
+  auto store_rows = [&](int tile) {
+    const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
+#pragma unroll
+    for (int u = 0; u < kRowsPer; ++u) {
+      const int p = hw + 8 * u, j = j0 + p;
+      if (j < n) {
+        const f32x4 y = *(const f32x4*)(ybuf + p * kYRow + 4 * hl);
+        const int64_t off = ((int64_t)i * n + j) * kC + 4 * hl;
+        if (out_mode == kOutBF16 || (out_mode == kOutAccumulate && !x_in_regs))
+          store_row4(out, off, y, y, out_mode, false);
+        else
+          *(f32x4*)((float*)out + off) = y;
+      }
+    }
+  };
+
+  int tile = blockIdx.x, prev = -1;
   if (tile < total) fetch(tile);
   for (; tile < total; tile += gridDim.x) {
     const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
@@ -319,6 +359,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
         *(bf16x4*)(xo + (32 * pb + (l & 31)) * kLdsRow + c0 + 8 * q + 4 * (l >> 5)) = v;
       }
     }
+    if (prev >= 0) store_rows(prev);
     __syncthreads();
     if (tile + (int)gridDim.x < total) fetch(tile + gridDim.x);
 #pragma unroll
@@ -344,22 +385,21 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
 #pragma unroll
       for (int r = 0; r < 16; ++r) res[nt][r] = rbf(ay[r] * sigmoid_f(ag[r]));  // the bf16 module output
     }
-    __syncthreads();  // xo / xg are dead; ybuf aliases them
 #pragma unroll
     for (int nt = 0; nt < kP3 / 32; ++nt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) ybuf[(nt * 32 + drow(r, l)) * kYRow + c0 + (l & 31)] = res[nt][r];
     __syncthreads();
+    if (out_mode == kOutResidual || (out_mode == kOutAccumulate && x_in_regs)) {
 #pragma unroll
-    for (int u = 0; u < kRowsPer; ++u) {
-      const int p = hw + 8 * u, j = j0 + p;
-      if (j < n) {
-        const f32x4 y = *(const f32x4*)(ybuf + p * kYRow + 4 * hl);
-        store_row4(out, ((int64_t)i * n + j) * kC + 4 * hl, y, xc[u], out_mode, x_in_regs);
+      for (int u = 0; u < kRowsPer; ++u) {
+        f32x4* row = (f32x4*)(ybuf + (hw + 8 * u) * kYRow + 4 * hl);
+        *row = xc[u] + *row;
       }
     }
-    __syncthreads();
+    prev = tile;
   }
+  if (prev >= 0) store_rows(prev);
 }
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
