@@ -86,8 +86,14 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 // (i, j0..j0+63) of the row frame over the padded np x np range, so padding
 // rows and keys get their zero / -inf values from the same code; the next
 // tile's input rows are prefetched into registers during the current tile's
-// MFMAs.
+// MFMAs.  q, k and v^T leave through an LDS stage in their HBM order and are
+// stored in the next iteration, before the next prefetch: vmcnt counts
+// stores in issue order, so a wait for the prefetch never waits for fresh
+// stores.  q and k are computed as D[d][pair] and v^T as D[pair][d], so each
+// lane holds 4 consecutive elements of one stage row (one 8-byte LDS write).
 constexpr int kP1 = 64;
+constexpr int kQRow = kD + 8;   // staged q / k row of one pair (bf16, 80 bytes)
+constexpr int kVRow = kP1 + 8;  // staged v^T row of one head dim (bf16, 144 bytes)
 
 template <typename TIn>
 __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restrict__ x, const float* __restrict__ mask,
@@ -96,6 +102,9 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
                                                               const bf16* __restrict__ w_proj, float inf, int starting,
                                                               Layout L) {
   __shared__ __attribute__((aligned(16))) bf16 xt[kP1 * kLdsRow];
+  __shared__ __attribute__((aligned(16))) bf16 sq[kH * kP1 * kQRow];
+  __shared__ __attribute__((aligned(16))) bf16 sk[kH * kP1 * kQRow];
+  __shared__ __attribute__((aligned(16))) bf16 sv[kH * kD * kVRow];
   const int n = L.n, np = L.np;
   const int t = threadIdx.x, l = lane_id(), w = t >> 6, h = w, g = l >> 4, lq = l & 15;
   const int hw = t >> 5, hl = t & 31;
@@ -115,17 +124,40 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) wb[ks] = *(const bf16x8*)(w_proj + (3 * kC + lq) * kC + 32 * ks + 8 * g);
 
-  // Input rows (clamped into range: every load is unconditional, padding rows
-  // are zeroed after the LayerNorm).
+  // Input rows and the mask value of position j0 + t % 64 (clamped into range:
+  // every load is unconditional, padding rows are zeroed after the LayerNorm).
   constexpr int kRowsPer = kP1 / 8;
   f32x4 px[kRowsPer];
+  float mpre = 1.f;
   auto fetch = [&](int tile) {
     const int i = min(tile / tiles_x, n - 1), j0 = (tile % tiles_x) * kP1;
+    if (mask) {
+      const int jc = min(j0 + (t & (kP1 - 1)), n - 1);
+      mpre = starting ? mask[(int64_t)i * n + jc] : mask[(int64_t)jc * n + i];
+    }
 #pragma unroll
     for (int u = 0; u < kRowsPer; ++u) px[u] = load4(xrow(x, n, starting, i, min(j0 + hw + 8 * u, n - 1)) + 4 * hl);
   };
 
-  int tile = blockIdx.x;
+  // Stage -> HBM, 16-byte chunks: q and k are 4 KB runs per head, v^T 128-byte runs per (head, dim).
+  auto store_stage = [&](int tile) {
+    const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP1;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = t + 256 * u, hh = c >> 8, p = (c >> 2) & (kP1 - 1), part = c & 3;
+      const int64_t off = (((int64_t)i * kH + hh) * np + j0 + p) * kD + 8 * part;
+      *(bf16x8*)(L.q + off) = *(const bf16x8*)(sq + (hh * kP1 + p) * kQRow + 8 * part);
+      *(bf16x8*)(L.k + off) = *(const bf16x8*)(sk + (hh * kP1 + p) * kQRow + 8 * part);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = t + 256 * u, hh = c >> 8, d = (c >> 3) & (kD - 1), part = c & 7;
+      *(bf16x8*)(L.vt + (((int64_t)i * kH + hh) * kD + d) * np + j0 + 8 * part) =
+          *(const bf16x8*)(sv + (hh * kD + d) * kVRow + 8 * part);
+    }
+  };
+
+  int tile = blockIdx.x, prev = -1;
   if (tile < total) fetch(tile);
   for (; tile < total; tile += gridDim.x) {
     const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP1;
@@ -139,12 +171,10 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
     if (t < kP1) {
       // mask bias mb[i][j] = log2(e) * inf * (mask'[i][j] - 1); 0 outside n x n
       const int j = j0 + t;
-      const bool in = i < n && j < n;
-      const int ic = min(i, n - 1), jc = min(j, n - 1);
-      const float mv = mask ? (starting ? mask[(int64_t)ic * n + jc] : mask[(int64_t)jc * n + ic]) : 1.f;
-      L.mb[(int64_t)i * np + j] = in ? inf * (mv - 1.f) * kLog2e : 0.f;
+      L.mb[(int64_t)i * np + j] = (i < n && j < n) ? inf * (mpre - 1.f) * kLog2e : 0.f;
     }
-    __syncthreads();
+    if (prev >= 0) store_stage(prev);
+    __syncthreads();  // xt written; the stage has been read
     if (tile + (int)gridDim.x < total) fetch(tile + gridDim.x);
 
 #pragma unroll
@@ -152,27 +182,32 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
       bf16x8 xf[8];
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) xf[ks] = frag(xt, kLdsRow, nt * 32, ks);
-      // q, k: D[pair][d], lane -> d, register r -> pair 8(r/4) + 4(l/32) + r%4;
-      // each store writes 2 contiguous 64-byte rows.
-      const int64_t qk_off = (((int64_t)i * kH + h) * np + j0 + nt * 32 + 4 * (l >> 5)) * kD + (l & 31);
+      // q, k: D[d][pair], lane -> pair nt*32 + l%32, registers 4q'..4q'+3 -> d 8q' + 4(l/32) + 0..3.
 #pragma unroll
       for (int kind = 0; kind < 2; ++kind) {
         f32x16 acc = zero16();
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) acc = mfma32(xf[ks], kind == 0 ? wq[ks] : wk[ks], acc);
-        bf16* dst = (kind == 0 ? L.q : L.k) + qk_off;
+        for (int ks = 0; ks < 8; ++ks) acc = mfma32(kind == 0 ? wq[ks] : wk[ks], xf[ks], acc);
+        bf16* dst = (kind == 0 ? sq : sk) + (h * kP1 + nt * 32 + (l & 31)) * kQRow + 4 * (l >> 5);
         const float sc = kind == 0 ? qscale : 1.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dst[(8 * (r >> 2) + (r & 3)) * kD] = (bf16)(acc[r] * sc);
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const bf16x4 v = {(bf16)(acc[4 * q4] * sc), (bf16)(acc[4 * q4 + 1] * sc), (bf16)(acc[4 * q4 + 2] * sc),
+                            (bf16)(acc[4 * q4 + 3] * sc)};
+          *(bf16x4*)(dst + 8 * q4) = v;
+        }
       }
-      // v^T: D[d][pair], lane -> pair, register -> d; keys are stored permuted
-      // inside each 32-key block (see vperm), still 64 contiguous bytes per row.
+      // v^T: D[pair][d], lane -> d = l%32, registers 4q'..4q'+3 -> pairs nt*32 + 8q' + 4(l/32) + 0..3,
+      // stored at their permuted key slots (vperm keeps runs of 4 keys together).
       f32x16 av = zero16();
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) av = mfma32(wv[ks], xf[ks], av);
-      bf16* vdst = L.vt + ((int64_t)i * kH + h) * kD * np + (int64_t)(4 * (l >> 5)) * np + j0 + nt * 32 + vperm(l & 31);
+      for (int ks = 0; ks < 8; ++ks) av = mfma32(xf[ks], wv[ks], av);
+      bf16* vdst = sv + (h * kD + (l & 31)) * kVRow + nt * 32;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) vdst[(int64_t)(8 * (r >> 2) + (r & 3)) * np] = (bf16)av[r];
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const bf16x4 v = {(bf16)av[4 * q4], (bf16)av[4 * q4 + 1], (bf16)av[4 * q4 + 2], (bf16)av[4 * q4 + 3]};
+        *(bf16x4*)(vdst + vperm(8 * q4 + 4 * (l >> 5))) = v;
+      }
     }
     {
       // Triangle bias for pairs j0 + 16w .. +15: D[head][pair] on 16x16x32,
@@ -189,8 +224,10 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
         for (int r = 0; r < kH; ++r) dst[r * head_stride] = (tb_t)(j < n ? ab[r] * kLog2e : kPadBias);
       }
     }
-    __syncthreads();
+    __syncthreads();  // the stage is written; xt has been read
+    prev = tile;
   }
+  if (prev >= 0) store_stage(prev);
 }
 
 // ------------------------------------------------------------------ K2
