@@ -501,7 +501,10 @@ __global__ __launch_bounds__(kCoreThreads) __attribute__((amdgpu_waves_per_eu(4)
 // ------------------------------------------------------------------ K3
 // Persistent and weight-stationary; a tile is 64 positions (i, j0..j0+63) of
 // the row frame.  Input rows stay in registers from the prefetch to the
-// residual store, so x is read once; results are re-laid out through LDS.
+// residual add, so x is read once; results are re-laid out through LDS
+// (ybuf), where the residual is added.  Tile k's rows are stored from ybuf in
+// iteration k+1, before the next prefetch: vmcnt counts stores in issue
+// order, so the wait for that prefetch does not wait for fresh stores.
 constexpr int kP3 = 64;
 
 template <typename TIn>
@@ -513,10 +516,9 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
                                                              const float* __restrict__ b_o, int starting, void* out,
                                                              int out_mode, Layout L) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kP3 * kLdsRow];
+  __shared__ __attribute__((aligned(16))) float ybuf[kP3 * kYRow];  // fp32 result rows
   bf16* xg = smem;                   // LN(x'), pairs x channels
   bf16* xo = smem + kP3 * kLdsRow;   // attention output, then o * gate
-  float* ybuf = (float*)smem;        // fp32 result rows (aliases both)
-  static_assert(kP3 * kYRow * 4 <= 2 * kP3 * kLdsRow * 2, "ybuf must fit in the tile buffers");
   const int n = L.n;
   const int t = threadIdx.x, l = lane_id(), w = t >> 6, c0 = 32 * w, ch = c0 + (l & 31);
   const int hw = t >> 5, hl = t & 31;
@@ -532,6 +534,7 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
   }
   const float bg = b_g[ch], bo = b_o[ch];
 
+  // Rows past n re-read row n-1 (unconditional loads) and are not stored.
   constexpr int kRowsPer = kP3 / 8;
   f32x4 px[kRowsPer];
   bf16x4 po[kRowsPer];
@@ -539,21 +542,32 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
     const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
 #pragma unroll
     for (int u = 0; u < kRowsPer; ++u) {
-      const int j = j0 + hw + 8 * u;
+      const int j = min(j0 + hw + 8 * u, n - 1);
+      px[u] = load4(xrow(x, n, starting, i, j) + 4 * hl);
+      po[u] = *(const bf16x4*)(L.o + ((int64_t)i * n + j) * kC + 4 * hl);
+    }
+  };
+  // Rows of ybuf (residual already added where it is held in registers) to
+  // the output; thread (half-wave row, 4 channels) as in the residual add.
+  auto store_rows = [&](int tile) {
+    const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
+#pragma unroll
+    for (int u = 0; u < kRowsPer; ++u) {
+      const int p = hw + 8 * u, j = j0 + p;
       if (j < n) {
-        px[u] = load4(xrow(x, n, starting, i, j) + 4 * hl);
-        po[u] = *(const bf16x4*)(L.o + ((int64_t)i * n + j) * kC + 4 * hl);
-      } else {
-        px[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-        po[u] = bf16x4{};
+        const f32x4 y = *(const f32x4*)(ybuf + p * kYRow + 4 * hl);
+        const int64_t off = (starting ? (int64_t)i * n + j : (int64_t)j * n + i) * kC + 4 * hl;
+        if (out_mode == kOutBF16 || (out_mode == kOutAccumulate && !x_in_regs))
+          store_row4(out, off, y, y, out_mode, false);
+        else
+          *(f32x4*)((float*)out + off) = y;
       }
     }
   };
 
-  int tile = blockIdx.x;
+  int tile = blockIdx.x, prev = -1;
   if (tile < total) fetch(tile);
   for (; tile < total; tile += gridDim.x) {
-    const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
     f32x4 xc[kRowsPer];
 #pragma unroll
     for (int u = 0; u < kRowsPer; ++u) {
@@ -563,6 +577,7 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
       *(bf16x4*)(xg + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
       *(bf16x4*)(xo + (hw + 8 * u) * kLdsRow + 4 * hl) = po[u];
     }
+    if (prev >= 0) store_rows(prev);
     __syncthreads();
     if (tile + (int)gridDim.x < total) fetch(tile + gridDim.x);
 
@@ -580,32 +595,25 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
       }
     }
     __syncthreads();
-    f32x16 res[kP3 / 32];
 #pragma unroll
     for (int nt = 0; nt < kP3 / 32; ++nt) {
       f32x16 acc = zero16();
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) acc = mfma32(frag(xo, kLdsRow, nt * 32, ks), wo[ks], acc);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) res[nt][r] = rbf(acc[r] + bo);
+      for (int r = 0; r < 16; ++r) ybuf[(nt * 32 + drow(r, l)) * kYRow + ch] = rbf(acc[r] + bo);
     }
-    __syncthreads();  // xg / xo are dead; ybuf aliases them
-#pragma unroll
-    for (int nt = 0; nt < kP3 / 32; ++nt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) ybuf[(nt * 32 + drow(r, l)) * kYRow + ch] = res[nt][r];
     __syncthreads();
+    if (out_mode == kOutResidual || (out_mode == kOutAccumulate && x_in_regs)) {
 #pragma unroll
-    for (int u = 0; u < kRowsPer; ++u) {
-      const int p = hw + 8 * u, j = j0 + p;
-      if (j < n) {
-        const f32x4 y = *(const f32x4*)(ybuf + p * kYRow + 4 * hl);
-        const int64_t pair = starting ? (int64_t)i * n + j : (int64_t)j * n + i;
-        store_row4(out, pair * kC + 4 * hl, y, xc[u], out_mode, x_in_regs);
+      for (int u = 0; u < kRowsPer; ++u) {
+        f32x4* row = (f32x4*)(ybuf + (hw + 8 * u) * kYRow + 4 * hl);
+        *row = xc[u] + *row;
       }
     }
-    __syncthreads();
+    prev = tile;
   }
+  if (prev >= 0) store_rows(prev);
 }
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }

@@ -150,25 +150,43 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
 // Batched NT GEMM over channels: O_c[m][n] = sum_k A_c[m][k] * B_c[n][k].
 // Operand tiles are copied global -> LDS by the DMA path (global_load_lds,
 // 1 KB per wave instruction, lane l to byte 16 l), so the LDS tiles are dense
-// rows of BK bf16 with 16-byte chunks XOR-swizzled by (row / 2) % 8: the
-// fragment reads of 16 consecutive rows hit 16 distinct 4-bank groups.  The
-// DMA of stage k+1 runs during stage k's MFMAs with no staging registers.
+// rows of BK bf16 whose 16-byte chunks are XOR-swizzled by row: the fragment
+// reads of 16 consecutive rows hit 16 distinct 4-bank groups.  NS stage
+// buffers form a ring; the DMA of stage k + NS - 1 is issued while stage k is
+// multiplied, so HBM / L2 latency is covered by NS - 1 stages of MFMA work
+// and no staging registers are needed.  The MFMA computes D[n][m] (B as the
+// A operand), so a lane holds 4 consecutive n of one row m: the result goes
+// through LDS with 8-byte writes and leaves as 16-byte row stores.
 __device__ __forceinline__ void lds_dma16(const void* src, unsigned lds_addr) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
+// s_waitcnt vmcnt(n) with the other counters left open (n < 16).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int NS>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_kernel(
     const bf16* __restrict__ A, const bf16* __restrict__ B, bf16* __restrict__ O, int np, int tiles_n,
     int tiles_per_ch) {
   constexpr int kWavesN = BN / WN;
   constexpr int kWaves = (BM / WM) * kWavesN;
   constexpr int kMi = WM / 32, kNi = WN / 32;
-  static_assert(BK == 64, "one LDS row is 8 chunks of 16 bytes");
+  constexpr int kCpr = BK / 8;                    // 16-byte chunks per tile row
+  constexpr int kRpi = 1024 / (BK * 2);           // tile rows per DMA instruction
+  constexpr int kSwz = 16 / kCpr;                 // rows per swizzle step
+  static_assert(BK == 32 || BK == 64, "tile rows of 4 or 8 chunks");
   constexpr int kTileA = BM * BK * 2, kTileB = BN * BK * 2, kStage = kTileA + kTileB;
   constexpr int kDmaA = kTileA / 1024 / kWaves, kDmaB = kTileB / 1024 / kWaves;  // wave instructions per stage
+  constexpr int kDma = kDmaA + kDmaB;
   static_assert(kDmaA * kWaves * 1024 == kTileA && kDmaB * kWaves * 1024 == kTileB, "tile/wave mismatch");
-  __shared__ __attribute__((aligned(16))) char smem[2 * kStage];
+  static_assert(kDma * (NS - 2) < 16, "vmcnt immediate");
+  constexpr int kORow = BN * 2 + 16;              // output staging row (bytes)
+  constexpr int kSmem = NS * kStage > BM * kORow ? NS * kStage : BM * kORow;
+  __shared__ __attribute__((aligned(16))) char smem[kSmem];
 
   // Blocks are dispatched round-robin over the 8 XCDs; give every XCD whole
   // channels so the channel's operand planes stay in that XCD's L2.
@@ -185,16 +203,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
   const int wm0 = (wv / kWavesN) * WM, wn0 = (wv % kWavesN) * WN;
   const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
 
-  // DMA instruction u of this wave copies tile rows 8 q .. 8 q + 7 (q = wave
-  // + kWaves u): lane l -> row 8 q + l / 8, stored chunk l % 8 holding k-chunk
-  // (l % 8) ^ ((row / 2) % 8).
+  // DMA instruction u of this wave copies tile rows kRpi q .. kRpi q + kRpi - 1
+  // (q = wave + kWaves u): lane l -> row kRpi q + l / kCpr, stored chunk
+  // l % kCpr holding k-chunk (l % kCpr) ^ ((row / kSwz) % kCpr).
   auto dma_stage = [&](int k0, int buf) {
     const unsigned base = lds0 + buf * kStage;
 #pragma unroll
-    for (int u = 0; u < kDmaA + kDmaB; ++u) {
+    for (int u = 0; u < kDma; ++u) {
       const bool is_a = u < kDmaA;
       const int q = wv + kWaves * (is_a ? u : u - kDmaA);
-      const int row = 8 * q + (l >> 3), chunk = (l & 7) ^ ((row >> 1) & 7);
+      const int row = kRpi * q + l / kCpr, chunk = (l % kCpr) ^ ((row / kSwz) % kCpr);
       const bf16* src = (is_a ? Ac : Bc) + (int64_t)row * np + k0 + 8 * chunk;
       lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (is_a ? 0 : kTileA) + 1024 * q));
     }
@@ -202,7 +220,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
   // Fragment (row0 + l % 32, k-step ks) of a tile at byte offset tile_off.
   auto sfrag = [&](const char* sb, int tile_off, int row0, int ks) -> bf16x8 {
     const int row = row0 + (l & 31), chunk = 2 * ks + (l >> 5);
-    return *(const bf16x8*)(sb + tile_off + row * (BK * 2) + ((chunk ^ ((row >> 1) & 7)) * 16));
+    return *(const bf16x8*)(sb + tile_off + row * (BK * 2) + ((chunk ^ ((row / kSwz) % kCpr)) * 16));
   };
 
   f32x16 acc[kMi][kNi];
@@ -211,14 +229,20 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
 #pragma unroll
     for (int j = 0; j < kNi; ++j) acc[i][j] = zero16();
 
-  const int kt_count = np / BK;
-  dma_stage(0, 0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's DMAs
-  __syncthreads();
+  const int kt_count = np / BK;  // >= NS - 1: np is a multiple of 256
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) dma_stage(s * BK, s);
   for (int kt = 0; kt < kt_count; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < kt_count) dma_stage((kt + 1) * BK, cur ^ 1);
-    const char* sb = smem + cur * kStage;
+    // Stage kt has landed once at most (stages issued after it) x kDma of
+    // this wave's DMAs are outstanding; the barrier publishes every wave's.
+    const int after = kt_count - 1 - kt < NS - 2 ? kt_count - 1 - kt : NS - 2;
+    if (NS >= 3 && after == 1) wait_vm<(NS >= 3 ? kDma : 0)>();
+    else if (NS >= 4 && after == 2) wait_vm<(NS >= 4 ? 2 * kDma : 0)>();
+    else if (NS >= 5 && after == 3) wait_vm<(NS >= 5 ? 3 * kDma : 0)>();
+    else if (after == 0) wait_vm<0>();
+    __syncthreads();  // stage kt visible; stage kt - 1's buffer is free
+    if (kt + NS - 1 < kt_count) dma_stage((kt + NS - 1) * BK, (kt + NS - 1) % NS);
+    const char* sb = smem + (kt % NS) * kStage;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8 af[kMi], bfr[kNi];
@@ -229,23 +253,32 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
 #pragma unroll
       for (int i = 0; i < kMi; ++i)
 #pragma unroll
-        for (int j = 0; j < kNi; ++j) acc[i][j] = mfma32(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < kNi; ++j) acc[i][j] = mfma32(bfr[j], af[i], acc[i][j]);
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // the next stage's DMAs
-    __syncthreads();
   }
+  __syncthreads();  // every wave is done with the stage buffers
 
-  bf16* Oc = O + c * plane + (int64_t)(tm * BM) * np + tn * BN;
+  // acc[i][j] = D[n][m]: lane -> m = wm0 + 32 i + l%32, registers 4q'..4q'+3 ->
+  // n = wn0 + 32 j + 8q' + 4(l/32) + 0..3, written as one 8-byte LDS store.
 #pragma unroll
   for (int i = 0; i < kMi; ++i)
 #pragma unroll
     for (int j = 0; j < kNi; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        int m = wm0 + 32 * i + drow(r, l);
-        int nn = wn0 + 32 * j + (l & 31);
-        Oc[(int64_t)m * np + nn] = (bf16)acc[i][j][r];
+      for (int q = 0; q < 4; ++q) {
+        const int m = wm0 + 32 * i + (l & 31), nn = wn0 + 32 * j + 8 * q + 4 * (l >> 5);
+        const bf16x4 v = {(bf16)acc[i][j][4 * q], (bf16)acc[i][j][4 * q + 1], (bf16)acc[i][j][4 * q + 2],
+                          (bf16)acc[i][j][4 * q + 3]};
+        *(bf16x4*)(smem + m * kORow + nn * 2) = v;
       }
+  __syncthreads();
+  bf16* Oc = O + c * plane + (int64_t)(tm * BM) * np + tn * BN;
+  constexpr int kChunksRow = BN * 2 / 16;
+#pragma unroll 4
+  for (int e = t; e < BM * kChunksRow; e += kWaves * 64) {
+    const int m = e / kChunksRow, ch = e % kChunksRow;
+    *(bf16x8*)(Oc + (int64_t)m * np + 8 * ch) = *(const bf16x8*)(smem + m * kORow + 16 * ch);
+  }
 }
 
 // ------------------------------------------------------------------ K3
@@ -447,10 +480,13 @@ int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, c
     if (int rc = check_launch("trimul_proj")) return rc;
   }
   if (stages & 2) {
-    constexpr int BM = 256, BN = 256, BK = 64, WM = 64, WN = 128;
+    // Two 64-deep stages: 32-deep stages in a 3- or 4-stage ring measured
+    // slower (more barriers per k), as did register staging of the operands.
+    constexpr int BM = 256, BN = 256, BK = 64, WM = 64, WN = 128, NS = 2;
     const int tiles_n = np / BN, tiles_per_ch = (np / BM) * tiles_n;
-    trimul_contract_kernel<BM, BN, BK, WM, WN><<<dim3(kC * tiles_per_ch), (BM / WM) * (BN / WN) * 64, 0, stream>>>(
-        a_pl, b_pl, o_pl, np, tiles_n, tiles_per_ch);
+    trimul_contract_kernel<BM, BN, BK, WM, WN, NS>
+        <<<dim3(kC * tiles_per_ch), (BM / WM) * (BN / WN) * 64, 0, stream>>>(a_pl, b_pl, o_pl, np, tiles_n,
+                                                                             tiles_per_ch);
     if (int rc = check_launch("trimul_contract")) return rc;
   }
   if (stages & 4) {
