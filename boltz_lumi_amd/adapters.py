@@ -14,8 +14,10 @@ Patched (class name, path rule -> replacement):
   Transition named "*.transition_z"                -> pair_transition.transition_forward
   AdaLN / ConditionedTransitionBlock under
       "structure_module.score_model."              -> diffusion.adaln_forward / transition_forward
-Out of scope (left to upstream): token-transformer AttentionPairBias and the
-``structure_module.sample`` wrapper (reference adapters.py:39-46).
+  AttentionPairBias under
+      "structure_module.score_model.token_transformer."
+                                                   -> pair_bias.prepared_forward
+  structure_module.sample                          -> diffusion.optimized_sample
 """
 
 from __future__ import annotations
@@ -27,6 +29,7 @@ from ._guards import gfx950_available
 TRIANGLE_ATTENTION = {"TriangleAttention", "TriangleAttentionEndingNode"}
 TRIANGLE_MULTIPLICATION = {"TriangleMultiplicationIncoming", "TriangleMultiplicationOutgoing"}
 SCORE_MODEL = "structure_module.score_model."
+TOKEN_TRANSFORMER = SCORE_MODEL + "token_transformer."
 
 FLAG = "_bmx_optimized"
 
@@ -50,8 +53,9 @@ def install(model, *, require_boltz2: bool = True, require_device: bool = True):
     from . import _native
 
     _native.lib()  # fail loudly here, not inside the first forward
-    from .diffusion import adaln_forward, transition_forward
+    from .diffusion import adaln_forward, optimized_sample, transition_forward
     from .multiplication import normalized_forward
+    from .pair_bias import prepared_forward
     from .pair_transition import transition_forward as pair_transition_forward
     from .triangle import contiguous_mask_chunk, normalization_forward, triangle_attention_forward
 
@@ -76,6 +80,13 @@ def install(model, *, require_boltz2: bool = True, require_device: bool = True):
         elif name.startswith(SCORE_MODEL) and cls == "ConditionedTransitionBlock":
             module.forward = MethodType(transition_forward, module)
             patched += 1
+        elif name.startswith(TOKEN_TRANSFORMER) and cls == "AttentionPairBias":
+            module.forward = MethodType(prepared_forward, module)
+            patched += 1
+    structure = getattr(model, "structure_module", None)
+    if structure is not None and hasattr(type(structure), "sample"):
+        structure.sample = MethodType(optimized_sample, structure)
+        patched += 1
     setattr(model, FLAG, True)
     return patched
 
@@ -84,7 +95,8 @@ def uninstall(model) -> int:
     """Remove the instance-level patches installed by :func:`install`."""
     removed = 0
     for _, module in model.named_modules():
-        for owner, attr in ((module, "forward"), (module, "_chunk"), (getattr(module, "layer_norm", None), "forward")):
+        for owner, attr in ((module, "forward"), (module, "_chunk"), (module, "sample"),
+                            (getattr(module, "layer_norm", None), "forward")):
             if owner is not None and attr in vars(owner) and isinstance(vars(owner)[attr], MethodType):
                 if vars(owner)[attr].__func__.__module__.startswith(__package__):
                     del owner.__dict__[attr]

@@ -69,47 +69,53 @@ __global__ __launch_bounds__(256) void pair_bias_kernel(const TIn* __restrict__ 
 }
 
 // ------------------------------------------------------------------
-// Pair-biased attention of the sequence stack, fp32, one pass:
-//   out[i][h*24+d] = sigmoid(g[i][h*24+d]) * sum_j softmax_j(q_i.k_j / sqrt(24) + bias[h][i][j]
-//                                                            + (1 - mask[j]) * -inf) v_j[d]
-// (upstream AttentionPairBias, math as pair_bias.py:21-36; the [16, N, N]
-// logits never reach HBM).
+// Pair-biased attention of AttentionPairBias, fp32, one pass:
+//   out[i][h*D+d] = sigmoid(g[i][h*D+d]) * sum_j softmax_j(q_i.k_j / sqrt(D) + bias[h][i][j]
+//                                                          + (1 - mask[j]) * -inf) v_j[d]
+// for D = 24 (Pairformer sequence stack, 16 x 24) or 48 (diffusion token
+// transformer, 16 x 48); upstream AttentionPairBias, math as
+// pair_bias.py:21-36; the [H, N, N] logits never reach HBM.
 //
 // Both products run on fp32 MFMA (v_mfma_f32_16x16x4f32; lane l, group
 // gi = l / 16: A holds A[l%16][k = gi], B holds B[k = gi][l%16], D register r
 // holds D[4 gi + r][l%16]).  A block owns 16 queries of one head; its 4 waves
 // split the keys (wave w takes the 64-key steps w, w + 4, ...) and merge
 // their softmax states through LDS at the end.  Per 16-key tile:
-//   S[key][q]   = K Q^T        A = K rows, B = Q^T; the 24 head dims are
-//                              the k index 6 gi + s of six MFMA steps;
+//   S[key][q]   = K Q^T        A = K rows, B = Q^T; the D head dims are the
+//                              k index (D/4) gi + s of D/4 MFMA steps;
 //   O^T[d][q]  += V^T P^T      B = P^T is the S tile itself (register s of
 //                              lane (q, gi) is key 4 gi + s, the k index of
-//                              step s), A = V^T in two 16-row d tiles (rows
-//                              24..31 are zero).
+//                              step s), A = V^T in ceil(D/16) 16-row d tiles
+//                              (rows past D are zero).
 // Every lane then holds whole columns (one query) of S and O^T, so the
 // running max and the rescale need only the xor-16 / xor-32 exchanges.
-constexpr int kAttnD = 24, kAttnQ = 16, kAttnWaves = 4, kAttnStep = 64;
+constexpr int kAttnQ = 16, kAttnWaves = 4, kAttnStep = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
+template <int D>
 __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                             const float* __restrict__ v,
                                                             const float* __restrict__ bias,
                                                             const float* __restrict__ mask,
-                                                            const float* __restrict__ g, int n, int64_t ld,
+                                                            const float* __restrict__ g, int n, int64_t ld, int heads,
                                                             float inf, float rscale, bool vec,
                                                             float* __restrict__ out) {
-  constexpr int D = kAttnD, HD = kHeads * D;
-  __shared__ float part_o[kAttnWaves][32][kAttnQ];
+  constexpr int KS = D / 4;          // QK^T MFMA steps
+  constexpr int DT = (D + 15) / 16;  // O^T d tiles
+  static_assert(D % 4 == 0, "head dim");
+  const int HD = heads * D;
+  __shared__ float part_o[kAttnWaves][16 * DT][kAttnQ];
   __shared__ float part_m[kAttnWaves][kAttnQ], part_l[kAttnWaves][kAttnQ];
   const int h = blockIdx.y, q0 = blockIdx.x * kAttnQ;
   const int w = threadIdx.x >> 6, l = lane_id(), gi = l >> 4, c = l & 15;
   const int qc = min(q0 + c, n - 1);  // rows past the end re-read the last one and are not stored
-  float qf[6];
+  float qf[KS];
 #pragma unroll
-  for (int s = 0; s < 6; ++s) qf[s] = q[(int64_t)qc * ld + h * D + 6 * gi + s];
+  for (int s = 0; s < KS; ++s) qf[s] = q[(int64_t)qc * ld + h * D + KS * gi + s];
   const float* brow = bias + ((int64_t)h * n + qc) * n;
-  const int dv1 = 16 + (c & 7);  // second d tile: rows 16..23 real, 24..31 zero
-  f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = o0;
+  f32x4 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -3.4e38f, lsum = 0.f;
   for (int key0 = w * kAttnStep; key0 < n; key0 += kAttnWaves * kAttnStep) {
     const bool full = vec && key0 + kAttnStep <= n;
@@ -118,10 +124,10 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int kr = min(key0 + 16 * t + c, n - 1);
-      const float* krow = k + (int64_t)kr * ld + h * D + 6 * gi;
+      const float* krow = k + (int64_t)kr * ld + h * D + KS * gi;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 6; ++s) acc = mfma16f32(krow[s], qf[s], acc);
+      for (int s = 0; s < KS; ++s) acc = mfma16f32(krow[s], qf[s], acc);
       const int kb = key0 + 16 * t + 4 * gi;  // this lane's keys kb .. kb + 3
       f32x4 b4, m4;
       if (full) {
@@ -146,7 +152,7 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
     m = mn;
     lsum *= alpha;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) o0[r] *= alpha, o1[r] *= alpha;
+    for (int t = 0; t < DT; ++t) o[t] *= alpha;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -155,23 +161,25 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
         lsum += p;
         const int kr = min(key0 + 16 * t + 4 * gi + s, n - 1);
         const float* vrow = v + (int64_t)kr * ld + h * D;
-        const float a1 = vrow[dv1];
-        o0 = mfma16f32(vrow[c], p, o0);
-        o1 = mfma16f32(c < 8 ? a1 : 0.f, p, o1);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int d = 16 * dt + c;
+          const float a = vrow[d < D ? d : D - 1];  // clamped load, zero row past D
+          o[dt] = mfma16f32(d < D ? a : 0.f, p, o[dt]);
+        }
       }
     }
   }
-  // This wave's state for its 16 queries: O^T rows 4 gi + r (tile 0) and
-  // 16 + 4 gi + r (tile 1), the max m, and the key sum over the four lane groups.
+  // This wave's state for its 16 queries: O^T rows 16 dt + 4 gi + r, the max
+  // m, and the key sum over the four lane groups.
   lsum = col_sum(lsum);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    part_o[w][4 * gi + r][c] = o0[r];
-    part_o[w][16 + 4 * gi + r][c] = o1[r];
-  }
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part_o[w][16 * dt + 4 * gi + r][c] = o[dt][r];
   if (gi == 0) part_m[w][c] = m, part_l[w][c] = lsum;
   __syncthreads();
-  // Merge: thread (query qi, dim group) finishes 24 / 16 dims per 16 threads.
+  // Merge: thread (query qi, dim group) finishes D / 16 dims per 16 threads.
   const int qi = threadIdx.x & 15, i = q0 + qi;
   if (i < n) {
     float mm = part_m[0][qi];
@@ -219,17 +227,20 @@ int bmx_seq_attention_fwd(const float* q, const float* k, const float* v, const 
                           const float* g, int64_t n, int64_t ld, int heads, int head_dim, float inf, float* out,
                           hipStream_t stream) {
   BMX_REQUIRE(n >= 0 && n <= (1 << 20), "bmx_seq_attention_fwd: n must be in [0, 2^20]");
-  BMX_REQUIRE(heads == kHeads && head_dim == kAttnD, "bmx_seq_attention_fwd: built for %d heads x %d dims (got %d x %d)",
-              kHeads, kAttnD, heads, head_dim);
-  BMX_REQUIRE(ld >= kHeads * kAttnD, "bmx_seq_attention_fwd: row stride ld must be >= %d", kHeads * kAttnD);
+  BMX_REQUIRE(head_dim == 24 || head_dim == 48, "bmx_seq_attention_fwd: head_dim must be 24 or 48 (got %d)", head_dim);
+  BMX_REQUIRE(heads >= 1 && heads <= 64, "bmx_seq_attention_fwd: heads must be in [1, 64] (got %d)", heads);
+  BMX_REQUIRE(ld >= (int64_t)heads * head_dim, "bmx_seq_attention_fwd: row stride ld must be >= heads * head_dim");
   BMX_REQUIRE(inf > 0.f, "bmx_seq_attention_fwd: inf must be positive");
   if (n == 0) return BMX_OK;
   BMX_REQUIRE(q && k && v && bias && mask && g && out, "bmx_seq_attention_fwd: null pointer");
   // 16-byte bias / mask loads where every row start is aligned; scalar loads otherwise
   const bool vec = n % 4 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)mask % 16 == 0;
-  const dim3 grid((unsigned)((n + kAttnQ - 1) / kAttnQ), kHeads);
-  seq_attention_kernel<<<grid, 256, 0, stream>>>(q, k, v, bias, mask, g, (int)n, ld, inf, 1.f / sqrtf((float)kAttnD),
-                                                 vec, out);
+  const dim3 grid((unsigned)((n + kAttnQ - 1) / kAttnQ), (unsigned)heads);
+  const float rscale = 1.f / sqrtf((float)head_dim);
+  if (head_dim == 24)
+    seq_attention_kernel<24><<<grid, 256, 0, stream>>>(q, k, v, bias, mask, g, (int)n, ld, heads, inf, rscale, vec, out);
+  else
+    seq_attention_kernel<48><<<grid, 256, 0, stream>>>(q, k, v, bias, mask, g, (int)n, ld, heads, inf, rscale, vec, out);
   return check_launch("bmx_seq_attention_fwd");
 }
 

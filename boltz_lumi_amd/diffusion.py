@@ -1,8 +1,9 @@
-"""Diffusion AdaLN / conditioned-transition forwards patched onto the score model.
+"""Diffusion AdaLN / conditioned-transition forwards patched onto the score
+model, and the ``structure_module.sample`` wrapper.
 
-Reference: src/boltz_lumi/diffusion.py (adaln_forward :52-57,
-transition_forward :60-68, eligibility :37-49).  As in the reference these
-run in fp32 with autocast off.  AdaLN's a_norm + sigmoid(s_scale) modulation
+Reference: src/boltz_lumi/diffusion.py (optimized_sample :13-23, adaln_forward
+:52-57, transition_forward :60-68, eligibility :37-49).  As in the reference the
+AdaLN / transition forwards run in fp32 with autocast off.  AdaLN's a_norm + sigmoid(s_scale) modulation
 + s_bias become one LN/modulate kernel; the SwiGLU gate and the output gate
 are fused epilogues.  The conditioning projections are still called as
 submodules, so ``atom_conditioning_cache`` keeps working (reference
@@ -11,10 +12,31 @@ atom_conditioning.py:12-45).  Guard failures call the class forward.
 
 from __future__ import annotations
 
+from contextlib import nullcontext
+
 import torch
 
 from . import ops
 from ._guards import autocast_off, gfx950_tensor, inference
+from .atom_conditioning import atom_conditioning_cache
+from .pair_bias import prepare_token_bias
+
+
+def optimized_sample(self, *args, **kwargs):
+    """Drop-in for ``AtomDiffusion.sample`` (reference diffusion.py:13-23): in
+    inference the token transformer's fixed bias is packed head-major once
+    (``prepare_token_bias``, so each layer's attention reads a dense slice),
+    and with one sample of one structure the atom conditioning projections are
+    memoised for the call (``atom_conditioning_cache``)."""
+    sample = type(self).sample
+    if torch.is_grad_enabled() or self.training or "diffusion_conditioning" not in kwargs:
+        return sample(self, *args, **kwargs)
+    conditioning = dict(kwargs["diffusion_conditioning"])
+    conditioning["token_trans_bias"] = prepare_token_bias(conditioning["token_trans_bias"])
+    kwargs["diffusion_conditioning"] = conditioning
+    single = kwargs.get("multiplicity", 1) == 1 and conditioning["c"].shape[0] == 1
+    with atom_conditioning_cache(self.score_model) if single else nullcontext():
+        return sample(self, *args, **kwargs)
 
 
 def eligible(module, *tensors) -> bool:

@@ -21,6 +21,7 @@ from torch import nn
 import torch.nn.functional as F
 
 from . import ops
+from .pair_bias import fused_attention
 
 
 def _require_cuda(x: torch.Tensor, what: str) -> None:
@@ -195,31 +196,13 @@ class AttentionPairBias(nn.Module):
                 and self.proj_z[1].weight.shape == (16, 128))
 
     def attend(self, s, z, mask, k_in, multiplicity=1, bias=None):
-        """``g * attention`` before ``proj_o`` ([B, N, c_s]) from the fused
-        gfx950 kernel, or None where it does not apply (CPU, grad, another
-        head shape or dtype).  With ``k_in is s`` the four input projections
-        run as one GEMM whose column slices the kernel reads in place.
+        """``g * attention`` before ``proj_o`` from the fused kernel
+        (``pair_bias.fused_attention``), or None where it does not apply.
         ``bias``, when given, is ``pair_bias(z)`` computed already."""
-        if not (s.is_cuda and s.dtype == torch.float32 and k_in.dtype == torch.float32 and self.num_heads == 16
-                and self.head_dim == 24 and not torch.is_grad_enabled()):
-            return None
-        if k_in is s:
-            w = ops.cached_weight(self, "qkvg", (self.proj_q.weight, self.proj_k.weight, self.proj_v.weight,
-                                                 self.proj_g.weight), lambda *ws: torch.cat(ws, 0).float())
-            bq = ops.cached_weight(self, "qkvg_bias", (self.proj_q.bias,),
-                                   lambda b: torch.cat([b.float(), b.new_zeros(3 * self.c_s)]))
-            proj = F.linear(s, w, bq)
-            q, k, v, g = proj.split(self.c_s, dim=-1)
-        else:
-            q, k, v, g = self.proj_q(s), self.proj_k(k_in), self.proj_v(k_in), self.proj_g(s)
-        bias = self.pair_bias(z).float() if bias is None else bias
-        m = mask.float()
-        o = torch.empty(s.shape[:-1] + (self.c_s,), device=s.device, dtype=torch.float32)
-        for i in range(s.shape[0]):
-            # the bias of batch element i // multiplicity (upstream repeat_interleave)
-            ops.seq_attention(q[i], k[i], v[i], bias[i // multiplicity].contiguous(), m[i].contiguous(), g[i],
-                              self.inf, out=o[i])
-        return o
+        if (bias is None and s.is_cuda and self.head_dim in (24, 48) and not torch.is_grad_enabled()
+                and not self.training):
+            bias = self.pair_bias(z)
+        return fused_attention(self, s, z, mask, k_in, multiplicity, bias)
 
     def forward(self, s, z, mask, k_in, multiplicity=1):
         o = self.attend(s, z, mask, k_in, multiplicity)

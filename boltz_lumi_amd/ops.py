@@ -419,27 +419,30 @@ def pair_bias(proj_z_norm, proj_z_linear, z, out=None):
 
 
 def seq_attention(q, k, v, bias, mask, g, inf, out=None):
-    """Pair-biased softmax attention of the sequence stack, fp32, for one batch
-    element: q, k, v and the gate logits g are [N, 384] (16 heads x 24) with
+    """Pair-biased softmax attention of AttentionPairBias, fp32, for one batch
+    element: q, k, v and the gate logits g are [N, H * D] (D = 24 or 48) with
     unit column stride and one common row stride (e.g. column slices of a
-    fused [N, 1536] projection), bias [16, N, N], mask [N].  Returns (or
-    writes into ``out``) ``sigmoid(g) * softmax(q k^T / sqrt(24) + bias +
-    (1 - mask) * -inf) v`` as a contiguous [N, 384]."""
+    fused [N, 4 H D] projection), bias [H, N, N], mask [N].  Returns (or
+    writes into ``out``) ``sigmoid(g) * softmax(q k^T / sqrt(D) + bias +
+    (1 - mask) * -inf) v`` as a contiguous [N, H * D]."""
     _cuda(q, k, v, bias, mask, g)
-    n = q.shape[0]
-    ld = q.stride(0) if n > 1 else 384
+    _check(bias.dim() == 3, "expected a [H, N, N] bias")
+    heads, n = bias.shape[0], q.shape[0]
+    width = q.shape[1] if q.dim() == 2 else -1
+    _check(width > 0 and width % heads == 0 and width // heads in (24, 48), "expected H heads of 24 or 48 dims")
+    ld = q.stride(0) if n > 1 else width
     for t in (q, k, v, g):
-        _check(t.shape == (n, 384) and t.dtype == torch.float32 and t.stride(1) == 1
-               and (n <= 1 or t.stride(0) == ld), "expected fp32 [N, 384] q / k / v / g with one row stride")
-    _check(bias.shape == (16, n, n) and bias.dtype == torch.float32 and bias.is_contiguous(),
-           "expected a contiguous fp32 [16, N, N] bias")
+        _check(t.shape == (n, width) and t.dtype == torch.float32 and t.stride(1) == 1
+               and (n <= 1 or t.stride(0) == ld), "expected fp32 [N, H * D] q / k / v / g with one row stride")
+    _check(bias.shape == (heads, n, n) and bias.dtype == torch.float32 and bias.is_contiguous(),
+           "expected a contiguous fp32 [H, N, N] bias")
     _check(mask.shape == (n,) and mask.dtype == torch.float32 and mask.is_contiguous(), "expected an fp32 [N] mask")
     if out is None:
-        out = torch.empty((n, 384), device=q.device, dtype=torch.float32)
-    _check(out.shape == (n, 384) and out.dtype == torch.float32 and out.is_contiguous(),
-           "out must be a contiguous fp32 [N, 384]")
+        out = torch.empty((n, width), device=q.device, dtype=torch.float32)
+    _check(out.shape == (n, width) and out.dtype == torch.float32 and out.is_contiguous(),
+           "out must be a contiguous fp32 [N, H * D]")
     N.call("bmx_seq_attention_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), mask.data_ptr(),
-           g.data_ptr(), n, ld, 16, 24, float(inf), out.data_ptr(), _stream(q))
+           g.data_ptr(), n, ld, heads, width // heads, float(inf), out.data_ptr(), _stream(q))
     return out
 
 

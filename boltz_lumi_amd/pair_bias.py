@@ -1,0 +1,79 @@
+"""AttentionPairBias on gfx950: the fused pair-biased attention and the
+dense token-transformer bias storage.
+
+Reference: src/boltz_lumi/pair_bias.py.
+  prepare_token_bias (:6-13)  packs the diffusion token transformer's fixed
+                              [B, Q, K, layers * heads] bias so that every
+                              layer's [B, heads, Q, K] slice is dense.
+  prepared_forward (:15-36)   the token transformer's AttentionPairBias
+                              forward (installed at adapters.py:39-42).
+Here the logits / softmax / PV / gate part of both the token transformer's
+and the Pairformer trunk's AttentionPairBias runs as one kernel
+(``bmx_seq_attention_fwd``, 16 heads of 24 or 48 dims): the [B, H, N, N]
+logits never exist in HBM.  Projections stay on hipBLASLt; with
+``k_in is s`` the four input projections are one GEMM whose column slices the
+kernel reads in place.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import ops
+
+
+def prepare_token_bias(value: torch.Tensor) -> torch.Tensor:
+    """The same logical [B, Q, K, L*H] tensor (values unchanged, fp32) stored
+    head-major, so ``value[..., l*H:(l+1)*H].movedim(-1, 1)`` is dense per batch
+    element (reference pair_bias.py:6-13)."""
+    dense = torch.empty((value.shape[0], value.shape[3], value.shape[1], value.shape[2]), device=value.device,
+                        dtype=torch.float32)
+    dense.copy_(value.movedim(-1, 1))
+    return dense.movedim(1, -1)
+
+
+def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
+    """``sigmoid(proj_g(s)) * attention`` of an upstream-style AttentionPairBias
+    ``module`` before ``proj_o`` ([B, N, c_s], fp32), or None where the kernel
+    does not apply (CPU, grad, training, a head width other than 24 or 48).
+
+    ``bias`` is ``module.proj_z(z)`` ([B, H, N, N]) when not given; batch
+    element i uses bias ``i // multiplicity`` (upstream ``repeat_interleave``,
+    pair_bias.py:26-27).  Under autocast the projections run in its dtype and
+    are widened to fp32 for the attention, as upstream does (:29-33)."""
+    heads, width = module.num_heads, module.c_s
+    if not (s.is_cuda and k_in.is_cuda and width % heads == 0 and width // heads in (24, 48) and heads <= 64
+            and not module.training and not torch.is_grad_enabled()):
+        return None
+    if k_in is s:
+        w = ops.cached_weight(module, "qkvg", (module.proj_q.weight, module.proj_k.weight, module.proj_v.weight,
+                                               module.proj_g.weight), lambda *ws: torch.cat(ws, 0).float())
+        bq = ops.cached_weight(module, "qkvg_bias", (module.proj_q.bias,),
+                               lambda b: torch.cat([b.float(), b.new_zeros(3 * width)]))
+        proj = F.linear(s if torch.is_autocast_enabled() else s.float(), w, bq).float()
+        q, k, v, g = proj.split(width, dim=-1)
+    else:
+        q, k, v, g = (t.float().contiguous() for t in (module.proj_q(s), module.proj_k(k_in), module.proj_v(k_in),
+                                                        module.proj_g(s)))
+    if bias is None:
+        bias = module.proj_z(z)
+    bias = bias.float()
+    m = mask.float()
+    o = torch.empty(s.shape[:-1] + (width,), device=s.device, dtype=torch.float32)
+    for i in range(s.shape[0]):
+        mi = m[i if m.shape[0] > 1 else 0].contiguous()
+        ops.seq_attention(q[i], k[i], v[i], bias[i // multiplicity].contiguous(), mi, g[i], module.inf, out=o[i])
+    return o
+
+
+def prepared_forward(module, s, z, mask, k_in, multiplicity=1):
+    """Drop-in for the token transformer's ``AttentionPairBias.forward``
+    (reference pair_bias.py:15-36); upstream forward under grad, in training,
+    for ``compute_pair_bias`` modules and where the kernel does not apply."""
+    o = None
+    if not (torch.is_grad_enabled() or module.training or module.compute_pair_bias):
+        o = fused_attention(module, s, z, mask, k_in, multiplicity)
+    if o is None:
+        return type(module).forward(module, s, z, mask, k_in, multiplicity)
+    return module.proj_o(o)

@@ -167,14 +167,16 @@ int bmx_pair_transition_bias_fwd(const void* x, int x_dtype, int64_t rows, const
 int bmx_pair_bias_fwd(const void* z, int z_dtype, int64_t rows, const float* ln_w, const float* ln_b, float eps,
                       const float* w, int heads, float* out, bmx_stream_t stream);
 
-/* out[i][h*24+d] = sigmoid(g[i][h*24+d]) * sum_j softmax_j(q_i.k_j / sqrt(24) + bias[h][i][j]
- *                                                          + (1 - mask[j]) * -inf) v_j[d],  fp32,
- * for heads = 16, head_dim = 24.  q, k, v and the gate logits g are [n] rows of 384 values at
- * row stride ld (>= 384; e.g. column slices of one fused [n, 1536] projection), bias is
- * [16][n][n], mask [n], out [n][384] contiguous.
- * Replaces the logits / softmax / PV / gate part of AttentionPairBias.forward of the
- * sequence stack (math as src/boltz_lumi/pair_bias.py:21-36), which the reference leaves to
- * torch (adapters.py:39-45); the [16, n, n] logits never reach HBM. */
+/* out[i][h*D+d] = sigmoid(g[i][h*D+d]) * sum_j softmax_j(q_i.k_j / sqrt(D) + bias[h][i][j]
+ *                                                      + (1 - mask[j]) * -inf) v_j[d],  fp32,
+ * for head_dim D = 24 (Pairformer sequence stack, 16 x 24) or 48 (diffusion token transformer,
+ * 16 x 48) and 1 <= heads <= 64.  q, k, v and the gate logits g are [n] rows of heads * D values
+ * at row stride ld (>= heads * D; e.g. column slices of one fused [n, 4 * heads * D] projection),
+ * bias is [heads][n][n], mask [n], out [n][heads * D] contiguous.
+ * Replaces the logits / softmax / PV / gate part of AttentionPairBias.forward (math as
+ * src/boltz_lumi/pair_bias.py:21-36): the trunk's sequence stack, which the reference leaves to
+ * torch (adapters.py:39-45), and the token transformer's prepared_forward (pair_bias.py:15-36,
+ * installed at adapters.py:39-42); the [heads, n, n] logits never reach HBM. */
 int bmx_seq_attention_fwd(const float* q, const float* k, const float* v, const float* bias, const float* mask,
                           const float* g, int64_t n, int64_t ld, int heads, int head_dim, float inf, float* out,
                           bmx_stream_t stream);

@@ -15,6 +15,21 @@ from boltz_lumi_amd.atom_conditioning import atom_conditioning_cache
 from oracle import boltz_ref as R
 
 
+class AtomDiffusion(nn.Module):
+    """Stand-in for the structure module: ``sample`` records its keyword arguments."""
+
+    def __init__(self):
+        super().__init__()
+        self.score_model = nn.Module()
+        self.score_model.block = R.ConditionedTransitionBlock(16, 8)
+        self.score_model.token_transformer = nn.Module()
+        self.score_model.token_transformer.layers = nn.ModuleList([R.DiffusionTransformerLayer(2, 48, 8)])
+
+    def sample(self, *args, **kwargs):
+        self.seen = kwargs
+        return "sampled"
+
+
 class Boltz2(nn.Module):
     """Stand-in with the module paths adapters.install walks."""
 
@@ -22,9 +37,7 @@ class Boltz2(nn.Module):
         super().__init__()
         self.pairformer_module = nn.Module()
         self.pairformer_module.layers = nn.ModuleList([R.PairformerLayer(token_s=32, token_z=128, num_heads=4)])
-        self.structure_module = nn.Module()
-        self.structure_module.score_model = nn.Module()
-        self.structure_module.score_model.block = R.ConditionedTransitionBlock(16, 8)
+        self.structure_module = AtomDiffusion()
 
 
 def test_version_pin():
@@ -43,14 +56,46 @@ def test_install_requires_boltz2_and_gfx950():
 def test_install_patches_by_class_and_path_and_is_idempotent():
     model = Boltz2()
     n = adapters.install(model, require_device=False)
-    # tri_mul_out, tri_mul_in, tri_att_start, tri_att_end, transition_z, AdaLN, CTB
-    assert n == 7
+    # tri_mul_out, tri_mul_in, tri_att_start, tri_att_end, transition_z; score model: block (CTB) and its
+    # AdaLN, token-transformer layer's AdaLN, AttentionPairBias, CTB and its AdaLN; structure_module.sample
+    assert n == 12
     layer = model.pairformer_module.layers[0]
     assert "forward" in vars(layer.tri_att_start) and "forward" in vars(layer.tri_att_start.layer_norm)
     assert "forward" in vars(layer.transition_z) and "forward" not in vars(layer.transition_s)
+    assert "forward" not in vars(layer.attention)  # the trunk's AttentionPairBias stays upstream
+    token_layer = model.structure_module.score_model.token_transformer.layers[0]
+    assert "forward" in vars(token_layer.pair_bias_attn) and "sample" in vars(model.structure_module)
     assert adapters.install(model, require_device=False) == 0
-    assert adapters.uninstall(model) >= 7
-    assert "forward" not in vars(layer.tri_att_start)
+    assert adapters.uninstall(model) >= 12
+    assert "forward" not in vars(layer.tri_att_start) and "sample" not in vars(model.structure_module)
+
+
+def test_prepare_token_bias_keeps_values_and_packs_each_layer_densely():
+    from boltz_lumi_amd.pair_bias import prepare_token_bias
+
+    g = torch.Generator().manual_seed(4)
+    bias = torch.randn(2, 5, 7, 3 * 4, generator=g)  # [B, Q, K, layers * heads]
+    packed = prepare_token_bias(bias)
+    assert packed.shape == bias.shape and packed.dtype == torch.float32 and torch.equal(packed, bias)
+    for layer in range(3):
+        per_layer = packed[..., 4 * layer:4 * (layer + 1)].movedim(-1, 1)  # upstream proj_z (Rearrange)
+        assert all(per_layer[b].is_contiguous() for b in range(2))
+    assert torch.equal(prepare_token_bias(bias.bfloat16()), bias.bfloat16().float())
+
+
+def test_sample_wrapper_packs_the_token_bias_and_passes_through_under_grad():
+    model = Boltz2().eval()
+    adapters.install(model, require_device=False)
+    sm = model.structure_module
+    bias = torch.randn(1, 4, 4, 6)
+    cond = {"token_trans_bias": bias, "c": torch.zeros(2, 3)}
+    with torch.no_grad():
+        assert sm.sample(diffusion_conditioning=cond, multiplicity=2) == "sampled"
+    seen = sm.seen["diffusion_conditioning"]["token_trans_bias"]
+    assert torch.equal(seen, bias) and seen.movedim(-1, 1)[0].is_contiguous()
+    assert cond["token_trans_bias"] is bias  # the caller's dict is not modified
+    assert sm.sample(diffusion_conditioning=cond, multiplicity=2) == "sampled"  # grad on: untouched
+    assert sm.seen["diffusion_conditioning"] is cond
 
 
 def test_cpu_tensors_fall_back_to_upstream_exactly():

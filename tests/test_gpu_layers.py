@@ -164,7 +164,7 @@ def test_attention_pair_bias_forward_matches_upstream(gpu, n, same_k, multiplici
         want = ref(s, z, mask, k_in, multiplicity=multiplicity)
     mine = layers.AttentionPairBias(384, 128, 16)
     mine.load_state_dict(ref.state_dict())
-    mine = mine.to(gpu)
+    mine = mine.to(gpu).eval()
     sd = s.to(gpu)
     kd = sd if same_k else k_in.to(gpu)
     with torch.inference_mode():
@@ -185,3 +185,66 @@ def test_transition_residual_matches_upstream(gpu):
     with torch.inference_mode():
         got = t.residual(x.to(gpu))
     assert max_rel(got, want) < 1e-5
+
+
+def _token_bias(g, b, n, layers, heads):
+    """A fixed token-transformer bias [B, N, N, layers * heads], packed as the
+    sample wrapper packs it."""
+    from boltz_lumi_amd.pair_bias import prepare_token_bias
+
+    return prepare_token_bias(torch.randn(b, n, n, layers * heads, generator=g) * 2)
+
+
+@pytest.mark.parametrize("n,multiplicity,autocast", [(200, 2, False), (64, 1, False), (130, 2, True)])
+def test_token_transformer_attention_matches_upstream(gpu, n, multiplicity, autocast):
+    """The token transformer's AttentionPairBias (16 heads x 48, prepacked
+    bias slice of layer 1 of 2) through prepared_forward against the fp32
+    upstream forward: 1e-4 in fp32, 2e-2 under bf16 autocast."""
+    import copy
+
+    from boltz_lumi_amd.pair_bias import prepared_forward
+
+    g = torch.Generator().manual_seed(300 + n)
+    ref = R.randomize(R.AttentionPairBias(768, num_heads=16, compute_pair_bias=False), generator=g).eval()
+    bz = 1
+    s = torch.randn(bz * multiplicity, n, 768, generator=g)
+    bias = _token_bias(g, bz, n, 2, 16)[..., 16:32]
+    mask = torch.ones(bz * multiplicity, n)
+    mask[-1, -9:] = 0
+    with torch.no_grad():
+        want = ref(s, bias, mask, s, multiplicity=multiplicity)
+    mine = copy.deepcopy(ref).to(gpu)
+    sd = s.to(gpu)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        got = prepared_forward(mine, sd, bias.to(gpu), mask.to(gpu), sd, multiplicity)
+    assert max_rel(got.float(), want) < (2e-2 if autocast else 1e-4)
+
+
+def test_token_transformer_attention_falls_back_under_grad(gpu):
+    import copy
+
+    from boltz_lumi_amd.pair_bias import prepared_forward
+
+    g = torch.Generator().manual_seed(9)
+    ref = R.randomize(R.AttentionPairBias(768, num_heads=16, compute_pair_bias=False), generator=g).to(gpu)
+    s = torch.randn(1, 40, 768, generator=g).to(gpu)
+    bias = _token_bias(g, 1, 40, 1, 16).to(gpu)
+    mask = torch.ones(1, 40, device=gpu)
+    want = ref(s, bias, mask, s)
+    got = prepared_forward(copy.deepcopy(ref), s, bias, mask, s)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("heads,n", [(4, 77), (16, 256)])
+def test_seq_attention_head_dim_48_matches_fp64(gpu, heads, n):
+    g = torch.Generator().manual_seed(heads * 1000 + n)
+    width = heads * 48
+    q, k, v, gate = (torch.randn(n, width, generator=g) for _ in range(4))
+    bias = torch.randn(heads, n, n, generator=g)
+    mask = (torch.rand(n, generator=g) > 0.2).float()
+    mask[0] = 1
+    qh, kh, vh = (t.double().view(n, heads, 48).transpose(0, 1) for t in (q, k, v))
+    logits = qh @ kh.transpose(-1, -2) / 48 ** 0.5 + bias.double() + (1 - mask.double()) * -1e6
+    want = torch.sigmoid(gate.double()) * (torch.softmax(logits, -1) @ vh).transpose(0, 1).reshape(n, width)
+    got = ops.seq_attention(*(t.to(gpu) for t in (q, k, v, bias, mask, gate)), 1e6)
+    assert max_rel(got, want) < 1e-4
