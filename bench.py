@@ -37,6 +37,9 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=3, help="repetitions of the per-kernel timing pass")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first copy 1 GiB device-to-device (a kernel of known traffic for scaling PMC byte counters)")
+    p.add_argument("--workload", choices=("pairformer", "token-attention"), default="pairformer",
+                   help="pairformer: the headline PairformerLayer line (default); token-attention: the diffusion "
+                        "token transformer's AttentionPairBias (16 x 48 heads, 5 samples, prepacked bias)")
     return p.parse_args()
 
 
@@ -141,12 +144,105 @@ def cpu_baseline(n: int, seed: int):
     return dt * 1e3, cores
 
 
+PEAK_FP32_TFLOPS = 157.3
+
+
+def token_attention(args):
+    """One token-transformer AttentionPairBias forward (c_s 768, 16 heads x 48)
+    over 5 samples of N tokens sharing one prepacked [1, N, N, 24 * 16] bias
+    (BASELINE configs[4] shape, one of the 24 layers), through the drop-in
+    ``prepared_forward``.  The roofline covers the fused attention kernel: fp32
+    MFMA flops 4 * 16 * 48 * N^2 per sample."""
+    import torch
+    from boltz_lumi_amd import layers, ops
+    from boltz_lumi_amd.pair_bias import prepare_token_bias, prepared_forward
+
+    dev = torch.device("cuda:0")
+    n, samples, heads, width = args.n, 5, 16, 768
+    module = init_weights(layers.AttentionPairBias(width, num_heads=heads, compute_pair_bias=False), 0).to(dev).eval()
+    g = torch.Generator().manual_seed(0)
+    s = torch.randn(samples, n, width, generator=g).to(dev)
+    bias = prepare_token_bias(torch.randn(1, n, n, 24 * heads, generator=g).to(dev))[..., :heads]
+    mask = torch.ones(samples, n, device=dev)
+
+    def step():
+        prepared_forward(module, s, bias, mask, s, multiplicity=samples)
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        # the attention kernel alone, on the same inputs
+        proj = torch.randn(n, 4 * width, generator=g).to(dev)
+        q, k, v, gl = proj.split(width, dim=-1)
+        b0, m0 = bias[0].movedim(-1, 0), mask[0]
+        out = torch.empty(n, width, device=dev)
+        reps = max(args.steps, 10) * samples
+        ops.seq_attention(q, k, v, b0, m0, gl, module.inf, out=out)
+        e0.record()
+        for _ in range(reps):
+            ops.seq_attention(q, k, v, b0, m0, gl, module.inf, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        kms = e0.elapsed_time(e1) / reps
+    flops = 4.0 * heads * 48 * n * n
+    achieved = flops / (kms * 1e-3) / 1e12
+    out_line = {
+        "metric": "token-transformer AttentionPairBias ms @N=1024, 5 samples",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (s ~ N(0,1), bias ~ N(0,1) prepacked, masks ones; weights seed 0)",
+        "config": {"workload": f"diffusion token-transformer AttentionPairBias forward (prepared_forward), "
+                               f"c_s=768, 16 heads x 48, {samples} samples x N={n} (BASELINE configs[4] shape)",
+                   "n_tokens": n, "samples": samples},
+        "roofline": {"kernel": "seq_attention", "bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+                     "traffic": None, "kernel_ms_per_sample": round(kms, 4)},
+    }
+    if not args.no_cpu_baseline:
+        out_line["cpu_baseline"] = token_attention_cpu(min(n, args.cpu_n or n))
+    print(json.dumps(out_line), flush=True)
+
+
+def token_attention_cpu(n: int):
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import boltz_ref as R  # the checker, timed as the reference CPU path
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    module = init_weights(R.AttentionPairBias(768, num_heads=16, compute_pair_bias=False), 0).eval()
+    g = torch.Generator().manual_seed(0)
+    s = torch.randn(1, n, 768, generator=g)
+    bias = torch.randn(1, n, n, 16, generator=g)
+    mask = torch.ones(1, n)
+    with torch.inference_mode():
+        module(s[:, :32], bias[:, :32, :32], mask[:, :32], s[:, :32])
+        t0 = time.perf_counter()
+        module(s, bias, mask, s)
+        dt = time.perf_counter() - t0
+    return {"value": round(dt * 1e3 * 5, 1), "unit": "ms per 5-sample forward (1 sample timed, x5)",
+            "cores": cores, "kind": "port",
+            "sample": f"one sample of the fp32 CPU oracle AttentionPairBias at N={n} (oracle/boltz_ref.py), "
+                      f"{cores} threads, scaled x5"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding of the pair stack is a design note, not built)"}))
         sys.exit(2)
+    if args.workload == "token-attention":
+        return token_attention(args)
     import torch
     from boltz_lumi_amd import layers, ops
 

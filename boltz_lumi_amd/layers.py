@@ -159,6 +159,13 @@ class Transition(nn.Module):
         return torch.addmm(x2, h.reshape(-1, self.hidden), self.fc3.weight.t()).view(x.shape)
 
 
+class _HeadsFirst(nn.Module):
+    """``Rearrange("b ... h -> b h ...")`` of upstream proj_z (parameter-free)."""
+
+    def forward(self, x):
+        return x.movedim(-1, 1)
+
+
 class AttentionPairBias(nn.Module):
     """Upstream ``attentionv2.AttentionPairBias`` (sequence stack, fp32)."""
 
@@ -174,6 +181,8 @@ class AttentionPairBias(nn.Module):
         self.compute_pair_bias = compute_pair_bias
         if compute_pair_bias:
             self.proj_z = nn.Sequential(nn.LayerNorm(c_z), nn.Linear(c_z, num_heads, bias=False))
+        else:
+            self.proj_z = _HeadsFirst()
         self.proj_o = nn.Linear(c_s, c_s, bias=False)
 
     def pair_bias(self, z):
