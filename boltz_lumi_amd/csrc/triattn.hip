@@ -283,12 +283,15 @@ __device__ __forceinline__ void lds_dma16(const void* src, unsigned lds_addr) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
 }
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+__device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
 template <bool MASKED>
 __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0, char* lds) {
   constexpr int G = kRows;
   const int n = L.n, np = L.np;
-  const int t = threadIdx.x, l = lane_id(), g = l >> 4, lq = l & 15, w = t >> 6;
+  // w is wave-uniform: read into an SGPR so that the DMA job set-up and the
+  // LDS (M0) addresses below stay scalar.
+  const int l = lane_id(), g = l >> 4, lq = l & 15, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nk = (n + kKT - 1) / kKT * kKT;
   const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
   const bf16* kb[G];
@@ -308,36 +311,42 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
   // copies its own 16 queries' 4 tiles (2 KB, contiguous in the bias layout).
   // Mask bias: wave 0's first 32 lanes copy 64 keys of both rows.
   static_assert(kCoreWaves == 8 && G == 2, "DMA job split assumes 8 waves and 2 rows");
-  int64_t kv_off[2];
+  // Each source walks forward by one stage per call: K rows by kKT * kD
+  // elements, V^T rows by kKT keys, the bias by 4 key blocks (kKT * 16).
+  const bf16* kv_src[2];
+  int kv_step[2];
   unsigned kv_lds[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const int job = w + 8 * u, r = job >> 3, kind = (job >> 2) & 1, quarter = job & 3;
     if (kind == 0) {
       const int key = 16 * quarter + (l >> 2), c = (l & 3) ^ ((key >> 2) & 3);
-      kv_off[u] = (kb[r] - L.k) + (int64_t)key * kD + 8 * c;
+      kv_src[u] = kb[r] + key * kD + 8 * c;
+      kv_step[u] = kKT * kD;
     } else {
       const int d = 8 * quarter + (l >> 3), c = (l & 7) ^ ((d >> 1) & 7);
-      kv_off[u] = (vb[r] - L.vt) + (int64_t)d * np + 8 * c;
+      kv_src[u] = vb[r] + (int64_t)d * np + 8 * c;
+      kv_step[u] = kKT;
     }
     kv_lds[u] = (kind == 0 ? kOffK : kOffV) + r * kTileBytes + 1024 * quarter;
   }
   const bf16* tb_src = L.tb + tb_offset(np, h, q0, 0) + 8 * l;  // + 256 per 16-key block
   const int i_mb = min(i0 + (l >> 4), n - 1);
   const float* mb_src = L.mb + (int64_t)i_mb * np + 4 * lq;
-  auto dma_stage = [&](int k0, int buf) {
+  auto dma_stage = [&](int buf) {
     const unsigned base = lds0 + buf * kStageBytes;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int job = w + 8 * u, kind = (job >> 2) & 1;
-      const bf16* src = kind == 0 ? L.k + kv_off[u] + (int64_t)k0 * kD : L.vt + kv_off[u] + k0;
-      lds_dma16(src, __builtin_amdgcn_readfirstlane(base + kv_lds[u]));
+      lds_dma16(kv_src[u], __builtin_amdgcn_readfirstlane(base + kv_lds[u]));
+      kv_src[u] += kv_step[u];
     }
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb)
-      lds_dma16(tb_src + 16 * (k0 + 32 * hb),
+      lds_dma16(tb_src + 16 * 32 * hb,
                 __builtin_amdgcn_readfirstlane(base + kOffBias + w * kBiasWaveBytes + 1024 * hb));
-    if (MASKED && w == 0 && l < 32) lds_dma16(mb_src + k0, __builtin_amdgcn_readfirstlane(base + kOffMb));
+    tb_src += 16 * kKT;
+    if (MASKED && w == 0 && l < 32) lds_dma16(mb_src, __builtin_amdgcn_readfirstlane(base + kOffMb));
+    mb_src += kKT;
   };
 
   // O^T tiles (d 0..15, 16..31) and the row sum l, which an MFMA with an
@@ -364,13 +373,13 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
   const int k_rd = kOffK + (4 * lq + (g ^ ((lq >> 2) & 3))) * 16;  // + 1024 j (16 keys) + r tile
   const int b_rd = kOffBias + w * kBiasWaveBytes + 16 * (l & 31);   // + 512 j
 
-  dma_stage(0, 0);
+  dma_stage(0);
   wait_vm0();
   __syncthreads();
   for (int k0 = 0; k0 < nk; k0 += kKT) {
     const int cur = (k0 / kKT) & 1;
     const bool more = k0 + kKT < nk;
-    if (more) dma_stage(k0 + kKT, cur ^ 1);
+    if (more) dma_stage(cur ^ 1);
     const char* sb = lds + cur * kStageBytes;
     // S^T for all rows first, so the scheduler can overlap one row's MFMAs
     // with another row's max / exp work inside one basic block.
@@ -387,12 +396,14 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
         // multiplies by zero (the bias is finite).
         s[r][j] = mfma16(ident, *(const bf16x8*)(sb + b_rd + 512 * j), s[r][j]);
       }
-      // This lane's max over its 16 keys; the max over all keys of a query
-      // (4 lanes) is only needed when some lane crosses the lazy threshold.
-      mt[r] = fmaxf(fmaxf(s[r][0][0], s[r][0][1]), fmaxf(s[r][0][2], s[r][0][3]));
-#pragma unroll
-      for (int j = 1; j < 4; ++j)
-        mt[r] = fmaxf(mt[r], fmaxf(fmaxf(s[r][j][0], s[r][j][1]), fmaxf(s[r][j][2], s[r][j][3])));
+      // This lane's max over its 16 keys (a v_max3 tree: 5 + 2 + 1); the max
+      // over all keys of a query (4 lanes) is only needed when some lane
+      // crosses the lazy threshold.
+      const f32x4* sr = s[r];
+      const float a0 = max3f(sr[0][0], sr[0][1], sr[0][2]), a1 = max3f(sr[0][3], sr[1][0], sr[1][1]);
+      const float a2 = max3f(sr[1][2], sr[1][3], sr[2][0]), a3 = max3f(sr[2][1], sr[2][2], sr[2][3]);
+      const float a4 = max3f(sr[3][0], sr[3][1], sr[3][2]);
+      mt[r] = fmaxf(max3f(a0, a1, a2), max3f(a3, a4, sr[3][3]));
     }
     bool grow = false;
 #pragma unroll
