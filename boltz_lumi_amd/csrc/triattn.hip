@@ -285,8 +285,15 @@ __device__ __forceinline__ void lds_dma16(const void* src, unsigned lds_addr) {
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 __device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
-template <bool MASKED>
-__device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0, char* lds) {
+// SPEC (unmasked rows only): after the first stage the offset m is frozen and
+// the running max is not computed; p = exp2(s - m) may then exceed 2^kLazy.
+// That is exact up to a common scale as long as nothing overflows, which the
+// end of the pass checks (every row sum below 2^100 and every output finite);
+// otherwise nothing is written and false is returned, and the caller redoes
+// the block with the tracked max.
+template <bool MASKED, bool SPEC>
+__device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0, char* lds) {
+  static_assert(!(MASKED && SPEC), "speculation is for unmasked rows");
   constexpr int G = kRows;
   const int n = L.n, np = L.np;
   // w is wave-uniform: read into an SGPR so that the DMA job set-up and the
@@ -398,16 +405,18 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
       }
       // This lane's max over its 16 keys (a v_max3 tree: 5 + 2 + 1); the max
       // over all keys of a query (4 lanes) is only needed when some lane
-      // crosses the lazy threshold.
-      const f32x4* sr = s[r];
-      const float a0 = max3f(sr[0][0], sr[0][1], sr[0][2]), a1 = max3f(sr[0][3], sr[1][0], sr[1][1]);
-      const float a2 = max3f(sr[1][2], sr[1][3], sr[2][0]), a3 = max3f(sr[2][1], sr[2][2], sr[2][3]);
-      const float a4 = max3f(sr[3][0], sr[3][1], sr[3][2]);
-      mt[r] = fmaxf(max3f(a0, a1, a2), max3f(a3, a4, sr[3][3]));
+      // crosses the lazy threshold.  Speculative passes need it only once.
+      if (!SPEC || k0 == 0) {
+        const f32x4* sr = s[r];
+        const float a0 = max3f(sr[0][0], sr[0][1], sr[0][2]), a1 = max3f(sr[0][3], sr[1][0], sr[1][1]);
+        const float a2 = max3f(sr[1][2], sr[1][3], sr[2][0]), a3 = max3f(sr[2][1], sr[2][2], sr[2][3]);
+        const float a4 = max3f(sr[3][0], sr[3][1], sr[3][2]);
+        mt[r] = fmaxf(max3f(a0, a1, a2), max3f(a3, a4, sr[3][3]));
+      }
     }
     bool grow = false;
 #pragma unroll
-    for (int r = 0; r < G; ++r) grow |= MASKED ? mt[r] > m[r] + kLazy : mt[r] > kLazy;
+    for (int r = 0; r < G; ++r) grow |= SPEC ? false : MASKED ? mt[r] > m[r] + kLazy : mt[r] > kLazy;
     auto query_max = [](float v) {
       v = fmaxf(v, __shfl_xor(v, 16, kWave));
       return fmaxf(v, __shfl_xor(v, 32, kWave));
@@ -465,6 +474,20 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
     wait_vm0();  // this wave's DMAs of the next stage
     __syncthreads();
   }
+  if (SPEC) {
+    // Exponent-field tests (this file builds with -fno-honor-nans, so no
+    // floating-point NaN compares): every row sum below 2^101, every output finite.
+    bool ok = true;
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      ok &= ((__float_as_uint(ls[r][0]) >> 23) & 0xFF) <= 127 + 100;
+#pragma unroll
+      for (int mt2 = 0; mt2 < 2; ++mt2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ok &= (__float_as_uint(o[r][mt2][e]) & 0x7F800000u) != 0x7F800000u;
+    }
+    if (__syncthreads_or(!ok)) return false;
+  }
   const int q = q0 + lq;
 #pragma unroll
   for (int r = 0; r < G; ++r) {
@@ -479,6 +502,7 @@ __device__ __forceinline__ void core_rows(const Layout& L, int i0, int h, int q0
       }
     }
   }
+  return true;
 }
 
 // Two 8-wave blocks per CU need <= 128 VGPRs; one register more would leave a
@@ -503,10 +527,12 @@ __global__ __launch_bounds__(kCoreThreads) __attribute__((amdgpu_waves_per_eu(4)
     for (int k = t; k < n; k += kCoreThreads) masked |= mbrow[k] != 0.f;
   }
   masked = __syncthreads_or(masked);
-  if (masked)
-    core_rows<true>(L, i0, h, q0, stage_lds);
-  else
-    core_rows<false>(L, i0, h, q0, stage_lds);
+  if (masked) {
+    core_rows<true, false>(L, i0, h, q0, stage_lds);
+  } else if (!core_rows<false, true>(L, i0, h, q0, stage_lds)) {
+    // a score rose far above the first stage's max: redo the block with the tracked max
+    core_rows<false, false>(L, i0, h, q0, stage_lds);
+  }
 }
 
 // ------------------------------------------------------------------ K3
