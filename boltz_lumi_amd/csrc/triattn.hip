@@ -287,10 +287,14 @@ __device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf
 
 // SPEC (unmasked rows only): after the first stage the offset m is frozen and
 // the running max is not computed; p = exp2(s - m) may then exceed 2^kLazy.
-// That is exact up to a common scale as long as nothing overflows, which the
-// end of the pass checks (every row sum below 2^100 and every output finite);
-// otherwise nothing is written and false is returned, and the caller redoes
-// the block with the tracked max.
+// The offset is also shared by the block's rows (the max of their first-stage
+// maxima), so the bias tile minus m, which does not depend on the row, is
+// formed by one identity MFMA per key tile and is the C operand of every
+// row's K Q^T.  That is exact up to a common scale as long as nothing
+// overflows and no row's sum falls towards the fp32 underflow range, which the
+// end of the pass checks (every row sum in [2^-60, 2^100], every output
+// finite); otherwise nothing is written and false is returned, and the caller
+// redoes the block with per-row tracked maxima.
 template <bool MASKED, bool SPEC>
 __device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0, char* lds) {
   static_assert(!(MASKED && SPEC), "speculation is for unmasked rows");
@@ -392,16 +396,27 @@ __device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0
     // with another row's max / exp work inside one basic block.
     f32x4 s[G][4];
     float mt[G];
-#pragma unroll
-    for (int r = 0; r < G; ++r) {
+    // Triangle-bias B tile j: lanes of groups 0 and 1 hold keys 16j + 8g .. +7
+    // of their query; groups 2 and 3 read the same bytes, which ident
+    // multiplies by zero (the bias is finite).
+    if constexpr (SPEC) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f32x4 c = MASKED ? *(const f32x4*)(sb + kOffMb + r * kKT * 4 + (16 * j + 4 * g) * 4) : mneg[r];
-        s[r][j] = mfma16(*(const bf16x8*)(sb + k_rd + r * kTileBytes + 1024 * j), qf[r], c);
-        // Triangle-bias B tile j: lanes of groups 0 and 1 hold keys 16j + 8g .. +7
-        // of their query; groups 2 and 3 read the same bytes, which ident
-        // multiplies by zero (the bias is finite).
-        s[r][j] = mfma16(ident, *(const bf16x8*)(sb + b_rd + 512 * j), s[r][j]);
+        const f32x4 bc = mfma16(ident, *(const bf16x8*)(sb + b_rd + 512 * j), mneg[0]);
+#pragma unroll
+        for (int r = 0; r < G; ++r)
+          s[r][j] = mfma16(*(const bf16x8*)(sb + k_rd + r * kTileBytes + 1024 * j), qf[r], bc);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      if constexpr (!SPEC) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 c = MASKED ? *(const f32x4*)(sb + kOffMb + r * kKT * 4 + (16 * j + 4 * g) * 4) : mneg[r];
+          s[r][j] = mfma16(*(const bf16x8*)(sb + k_rd + r * kTileBytes + 1024 * j), qf[r], c);
+          s[r][j] = mfma16(ident, *(const bf16x8*)(sb + b_rd + 512 * j), s[r][j]);
+        }
       }
       // This lane's max over its 16 keys (a v_max3 tree: 5 + 2 + 1); the max
       // over all keys of a query (4 lanes) is only needed when some lane
@@ -422,9 +437,13 @@ __device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0
       return fmaxf(v, __shfl_xor(v, 32, kWave));
     };
     if ((!MASKED && k0 == 0) || __any(grow)) {  // wave-uniform; rare after the first stages
+      float mall = mt[0];
+#pragma unroll
+      for (int r = 1; r < G; ++r) mall = fmaxf(mall, mt[r]);
+      const float qshared = SPEC ? query_max(mall) : 0.f;
 #pragma unroll
       for (int r = 0; r < G; ++r) {
-        const float qmax = query_max(mt[r]);
+        const float qmax = SPEC ? qshared : query_max(mt[r]);
         float mn;
         if (MASKED)
           mn = fmaxf(m[r], qmax);
@@ -476,11 +495,12 @@ __device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0
   }
   if (SPEC) {
     // Exponent-field tests (this file builds with -fno-honor-nans, so no
-    // floating-point NaN compares): every row sum below 2^101, every output finite.
+    // floating-point NaN compares): every row sum in [2^-60, 2^101), every output finite.
     bool ok = true;
 #pragma unroll
     for (int r = 0; r < G; ++r) {
-      ok &= ((__float_as_uint(ls[r][0]) >> 23) & 0xFF) <= 127 + 100;
+      const unsigned ex = (__float_as_uint(ls[r][0]) >> 23) & 0xFF;
+      ok &= ex <= 127 + 100 && ex >= 127 - 60;
 #pragma unroll
       for (int mt2 = 0; mt2 < 2; ++mt2)
 #pragma unroll

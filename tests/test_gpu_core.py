@@ -72,3 +72,29 @@ def test_core_matches_fp32_softmax_of_its_inputs(gpu, boost):
     assert torch.isfinite(got).all()
     err = ((got - want).abs().max() / want.abs().max()).item()
     assert err < 2e-2, err
+
+
+@pytest.mark.parametrize("gap", [50.0, 200.0])
+def test_core_rows_far_below_their_block_partner(gpu, gap):
+    """A block's rows share one softmax offset in the speculative pass.  Even
+    rows get q = 1 and k = -gap/32, so their scores sit ``gap`` (log2 units)
+    below the odd rows': at 50 the shared offset leaves their weights near
+    2^-50, still exact in fp32 and bf16; at 200 their row sums underflow, the
+    pass reports it and the block is redone with per-row maxima."""
+    torch.manual_seed(6)
+    n = 200
+    m = layers.TriangleAttention().to(gpu).eval()
+    x = torch.randn(1, n, n, 128, device=gpu)
+    ws = ops.new_workspace(n, gpu)
+    with torch.inference_mode():
+        ops.triattn(m, x[0], None, True, ops.OUT_BF16, None, ws, stages=1)
+        npad, q, k, vt, o, tb, mb = _views(ws, n)
+        q[0:n:2, :, :n] = 1.0
+        k[0:n:2, :, :n] = -gap / D
+        ops.triattn(m, x[0], None, True, ops.OUT_BF16, None, ws, stages=2)
+        want = _reference(n, npad, q, k, vt, tb, mb)
+        got = o.float()
+    assert torch.isfinite(got).all()
+    for rows in (slice(0, n, 2), slice(1, n, 2)):
+        err = ((got[rows] - want[rows]).abs().max() / want[rows].abs().max()).item()
+        assert err < 2e-2, err
