@@ -359,6 +359,33 @@ class PairformerLayer(nn.Module):
         return s, z
 
 
+class PairformerNoSeqLayer(nn.Module):
+    """Upstream ``layers.pairformer.PairformerNoSeqLayer`` (eval mode): the
+    pair stack of ``PairformerLayer`` without the sequence stack.  Upstream
+    builds one per ``MSALayer`` (``token_z`` 128) and one per template
+    pairformer block (``template_dim`` 64).  The reference patches its modules
+    by class name and by the ``.transition_z`` suffix (``adapters.py:24-45``),
+    as in the trunk.  Composition order is PARITY UNPINNED as for
+    ``PairformerLayer``; ``tests/test_oracle_pins.py`` ties the two together.
+    """
+
+    def __init__(self, token_z=128, pairwise_head_width=32, pairwise_num_heads=4):
+        super().__init__()
+        self.token_z = token_z
+        self.tri_mul_out = TriangleMultiplicationOutgoing(token_z)
+        self.tri_mul_in = TriangleMultiplicationIncoming(token_z)
+        self.tri_att_start = TriangleAttention(token_z, pairwise_head_width, pairwise_num_heads, inf=1e9)
+        self.tri_att_end = TriangleAttentionEndingNode(token_z, pairwise_head_width, pairwise_num_heads, inf=1e9)
+        self.transition_z = Transition(token_z, token_z * 4)
+
+    def forward(self, z, pair_mask, chunk_size_tri_attn=None, use_kernels=False):
+        z = z + self.tri_mul_out(z, mask=pair_mask)
+        z = z + self.tri_mul_in(z, mask=pair_mask)
+        z = z + self.tri_att_start(z, mask=pair_mask, chunk_size=chunk_size_tri_attn)
+        z = z + self.tri_att_end(z, mask=pair_mask, chunk_size=chunk_size_tri_attn)
+        return z + self.transition_z(z)
+
+
 # --------------------------------------------------------------------------
 # Diffusion conditioning blocks  (reference: diffusion.py, rows A8-A10)
 # --------------------------------------------------------------------------

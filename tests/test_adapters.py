@@ -170,3 +170,38 @@ def test_conditioning_cache_is_inert_on_cpu():
         layer.adaln.s_norm(s)
     assert len(calls) == 2  # CPU inputs are never cached
     assert layer.adaln.s_norm.forward is counting
+
+
+def test_msa_template_and_confidence_stacks_are_patched_by_class_and_suffix():
+    """The reference selects pair modules by class name anywhere in the model
+    and transitions by the ``.transition_z`` suffix (adapters.py:24-45), so
+    the MSA, template and confidence stacks are patched like the trunk; the
+    MSA module's own ``msa_transition`` is not.  On CPU every patched forward
+    falls back to the upstream one bit for bit."""
+    model = nn.Module()
+    model.msa_module = nn.Module()
+    msa_layer = nn.Module()
+    msa_layer.pairformer_layer = R.PairformerNoSeqLayer(16, pairwise_head_width=8, pairwise_num_heads=2)
+    msa_layer.msa_transition = R.Transition(8, 32)
+    model.msa_module.layers = nn.ModuleList([msa_layer])
+    model.template_module = nn.Module()
+    model.template_module.pairformer = nn.Module()
+    model.template_module.pairformer.layers = nn.ModuleList(
+        [R.PairformerNoSeqLayer(8, pairwise_head_width=8, pairwise_num_heads=2)])
+    model.confidence_module = nn.Module()
+    model.confidence_module.pairformer_stack = nn.Module()
+    model.confidence_module.pairformer_stack.layers = nn.ModuleList(
+        [R.PairformerLayer(token_s=32, token_z=16, num_heads=4, pairwise_head_width=8, pairwise_num_heads=2)])
+    R.randomize(model, generator=torch.Generator().manual_seed(3)).eval()
+    z = torch.randn(2, 6, 6, 8)
+    pm = torch.ones(2, 6, 6)
+    pm[:, -1] = 0
+    template = model.template_module.pairformer.layers[0]
+    with torch.inference_mode():
+        want = template(z, pm)
+    assert adapters.install(model, require_boltz2=False, require_device=False) == 15
+    assert "forward" in vars(msa_layer.pairformer_layer.transition_z)
+    assert "forward" not in vars(msa_layer.msa_transition)
+    with torch.inference_mode():
+        assert torch.equal(template(z, pm), want)
+    adapters.uninstall(model)

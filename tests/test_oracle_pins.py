@@ -346,3 +346,26 @@ def test_pairformer_layer_runs_and_is_residual():
         mask = torch.ones(1, 6)
         s2, z2 = layer(s, z, mask, mask[:, :, None] * mask[:, None, :])
     assert torch.equal(z2, z) and torch.equal(s2, s)
+
+
+@pytest.mark.parametrize("token_z", [16, 8])
+def test_pairformer_no_seq_layer_is_the_trunk_pair_stack(token_z):
+    """The MSA / template stack layer with the trunk layer's pair weights
+    gives the trunk layer's z bit for bit (same modules, same order), at the
+    trunk's width and at a template-like narrower one."""
+    g = _gen(19)
+    layer = R.randomize(R.PairformerLayer(token_s=32, token_z=token_z, num_heads=4, pairwise_head_width=8,
+                                          pairwise_num_heads=2), generator=g)
+    noseq = R.PairformerNoSeqLayer(token_z, pairwise_head_width=8, pairwise_num_heads=2)
+    own = noseq.state_dict()
+    noseq.load_state_dict({k: v for k, v in layer.state_dict().items() if k in own})
+    with torch.no_grad():
+        s = torch.randn(1, 6, 32, generator=g)
+        z = torch.randn(1, 6, 6, token_z, generator=g)
+        mask = torch.ones(1, 6)
+        mask[:, -1] = 0
+        pair_mask = mask[:, :, None] * mask[:, None, :]
+        _, want = layer(s, z, mask, pair_mask)
+        got = noseq(z, pair_mask)
+    assert set(own) <= set(layer.state_dict())
+    assert torch.equal(got, want)
