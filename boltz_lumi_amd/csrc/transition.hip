@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256) void pair_bias_fold_kernel(const float* __rest
 }
 
 template <typename TIn, bool BIAS>
-__global__ __launch_bounds__(256) void pair_transition_kernel(const TIn* x, const float* __restrict__ ln_w,
+__global__ __launch_bounds__(256, 2) void pair_transition_kernel(const TIn* x, const float* __restrict__ ln_w,
                                                               const float* __restrict__ ln_b, float eps,
                                                               const bf16* __restrict__ w12,
                                                               const bf16* __restrict__ w3, void* out, int out_mode,
@@ -193,8 +193,9 @@ __global__ __launch_bounds__(256) void pair_transition_kernel(const TIn* x, cons
   const int t = threadIdx.x, l = lane_id(), w = t >> 6;
   const int c0 = 32 * w;  // this wave's 32 hidden channels of each chunk / 32 output channels
   // fc1 / fc2 rows of one 128-wide hidden chunk (A operands).  Chunk 0 is
-  // requested before the LayerNorm and chunk c+1 before the fc3 phase of
-  // chunk c, so the L2 latency of the weight stream is never waited on.
+  // requested before the LayerNorm and chunk c+1 right after the last fc1 |
+  // fc2 MFMAs of chunk c, so the last SiLU products and the fc3 phase of
+  // chunk c cover the L2 latency of the weight stream.
   bf16x8 f1[8], f2[8];
   auto load_w12 = [&](int hc) {
 #pragma unroll
@@ -222,6 +223,7 @@ __global__ __launch_bounds__(256) void pair_transition_kernel(const TIn* x, cons
         a1 = mfma32(f1[ks], xf, a1);
         a2 = mfma32(f2[ks], xf, a2);
       }
+      if (nt == 3 && hc + 1 < kHidden / kC) load_w12(hc + 1);
       // D[hidden][pair]: lane -> pair nt*32 + l%32, registers 4q..4q+3 ->
       // hidden channels c0 + 8q + 4(l/32) + 0..3, stored as one 8-byte write.
       bf16* dst = hid + (nt * 32 + (l & 31)) * kLdsRow + c0 + 4 * (l >> 5);
@@ -233,7 +235,6 @@ __global__ __launch_bounds__(256) void pair_transition_kernel(const TIn* x, cons
         *(bf16x4*)(dst + 8 * q) = v;
       }
     }
-    if (hc + 1 < kHidden / kC) load_w12(hc + 1);
     __syncthreads();
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
