@@ -37,9 +37,11 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=3, help="repetitions of the per-kernel timing pass")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first copy 1 GiB device-to-device (a kernel of known traffic for scaling PMC byte counters)")
-    p.add_argument("--workload", choices=("pairformer", "token-attention"), default="pairformer",
+    p.add_argument("--workload", choices=("pairformer", "token-attention", "diffusion"), default="pairformer",
                    help="pairformer: the headline PairformerLayer line (default); token-attention: the diffusion "
-                        "token transformer's AttentionPairBias (16 x 48 heads, 5 samples, prepacked bias)")
+                        "token transformer's AttentionPairBias (16 x 48 heads, 5 samples, prepacked bias); "
+                        "diffusion: the score model's AdaLN / ConditionedTransitionBlock forwards and their fused "
+                        "kernels at the token and atom transformer shapes")
     return p.parse_args()
 
 
@@ -235,6 +237,117 @@ def token_attention_cpu(n: int):
                       f"{cores} threads, scaled x5"}
 
 
+def diffusion(args):
+    """The diffusion score model's conditioning blocks at BASELINE configs[4]
+    shapes (5 samples; token transformer 1024 tokens x 768, atom transformer
+    8192 atoms x 128): AdaLN and ConditionedTransitionBlock forwards of one
+    layer of each transformer, fp32 as the reference runs them
+    (diffusion.py:37-68), plus the fused kernels alone (bmx_adaln, the
+    GATED_SWIGLU and GATE epilogues) against the 8 TB/s HBM roofline.  Bytes
+    per launch: AdaLN 16 M D (a, scale, shift in, out), GATED_SWIGLU 16 M Di
+    (u [M, 2 Di] and b in, out), GATE 12 M D."""
+    import torch
+    from boltz_lumi_amd import layers, ops
+
+    dev = torch.device("cuda:0")
+    samples = 5
+    shapes = {"token": (samples * args.n, 768, 768), "atom": (samples * 8192, 128, 128)}
+    g = torch.Generator().manual_seed(0)
+
+    def timed(fn, reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    kernels, blocks = {}, {}
+    with torch.inference_mode():
+        for name, (m, d, dc) in shapes.items():
+            di = 2 * d
+            adaln = init_weights(layers.AdaLN(d, dc), 0).to(dev).eval()
+            ctb = init_weights(layers.ConditionedTransitionBlock(d, dc), 1).to(dev).eval()
+            a = torch.randn(m, d, generator=g).to(dev)
+            c = torch.randn(m, dc, generator=g).to(dev)
+            for _ in range(args.warmup):
+                ctb(adaln(a, c), c)
+            torch.cuda.synchronize()
+            blocks[name] = timed(lambda: ctb(adaln(a, c), c), args.steps)
+            # Each kernel cycles over enough input sets that successive launches
+            # do not find their operands in the 256 MB Infinity Cache.
+            sets = 1 + (768 << 20) // (16 * m * d)
+            bufs = [{"a": torch.randn(m, d, generator=g).to(dev), "scale": torch.randn(m, d, generator=g).to(dev),
+                     "shift": torch.randn(m, d, generator=g).to(dev), "u": torch.randn(m, 2 * di, generator=g).to(dev),
+                     "b": torch.randn(m, di, generator=g).to(dev), "g": torch.randn(m, d, generator=g).to(dev),
+                     "y": torch.randn(m, d, generator=g).to(dev)} for _ in range(sets)]
+            reps = sets * max(1, max(args.steps, 10) // sets)
+            turn = [0]
+
+            def nxt():
+                turn[0] = (turn[0] + 1) % sets
+                return bufs[turn[0]]
+
+            for kname, fn, nbytes in (
+                    ("adaln", lambda: (lambda t: ops.adaln_modulate(t["a"], t["scale"], t["shift"], 1e-5))(nxt()),
+                     16 * m * d),
+                    ("gated_swiglu", lambda: (lambda t: ops.epilogue(t["u"], t["b"], None, ops.GATED_SWIGLU))(nxt()),
+                     16 * m * di),
+                    ("gate", lambda: (lambda t: ops.epilogue(t["g"], t["y"], None, ops.GATE))(nxt()), 12 * m * d)):
+                ms = timed(fn, reps)
+                gbs = nbytes / (ms * 1e-3) / 1e9
+                kernels[f"{kname}_{name}"] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(gbs, 1),
+                                              "frac": round(gbs / PEAK_HBM_GBS, 4), "input_sets": sets}
+            del bufs
+    ms = blocks["token"] + blocks["atom"]
+    dom = kernels["gated_swiglu_token"]
+    out_line = {
+        "metric": "diffusion conditioning blocks (AdaLN + ConditionedTransitionBlock) ms per token + atom layer, "
+                  "5 samples; AdaLN/gating kernels % of HBM roofline",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (activations and conditioning ~ N(0,1); weights seeds 0 and 1)",
+        "config": {"workload": f"diffusion score-model AdaLN + ConditionedTransitionBlock forward, token layer "
+                               f"({samples} x {args.n} x 768) + atom layer ({samples} x 8192 x 128), "
+                               f"BASELINE configs[4] shapes",
+                   "n_tokens": args.n, "n_atoms": 8192, "samples": samples,
+                   "block_ms": {k: round(v, 4) for k, v in blocks.items()}},
+        "roofline": {"kernel": "gated_swiglu (token)", "bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": dom["frac"], "traffic": None, "kernels": kernels},
+    }
+    if not args.no_cpu_baseline:
+        out_line["cpu_baseline"] = diffusion_cpu(args.n)
+    print(json.dumps(out_line), flush=True)
+
+
+def diffusion_cpu(n: int):
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import boltz_ref as R  # the checker, timed as the reference CPU path
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    total = 0.0
+    with torch.inference_mode():
+        for m, d in ((n, 768), (8192, 128)):
+            adaln = init_weights(R.AdaLN(d, d), 0).eval()
+            ctb = init_weights(R.ConditionedTransitionBlock(d, d), 1).eval()
+            a, c = torch.randn(1, m, d, generator=g), torch.randn(1, m, d, generator=g)
+            ctb(adaln(a[:, :64], c[:, :64]), c[:, :64])
+            t0 = time.perf_counter()
+            ctb(adaln(a, c), c)
+            total += time.perf_counter() - t0
+    return {"value": round(total * 1e3 * 5, 1), "unit": "ms per token + atom layer, 5 samples (1 sample timed, x5)",
+            "cores": cores, "kind": "port",
+            "sample": f"one sample of the fp32 CPU oracle AdaLN + ConditionedTransitionBlock (oracle/boltz_ref.py) "
+                      f"at {n} tokens x 768 and 8192 atoms x 128, {cores} threads, scaled x5"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -243,6 +356,8 @@ def main():
         sys.exit(2)
     if args.workload == "token-attention":
         return token_attention(args)
+    if args.workload == "diffusion":
+        return diffusion(args)
     import torch
     from boltz_lumi_amd import layers, ops
 

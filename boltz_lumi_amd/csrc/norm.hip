@@ -101,46 +101,56 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const T* __restrict__ x, c
 }
 
 // out = sigmoid(scale) * LN(a) + shift; multiply and add round separately as
-// in the eager PyTorch expression.
-template <typename T>
+// in the eager PyTorch expression.  LANES lanes per row: 64, or 32 for
+// d <= 128 (two rows per wave, so no lane idles at the atom transformer's
+// width).  a, scale and shift are all requested before the row reductions,
+// with indices clamped into the row so that every load is unconditional.
+template <typename T, int LANES>
 __global__ __launch_bounds__(256) void adaln_kernel(const T* __restrict__ a, const T* __restrict__ scale,
                                                     const T* __restrict__ shift, T* __restrict__ out,
                                                     int64_t rows, int d, float eps) {
 #pragma clang fp contract(off)
-  const int l = lane_id();
+  constexpr int kPer = LANES == 64 ? kMaxChunks : 1;  // float4 chunks per lane: d <= 4 * LANES * kPer
+  const int l = threadIdx.x & (LANES - 1);
   const int chunks = d >> 2;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  f32x4 v[kMaxChunks];
+  const int64_t row = (int64_t)blockIdx.x * (256 / LANES) + threadIdx.x / LANES;
+  if (row >= rows) return;  // whole rows (a half-wave's reductions stay inside the half-wave)
+  const int64_t base = row * d;
+  f32x4 v[kPer], sc[kPer], sh[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int ch = min(l + LANES * u, chunks - 1);
+    v[u] = load4(a + base + 4 * ch);
+    sc[u] = load4(scale + base + 4 * ch);
+    sh[u] = load4(shift + base + 4 * ch);
+  }
+  auto reduce = [](float x) { return LANES == 64 ? wave_sum(x) : half_sum(x); };
   float s = 0.f;
 #pragma unroll
-  for (int u = 0; u < kMaxChunks; ++u) {
-    int ch = l + 64 * u;
-    v[u] = ch < chunks ? load4(a + row * d + 4 * ch) : f32x4{0.f, 0.f, 0.f, 0.f};
-    s += v[u][0] + v[u][1] + v[u][2] + v[u][3];
-  }
-  const float mean = wave_sum(s) / d;
+  for (int u = 0; u < kPer; ++u)
+    if (l + LANES * u < chunks) s += v[u][0] + v[u][1] + v[u][2] + v[u][3];
+  const float mean = reduce(s) / d;
   float q = 0.f;
 #pragma unroll
-  for (int u = 0; u < kMaxChunks; ++u) {
-    if (l + 64 * u < chunks) {
+  for (int u = 0; u < kPer; ++u) {
+    if (l + LANES * u < chunks) {
       f32x4 dv = v[u] - mean;
       q += dv[0] * dv[0] + dv[1] * dv[1] + dv[2] * dv[2] + dv[3] * dv[3];
     }
   }
-  const float inv = rsqrtf(wave_sum(q) / d + eps);
+  const float inv = rsqrtf(reduce(q) / d + eps);
 #pragma unroll
-  for (int u = 0; u < kMaxChunks; ++u) {
-    int ch = l + 64 * u;
+  for (int u = 0; u < kPer; ++u) {
+    const int ch = l + LANES * u;
     if (ch < chunks) {
-      f32x4 sc = load4(scale + row * d + 4 * ch);
-      f32x4 sh = load4(shift + row * d + 4 * ch);
+      f32x4 r;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float an = (v[u][e] - mean) * inv;
-        float prod = sigmoid_f(sc[e]) * an;
-        out[row * d + 4 * ch + e] = (T)(prod + sh[e]);
+        float prod = sigmoid_f(sc[u][e]) * an;
+        r[e] = prod + sh[u][e];
       }
+      store4(out + base + 4 * ch, r);
     }
   }
 }
@@ -205,13 +215,20 @@ int bmx_adaln(const void* a, const void* scale, const void* shift, void* out, in
   BMX_REQUIRE(eps > 0.f, "bmx_adaln: eps must be positive");
   if (rows == 0) return BMX_OK;
   BMX_REQUIRE(a && scale && shift && out, "bmx_adaln: null pointer");
-  dim3 grid((unsigned)((rows + 3) / 4));
-  if (dtype == kF32)
-    adaln_kernel<float><<<grid, 256, 0, stream>>>((const float*)a, (const float*)scale, (const float*)shift,
-                                                  (float*)out, rows, dim, eps);
-  else
-    adaln_kernel<bf16><<<grid, 256, 0, stream>>>((const bf16*)a, (const bf16*)scale, (const bf16*)shift,
-                                                 (bf16*)out, rows, dim, eps);
+  const int align = dtype == kF32 ? 16 : 8;
+  BMX_REQUIRE(((uintptr_t)a | (uintptr_t)scale | (uintptr_t)shift | (uintptr_t)out) % align == 0,
+              "bmx_adaln: operands must be %d-byte aligned", align);
+#define ADALN(T, LANES)                                                                             \
+  adaln_kernel<T, LANES><<<dim3((unsigned)((rows + 256 / LANES - 1) / (256 / LANES))), 256, 0, stream>>>( \
+      (const T*)a, (const T*)scale, (const T*)shift, (T*)out, rows, dim, eps)
+  if (dtype == kF32) {
+    if (dim <= 128) ADALN(float, 32);
+    else ADALN(float, 64);
+  } else {
+    if (dim <= 128) ADALN(bf16, 32);
+    else ADALN(bf16, 64);
+  }
+#undef ADALN
   return check_launch("bmx_adaln");
 }
 

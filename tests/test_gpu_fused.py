@@ -10,6 +10,7 @@ import copy
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 from boltz_lumi_amd import ops
 from oracle import boltz_ref as R
@@ -175,3 +176,18 @@ def test_adaln_modulate_matches_oracle(gpu, dtype):
     with torch.inference_mode():
         got = ops.adaln_modulate(a.to(dtype).to(gpu), scale.to(dtype).to(gpu), shift.to(dtype).to(gpu), 1e-5)
     assert errors(got, want)["max_rel"] < (1e-5 if dtype == torch.float32 else TOL)
+
+
+@pytest.mark.parametrize("dim", [4, 100, 128, 132, 256, 1024])
+def test_adaln_modulate_widths_and_ragged_rows(gpu, dim):
+    """Both row layouts of bmx_adaln (a half-wave per row up to 128 channels,
+    a wave per row above) at widths that leave lanes or whole chunks idle,
+    with a row count that ends inside a block; fp32 against the eager
+    expression sigmoid(scale) * LN(a) + shift."""
+    g = torch.Generator().manual_seed(dim)
+    rows = 37
+    a, scale, shift = (torch.randn(rows, dim, generator=g) for _ in range(3))
+    want = torch.sigmoid(scale) * F.layer_norm(a, (dim,), eps=1e-5) + shift
+    with torch.inference_mode():
+        got = ops.adaln_modulate(a.to(gpu), scale.to(gpu), shift.to(gpu), 1e-5)
+    assert errors(got, want)["max_rel"] < 1e-5
