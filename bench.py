@@ -266,11 +266,13 @@ def diffusion(args):
         return e0.elapsed_time(e1) / reps
 
     kernels, blocks = {}, {}
+    modules = {name: (init_weights(layers.AdaLN(d, dc), 0).to(dev).eval(),
+                      init_weights(layers.ConditionedTransitionBlock(d, dc), 1).to(dev).eval())
+               for name, (m, d, dc) in shapes.items()}
     with torch.inference_mode():
         for name, (m, d, dc) in shapes.items():
             di = 2 * d
-            adaln = init_weights(layers.AdaLN(d, dc), 0).to(dev).eval()
-            ctb = init_weights(layers.ConditionedTransitionBlock(d, dc), 1).to(dev).eval()
+            adaln, ctb = modules[name]
             a = torch.randn(m, d, generator=g).to(dev)
             c = torch.randn(m, dc, generator=g).to(dev)
             for _ in range(args.warmup):

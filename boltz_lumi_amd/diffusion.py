@@ -7,7 +7,10 @@ AdaLN / transition forwards run in fp32 with autocast off.  AdaLN's a_norm + sig
 + s_bias become one LN/modulate kernel; the SwiGLU gate and the output gate
 are fused epilogues.  The conditioning projections are still called as
 submodules, so ``atom_conditioning_cache`` keeps working (reference
-atom_conditioning.py:12-45).  Guard failures call the class forward.
+atom_conditioning.py:12-45); the projections of the activation a (swish_gate,
+a_to_b, b_to_a), which the reference runs as fp32 hipBLASLt GEMMs, run as
+split-bf16 GEMMs with fp32 accumulation (``ops.linear_x3``, about 2^-16
+relative per product).  Guard failures call the class forward.
 """
 
 from __future__ import annotations
@@ -57,5 +60,10 @@ def transition_forward(self, a, s):
     if not eligible(self, a, s):
         return type(self).forward(self, a, s)
     a = self.adaln(a, s)
-    b = ops.epilogue(self.swish_gate[0](a).contiguous(), self.a_to_b(a).contiguous(), None, ops.GATED_SWIGLU)
-    return ops.epilogue(self.output_projection[0](s).contiguous(), self.b_to_a(b).contiguous(), None, ops.GATE)
+    if a.shape[-1] % 4:
+        b = ops.epilogue(self.swish_gate[0](a).contiguous(), self.a_to_b(a).contiguous(), None, ops.GATED_SWIGLU)
+        return ops.epilogue(self.output_projection[0](s).contiguous(), self.b_to_a(b).contiguous(), None, ops.GATE)
+    # The a-path projections as split-bf16 GEMMs with fp32 accumulation; the
+    # s-path output gate stays a submodule call (atom_conditioning_cache).
+    b = ops.epilogue(ops.linear_x3(a, self.swish_gate[0]), ops.linear_x3(a, self.a_to_b), None, ops.GATED_SWIGLU)
+    return ops.epilogue(self.output_projection[0](s).contiguous(), ops.linear_x3(b, self.b_to_a), None, ops.GATE)

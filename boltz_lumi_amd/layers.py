@@ -359,5 +359,5 @@ class ConditionedTransitionBlock(nn.Module):
 
     def forward(self, a, s):
         a = self.adaln(a, s)
-        b = ops.epilogue(self.swish_gate[0](a).contiguous(), self.a_to_b(a).contiguous(), None, ops.GATED_SWIGLU)
-        return ops.epilogue(self.output_projection[0](s).contiguous(), self.b_to_a(b).contiguous(), None, ops.GATE)
+        b = ops.epilogue(ops.linear_x3(a, self.swish_gate[0]), ops.linear_x3(a, self.a_to_b), None, ops.GATED_SWIGLU)
+        return ops.epilogue(self.output_projection[0](s).contiguous(), ops.linear_x3(b, self.b_to_a), None, ops.GATE)

@@ -54,13 +54,18 @@ def _inference_only() -> None:
     _check(not torch.is_grad_enabled(), "Inference only")
 
 
+def _version(p):
+    return -1 if p.is_inference() else p._version
+
+
 def cached_weight(module, name: str, sources, build):
     """Derived weight (e.g. a bf16 concatenation) cached on ``module``.
 
     Reused only while every source parameter keeps its identity, version,
     device and dtype (the rule of the reference's joint projection cache,
-    multiplication.py:29-40)."""
-    key = tuple((id(p), p._version, p.device, p.dtype) for p in sources)
+    multiplication.py:29-40).  Inference tensors carry no version counter;
+    for them only identity, device and dtype are checked."""
+    key = tuple((id(p), _version(p), p.device, p.dtype) for p in sources)
     cache = module.__dict__.setdefault("_bmx_weight_cache", {})
     hit = cache.get(name)
     if hit is None or hit[0] != key:
@@ -198,6 +203,53 @@ def silu_mul(a, b):
     if a.numel():
         N.call("bmx_silu_mul", a.data_ptr(), b.data_ptr(), out.data_ptr(), a.numel(), _stream(a))
     return out
+
+
+def split3(x):
+    """[bf16(x) | bf16(x) | bf16(x - bf16(x))] along the last axis (``bmx_split3_bf16``), bf16 [..., 3 k]."""
+    _cuda(x)
+    _check(x.dtype == torch.float32 and x.is_contiguous() and x.shape[-1] % 4 == 0,
+           "expected contiguous fp32 x with a multiple of 4 columns")
+    k = x.shape[-1]
+    out = torch.empty(x.shape[:-1] + (3 * k,), device=x.device, dtype=torch.bfloat16)
+    rows = x.numel() // k if k else 0
+    if rows:
+        N.call("bmx_split3_bf16", x.data_ptr(), rows, k, k, out.data_ptr(), _stream(x))
+    return out
+
+
+def _x3_weight(w):
+    """[bf16(W) | bf16(W - bf16(W)) | bf16(W)]^T, contiguous [3 K, N] bf16, for W [N, K] fp32."""
+    w = w.detach().float()
+    hi = w.to(torch.bfloat16)
+    lo = (w - hi.float()).to(torch.bfloat16)
+    return torch.cat([hi, lo, hi], dim=1).t().contiguous()
+
+
+def x3_weight(module, name, *weights):
+    """Split weight of ``mm_x3`` for the row concatenation of ``weights``
+    ([N_i, K] each), cached on ``module`` under ``name``."""
+    return cached_weight(module, name, weights, lambda *ws: _x3_weight(torch.cat(ws, 0)))
+
+
+def mm_x3(x, w3):
+    """``x @ W^T`` for fp32 x [M, K] and ``w3 = x3_weight(..W..)``: one hipBLASLt
+    bf16 GEMM with fp32 accumulation of ``split3(x)`` against the split weight
+    (x W ~ xh Wh + xh Wl + xl Wh, about 2^-16 relative per product); fp32 [M, N]."""
+    _check(x.dim() == 2 and w3.shape[0] == 3 * x.shape[1], "x does not match the split weight")
+    return torch.mm(split3(x.float().contiguous()), w3, out_dtype=torch.float32)
+
+
+def linear_x3(x, linear):
+    """``linear(x)`` for fp32 x through ``mm_x3``; the bias, if any, is added in fp32."""
+    _cuda(x)
+    k = x.shape[-1]
+    _check(linear.weight.shape[1] == k, "x does not match the linear's input width")
+    w = x3_weight(linear, "x3", linear.weight)
+    y = mm_x3(x.reshape(-1, k), w)
+    if linear.bias is not None:
+        y += linear.bias.float()
+    return y.view(x.shape[:-1] + (w.shape[1],))
 
 
 MODULATION, GATE, GATED_SWIGLU = 0, 1, 3

@@ -78,6 +78,14 @@ int bmx_silu_mul(const void* a, const void* b, void* out, int64_t n, bmx_stream_
 int bmx_diffusion_epilogue(int kind, const void* a, const void* b, const void* c, void* out, int dtype, int64_t rows,
                            int64_t cols, bmx_stream_t stream);
 
+/* out[r] = [bf16(x[r]) | bf16(x[r]) | bf16(x[r] - bf16(x[r]))] (3k bf16 per row) for rows of k fp32
+ * values at row stride ldx (k and ldx multiples of 4; x 16-byte, out 8-byte aligned).  The activation
+ * operand of the near-fp32 linears: one bf16 GEMM of this against the weight rows
+ * [bf16(W) | bf16(W - bf16(W)) | bf16(W)] with fp32 accumulation gives x W up to about 2^-16 relative
+ * per product.  No reference counterpart: it serves fp32 linears that the reference leaves to
+ * hipBLASLt (the conditioned transition's a-path projections, diffusion.py:60-68). */
+int bmx_split3_bf16(const float* x, int64_t rows, int64_t k, int64_t ldx, void* out, bmx_stream_t stream);
+
 /* P = softmax(round(round(S + mask) + bias)) over the last axis, rounding to dtype.
  * shape = {B, I, H, Q, K}; element strides of scores [B,I,H,Q,K], bias [B,1,H,Q,K], mask [B,I,1,1,K].
  * out is contiguous.  Replaces ordered_softmax (kernels/triangle_softmax.py:117-161) and

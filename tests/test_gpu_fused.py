@@ -191,3 +191,29 @@ def test_adaln_modulate_widths_and_ragged_rows(gpu, dim):
     with torch.inference_mode():
         got = ops.adaln_modulate(a.to(gpu), scale.to(gpu), shift.to(gpu), 1e-5)
     assert errors(got, want)["max_rel"] < 1e-5
+
+
+@pytest.mark.parametrize("m,k,n,bias", [(37, 768, 3072, False), (1024, 384, 1536, True), (41, 128, 256, True),
+                                        (5, 1536, 768, False)])
+def test_linear_x3_is_near_fp32(gpu, m, k, n, bias):
+    """One bf16 GEMM of the split activation [xh | xh | xl] against the split
+    weight [Wh | Wl | Wh] (fp32 accumulation) against the fp64 product: the
+    dropped xl Wl term and the residues below the low parts leave about 2^-16
+    relative per product, far inside the fp32-mode tolerance of 1e-4."""
+    g = torch.Generator().manual_seed(m + k)
+    lin = torch.nn.Linear(k, n, bias=bias)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(n, k, generator=g) * 0.05)
+        if bias:
+            lin.bias.copy_(torch.randn(n, generator=g))
+    x = torch.randn(2, m, k, generator=g)
+    want = torch.nn.functional.linear(x.double(), lin.weight.double(), None if not bias else lin.bias.double())
+    lin = lin.to(gpu)
+    with torch.inference_mode():
+        got = ops.linear_x3(x.to(gpu), lin)
+        split = ops.split3(x[0].to(gpu).contiguous())
+    assert got.dtype == torch.float32 and got.shape == want.shape
+    assert errors(got, want)["max_rel"] < 2e-5
+    hi = x[0].bfloat16()
+    assert torch.equal(split[:, :k].cpu(), hi) and torch.equal(split[:, k:2 * k].cpu(), hi)
+    assert torch.equal(split[:, 2 * k:].cpu(), (x[0] - hi.float()).bfloat16())
