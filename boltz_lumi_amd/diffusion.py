@@ -6,11 +6,12 @@ Reference: src/boltz_lumi/diffusion.py (optimized_sample :13-23, adaln_forward
 AdaLN / transition forwards run in fp32 with autocast off.  AdaLN's a_norm + sigmoid(s_scale) modulation
 + s_bias become one LN/modulate kernel; the SwiGLU gate and the output gate
 are fused epilogues.  The conditioning projections are still called as
-submodules, so ``atom_conditioning_cache`` keeps working (reference
-atom_conditioning.py:12-45); the projections of the activation a (swish_gate,
-a_to_b, b_to_a), which the reference runs as fp32 hipBLASLt GEMMs, run as
-split-bf16 GEMMs with fp32 accumulation (``ops.linear_x3``, about 2^-16
-relative per product).  Guard failures call the class forward.
+submodules while ``atom_conditioning_cache`` memoises them (reference
+atom_conditioning.py:12-45); otherwise they and the projections of the
+activation a (swish_gate, a_to_b, b_to_a), all fp32 hipBLASLt GEMMs in the
+reference, run as split-bf16 GEMMs with fp32 accumulation from 512 input
+channels up (``ops.linear_fp32``, about 2^-16 relative per product).  Guard failures call
+the class forward.
 """
 
 from __future__ import annotations
@@ -47,12 +48,22 @@ def eligible(module, *tensors) -> bool:
         gfx950_tensor(t) and t.dtype == torch.float32 and t.is_contiguous() for t in tensors)
 
 
+def _linear(linear, x):
+    """``linear(x)`` for fp32 x: ``ops.linear_fp32`` (the split-bf16 GEMM with
+    fp32 accumulation from 512 input channels up), or the submodule call when
+    it has an instance-level forward, such as the memo of
+    ``atom_conditioning_cache``."""
+    if "forward" in vars(linear):
+        return linear(x).contiguous()
+    return ops.linear_fp32(x, linear).contiguous()
+
+
 def adaln_forward(self, a, s):
     """Drop-in for ``AdaLN.forward(a, s)``."""
     if not eligible(self, a, s) or a.shape[-1] % 4 or a.shape[-1] > 1024:
         return type(self).forward(self, a, s)
     sn = self.s_norm(s)
-    return ops.adaln_modulate(a, self.s_scale(sn).contiguous(), self.s_bias(sn).contiguous(), self.a_norm.eps)
+    return ops.adaln_modulate(a, _linear(self.s_scale, sn), _linear(self.s_bias, sn), self.a_norm.eps)
 
 
 def transition_forward(self, a, s):
@@ -60,10 +71,5 @@ def transition_forward(self, a, s):
     if not eligible(self, a, s):
         return type(self).forward(self, a, s)
     a = self.adaln(a, s)
-    if a.shape[-1] % 4:
-        b = ops.epilogue(self.swish_gate[0](a).contiguous(), self.a_to_b(a).contiguous(), None, ops.GATED_SWIGLU)
-        return ops.epilogue(self.output_projection[0](s).contiguous(), self.b_to_a(b).contiguous(), None, ops.GATE)
-    # The a-path projections as split-bf16 GEMMs with fp32 accumulation; the
-    # s-path output gate stays a submodule call (atom_conditioning_cache).
-    b = ops.epilogue(ops.linear_x3(a, self.swish_gate[0]), ops.linear_x3(a, self.a_to_b), None, ops.GATED_SWIGLU)
-    return ops.epilogue(self.output_projection[0](s).contiguous(), ops.linear_x3(b, self.b_to_a), None, ops.GATE)
+    b = ops.epilogue(_linear(self.swish_gate[0], a), _linear(self.a_to_b, a), None, ops.GATED_SWIGLU)
+    return ops.epilogue(_linear(self.output_projection[0], s), _linear(self.b_to_a, b), None, ops.GATE)

@@ -335,8 +335,8 @@ class AdaLN(nn.Module):
     def forward(self, a, s):
         _require_cuda(a, "AdaLN")
         sn = ops.layer_norm(s.contiguous(), self.s_norm.weight, None, self.s_norm.eps)
-        return ops.adaln_modulate(a.contiguous(), self.s_scale(sn).contiguous(), self.s_bias(sn).contiguous(),
-                                  self.a_norm.eps)
+        scale, shift = ops.linear_fp32(sn, self.s_scale), ops.linear_fp32(sn, self.s_bias)
+        return ops.adaln_modulate(a.contiguous(), scale.contiguous(), shift.contiguous(), self.a_norm.eps)
 
 
 class SwiGLU(nn.Module):
@@ -359,5 +359,7 @@ class ConditionedTransitionBlock(nn.Module):
 
     def forward(self, a, s):
         a = self.adaln(a, s)
-        b = ops.epilogue(ops.linear_x3(a, self.swish_gate[0]), ops.linear_x3(a, self.a_to_b), None, ops.GATED_SWIGLU)
-        return ops.epilogue(self.output_projection[0](s).contiguous(), ops.linear_x3(b, self.b_to_a), None, ops.GATE)
+        u, v = ops.linear_fp32(a, self.swish_gate[0]), ops.linear_fp32(a, self.a_to_b)
+        b = ops.epilogue(u.contiguous(), v.contiguous(), None, ops.GATED_SWIGLU)
+        g, y = ops.linear_fp32(s, self.output_projection[0]), ops.linear_fp32(b, self.b_to_a)
+        return ops.epilogue(g.contiguous(), y.contiguous(), None, ops.GATE)

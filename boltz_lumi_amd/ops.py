@@ -240,6 +240,21 @@ def mm_x3(x, w3):
     return torch.mm(split3(x.float().contiguous()), w3, out_dtype=torch.float32)
 
 
+# Narrower fp32 linears (the atom transformer's 128 / 256) measured faster on
+# hipBLASLt's fp32 GEMM than as split-bf16 GEMMs; from 512 up (the token
+# transformer's 768 / 1536) the split form is ~1.5x faster per block.
+X3_MIN_K = 512
+
+
+def linear_fp32(x, linear):
+    """``linear(x)`` for fp32 x: ``linear_x3`` for input widths >= X3_MIN_K
+    (multiples of 4), else the fp32 GEMM."""
+    k = x.shape[-1]
+    if k >= X3_MIN_K and k % 4 == 0:
+        return linear_x3(x, linear)
+    return torch.nn.functional.linear(x, linear.weight, linear.bias)
+
+
 def linear_x3(x, linear):
     """``linear(x)`` for fp32 x through ``mm_x3``; the bias, if any, is added in fp32."""
     _cuda(x)
