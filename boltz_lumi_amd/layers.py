@@ -216,7 +216,7 @@ class AttentionPairBias(nn.Module):
     def forward(self, s, z, mask, k_in, multiplicity=1):
         o = self.attend(s, z, mask, k_in, multiplicity)
         if o is not None:
-            return self.proj_o(o)
+            return self.proj_o(o) if torch.is_autocast_enabled() else ops.linear_fp32(o, self.proj_o)
         b = s.shape[0]
         q = self.proj_q(s).view(b, -1, self.num_heads, self.head_dim).transpose(1, 2)
         k = self.proj_k(k_in).view(b, -1, self.num_heads, self.head_dim).transpose(1, 2)

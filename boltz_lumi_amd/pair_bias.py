@@ -12,7 +12,9 @@ and the Pairformer trunk's AttentionPairBias runs as one kernel
 (``bmx_seq_attention_fwd``, 16 heads of 24 or 48 dims): the [B, H, N, N]
 logits never exist in HBM.  Projections stay on hipBLASLt; with
 ``k_in is s`` the four input projections are one GEMM whose column slices the
-kernel reads in place.
+kernel reads in place.  In fp32 at 512 channels and up (the token
+transformer's 768) the projections are split-bf16 GEMMs with fp32
+accumulation (``ops.mm_x3``, about 2^-16 relative per product).
 """
 
 from __future__ import annotations
@@ -47,11 +49,16 @@ def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
             and not module.training and not torch.is_grad_enabled()):
         return None
     if k_in is s:
-        w = ops.cached_weight(module, "qkvg", (module.proj_q.weight, module.proj_k.weight, module.proj_v.weight,
-                                               module.proj_g.weight), lambda *ws: torch.cat(ws, 0).float())
+        weights = (module.proj_q.weight, module.proj_k.weight, module.proj_v.weight, module.proj_g.weight)
         bq = ops.cached_weight(module, "qkvg_bias", (module.proj_q.bias,),
                                lambda b: torch.cat([b.float(), b.new_zeros(3 * width)]))
-        proj = F.linear(s if torch.is_autocast_enabled() else s.float(), w, bq).float()
+        if not torch.is_autocast_enabled() and width >= ops.X3_MIN_K and width % 4 == 0:
+            # fp32 at the token transformer's width: one split-bf16 GEMM with fp32 accumulation
+            proj = ops.mm_x3(s.reshape(-1, width), ops.x3_weight(module, "qkvg_x3", *weights)).add_(bq)
+            proj = proj.view(s.shape[:-1] + (4 * width,))
+        else:
+            w = ops.cached_weight(module, "qkvg", weights, lambda *ws: torch.cat(ws, 0).float())
+            proj = F.linear(s if torch.is_autocast_enabled() else s.float(), w, bq).float()
         q, k, v, g = proj.split(width, dim=-1)
     else:
         q, k, v, g = (t.float().contiguous() for t in (module.proj_q(s), module.proj_k(k_in), module.proj_v(k_in),
@@ -76,4 +83,6 @@ def prepared_forward(module, s, z, mask, k_in, multiplicity=1):
         o = fused_attention(module, s, z, mask, k_in, multiplicity)
     if o is None:
         return type(module).forward(module, s, z, mask, k_in, multiplicity)
-    return module.proj_o(o)
+    if torch.is_autocast_enabled() or "forward" in vars(module.proj_o):
+        return module.proj_o(o)
+    return ops.linear_fp32(o, module.proj_o)
