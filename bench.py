@@ -238,16 +238,19 @@ def token_attention_cpu(n: int):
 
 
 def diffusion(args):
-    """The diffusion score model's conditioning blocks at BASELINE configs[4]
-    shapes (5 samples; token transformer 1024 tokens x 768, atom transformer
-    8192 atoms x 128): AdaLN and ConditionedTransitionBlock forwards of one
-    layer of each transformer, fp32 as the reference runs them
-    (diffusion.py:37-68), plus the fused kernels alone (bmx_adaln, the
-    GATED_SWIGLU and GATE epilogues) against the 8 TB/s HBM roofline.  Bytes
-    per launch: AdaLN 16 M D (a, scale, shift in, out), GATED_SWIGLU 16 M Di
-    (u [M, 2 Di] and b in, out), GATE 12 M D."""
+    """The diffusion score model's per-layer modules at BASELINE configs[4]
+    shapes (5 samples; token transformer 1024 tokens x 768 with 16 heads,
+    atom transformer 8192 atoms x 128 with 4 heads in windows of 32 queries
+    over 128 keys): the AdaLN, AttentionPairBias (prepared_forward, the fused
+    batched attention) and ConditionedTransitionBlock forwards of one layer of
+    each transformer, fp32 as the reference runs them (diffusion.py:37-68,
+    pair_bias.py:15-36), plus the fused elementwise kernels alone (bmx_adaln,
+    the GATED_SWIGLU and GATE epilogues) against the 8 TB/s HBM roofline.
+    Bytes per launch: AdaLN 16 M D (a, scale, shift in, out), GATED_SWIGLU
+    16 M Di (u [M, 2 Di] and b in, out), GATE 12 M D."""
     import torch
     from boltz_lumi_amd import layers, ops
+    from boltz_lumi_amd.pair_bias import prepare_token_bias, prepared_forward
 
     dev = torch.device("cuda:0")
     samples = 5
@@ -266,19 +269,50 @@ def diffusion(args):
         return e0.elapsed_time(e1) / reps
 
     kernels, blocks = {}, {}
+    heads = {"token": 16, "atom": 4}
     modules = {name: (init_weights(layers.AdaLN(d, dc), 0).to(dev).eval(),
+                      init_weights(layers.AttentionPairBias(d, num_heads=heads[name], compute_pair_bias=False), 2)
+                      .to(dev).eval(),
                       init_weights(layers.ConditionedTransitionBlock(d, dc), 1).to(dev).eval())
                for name, (m, d, dc) in shapes.items()}
     with torch.inference_mode():
         for name, (m, d, dc) in shapes.items():
             di = 2 * d
-            adaln, ctb = modules[name]
+            adaln, apb, ctb = modules[name]
             a = torch.randn(m, d, generator=g).to(dev)
             c = torch.randn(m, dc, generator=g).to(dev)
+            if name == "token":  # 5 samples sharing one prepacked layer bias
+                qs = a.view(samples, args.n, d)
+                ks, mult = qs, samples
+                z = prepare_token_bias(torch.randn(1, args.n, args.n, heads[name], generator=g).to(dev))
+                kmask = torch.ones(samples, args.n, device=dev)
+            else:  # windows of 32 atoms over the 128 atoms centred on them (to_keys)
+                nw, w, h = 8192 // 32, 32, 128
+                index = torch.stack([torch.clamp(torch.arange(h) + w * i - (h - w) // 2, 0, 8191)
+                                     for i in range(nw)]).to(dev)
+                qs = a.view(samples * nw, w, d)
+                ks, mult = a.view(samples, 8192, d)[:, index].reshape(samples * nw, h, d), 1
+                z = torch.randn(samples * nw, heads[name], w, h, generator=g).to(dev).movedim(1, -1)
+                kmask = torch.ones(samples * nw, h, device=dev)
+
+            gate = init_weights(torch.nn.Linear(dc, d), 3).to(dev)
+
+            def layer():  # upstream DiffusionTransformerLayer.forward
+                b = adaln(a, c)
+                bq = b.view(qs.shape)
+                if name == "token":
+                    k_in = bq
+                else:
+                    k_in = b.view(samples, 8192, d)[:, index].reshape(samples * nw, h, d)
+                o = prepared_forward(apb, bq, z, kmask, k_in, mult).reshape(a.shape)
+                x = a + torch.sigmoid(ops.linear_fp32(c, gate)) * o
+                return x + ctb(x, c)
+
             for _ in range(args.warmup):
-                ctb(adaln(a, c), c)
+                layer()
             torch.cuda.synchronize()
-            blocks[name] = timed(lambda: ctb(adaln(a, c), c), args.steps)
+            blocks[name] = timed(layer, args.steps)
+            blocks[name + "_attention"] = timed(lambda: prepared_forward(apb, qs, z, kmask, ks, mult), args.steps)
             # Each kernel cycles over enough input sets that successive launches
             # do not find their operands in the 256 MB Infinity Cache.
             sets = 1 + (768 << 20) // (16 * m * d)
@@ -307,13 +341,14 @@ def diffusion(args):
     ms = blocks["token"] + blocks["atom"]
     dom = kernels["gated_swiglu_token"]
     out_line = {
-        "metric": "diffusion conditioning blocks (AdaLN + ConditionedTransitionBlock) ms per token + atom layer, "
-                  "5 samples; AdaLN/gating kernels % of HBM roofline",
+        "metric": "diffusion score-model modules (AdaLN + AttentionPairBias + ConditionedTransitionBlock) ms per "
+                  "token + atom layer, 5 samples; AdaLN/gating kernels % of HBM roofline",
         "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic (activations and conditioning ~ N(0,1); weights seeds 0 and 1)",
-        "config": {"workload": f"diffusion score-model AdaLN + ConditionedTransitionBlock forward, token layer "
-                               f"({samples} x {args.n} x 768) + atom layer ({samples} x 8192 x 128), "
+        "config": {"workload": f"diffusion score-model AdaLN + AttentionPairBias + ConditionedTransitionBlock "
+                               f"forwards, token layer ({samples} x {args.n} x 768, 16 heads, one shared bias) + "
+                               f"atom layer ({samples} x 8192 x 128, 4 heads, windows of 32 queries x 128 keys), "
                                f"BASELINE configs[4] shapes",
                    "n_tokens": args.n, "n_atoms": 8192, "samples": samples,
                    "block_ms": {k: round(v, 4) for k, v in blocks.items()}},
@@ -336,18 +371,25 @@ def diffusion_cpu(n: int):
     g = torch.Generator().manual_seed(0)
     total = 0.0
     with torch.inference_mode():
-        for m, d in ((n, 768), (8192, 128)):
-            adaln = init_weights(R.AdaLN(d, d), 0).eval()
-            ctb = init_weights(R.ConditionedTransitionBlock(d, d), 1).eval()
+        for m, d, heads in ((n, 768, 16), (8192, 128, 4)):
+            layer = init_weights(R.DiffusionTransformerLayer(heads, d, d), 0).eval()
             a, c = torch.randn(1, m, d, generator=g), torch.randn(1, m, d, generator=g)
-            ctb(adaln(a[:, :64], c[:, :64]), c[:, :64])
+            if d == 768:
+                z, mask, to_keys, a, c = torch.randn(1, m, m, heads, generator=g), torch.ones(1, m), None, a, c
+            else:  # windows of 32 atoms over the 128 atoms centred on them
+                nw, w, h = m // 32, 32, 128
+                index = torch.stack([torch.clamp(torch.arange(h) + w * i - (h - w) // 2, 0, m - 1) for i in range(nw)])
+                to_keys = lambda x: x.view(1, m, -1)[:, index].reshape(nw, h, -1)
+                z, mask = torch.randn(nw, w, h, heads, generator=g), torch.ones(nw, w)
+                a, c = a.view(nw, w, d), c.view(nw, w, d)
             t0 = time.perf_counter()
-            ctb(adaln(a, c), c)
+            layer(a, c, bias=z, mask=mask, to_keys=to_keys)
             total += time.perf_counter() - t0
     return {"value": round(total * 1e3 * 5, 1), "unit": "ms per token + atom layer, 5 samples (1 sample timed, x5)",
             "cores": cores, "kind": "port",
-            "sample": f"one sample of the fp32 CPU oracle AdaLN + ConditionedTransitionBlock (oracle/boltz_ref.py) "
-                      f"at {n} tokens x 768 and 8192 atoms x 128, {cores} threads, scaled x5"}
+            "sample": f"one sample of the fp32 CPU oracle DiffusionTransformerLayer (oracle/boltz_ref.py) at {n} "
+                      f"tokens x 768 (16 heads) and 8192 atoms x 128 (4 heads, 32 x 128 windows), {cores} threads, "
+                      f"scaled x5"}
 
 
 def main():

@@ -51,6 +51,7 @@ SIGNATURES = {
     "bmx_pair_transition_bias_fwd": (c_int, [_P, c_int, c_int64, _P, _P, c_float, _P, _P, _P, c_int, _P, c_float, _P,
                                              _P]),
     "bmx_seq_attention_fwd": (c_int, [_P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int, c_int, c_float, _P, _P]),
+    "bmx_seq_attention_batched_fwd": (c_int, [_P, _P, _P, _P, _P, _P] + [c_int64] * 10 + [c_int, c_int, c_float, _P, _P]),
 }
 
 

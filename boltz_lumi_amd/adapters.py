@@ -15,8 +15,9 @@ Patched (class name, path rule -> replacement):
   AdaLN / ConditionedTransitionBlock under
       "structure_module.score_model."              -> diffusion.adaln_forward / transition_forward
   AttentionPairBias under
-      "structure_module.score_model.token_transformer."
-                                                   -> pair_bias.prepared_forward
+      "structure_module.score_model."              -> pair_bias.prepared_forward
+      (the reference patches the token transformer's only, adapters.py:39-42;
+      the atom transformer's windowed ones run on the same fused kernel here)
   structure_module.sample                          -> diffusion.optimized_sample
 """
 
@@ -29,7 +30,6 @@ from ._guards import gfx950_available
 TRIANGLE_ATTENTION = {"TriangleAttention", "TriangleAttentionEndingNode"}
 TRIANGLE_MULTIPLICATION = {"TriangleMultiplicationIncoming", "TriangleMultiplicationOutgoing"}
 SCORE_MODEL = "structure_module.score_model."
-TOKEN_TRANSFORMER = SCORE_MODEL + "token_transformer."
 
 FLAG = "_bmx_optimized"
 
@@ -80,7 +80,7 @@ def install(model, *, require_boltz2: bool = True, require_device: bool = True):
         elif name.startswith(SCORE_MODEL) and cls == "ConditionedTransitionBlock":
             module.forward = MethodType(transition_forward, module)
             patched += 1
-        elif name.startswith(TOKEN_TRANSFORMER) and cls == "AttentionPairBias":
+        elif name.startswith(SCORE_MODEL) and cls == "AttentionPairBias":
             module.forward = MethodType(prepared_forward, module)
             patched += 1
     structure = getattr(model, "structure_module", None)

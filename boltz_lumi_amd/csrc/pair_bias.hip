@@ -92,39 +92,61 @@ __global__ __launch_bounds__(256) void pair_bias_kernel(const TIn* __restrict__ 
 constexpr int kAttnQ = 16, kAttnWaves = 4, kAttnStep = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Batched shapes: element b of grid.z attends its nq query rows (q, g at row
+// stride ldq, element stride sq) over its nk key rows (k, v at ldk, sk) with
+// bias element b / bdiv ([heads][nq][nk], element stride sbias; upstream
+// repeat_interleave(multiplicity)) and mask element b (stride smask, 0 to
+// broadcast one mask); out element b is [nq][heads * D] at stride nq * heads * D.
+struct SeqAttnShape {
+  int nq, nk, bdiv;
+  int64_t ldq, ldk, sq, sk, sbias, smask;
+};
+
 template <int D>
 __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                             const float* __restrict__ v,
                                                             const float* __restrict__ bias,
                                                             const float* __restrict__ mask,
-                                                            const float* __restrict__ g, int n, int64_t ld, int heads,
+                                                            const float* __restrict__ g, SeqAttnShape sh, int heads,
                                                             float inf, float rscale, bool vec,
                                                             float* __restrict__ out) {
   constexpr int KS = D / 4;          // QK^T MFMA steps
   constexpr int DT = (D + 15) / 16;  // O^T d tiles
   static_assert(D % 4 == 0, "head dim");
   const int HD = heads * D;
+  const int nq = sh.nq, nk = sh.nk;
+  const int64_t ldq = sh.ldq, ldk = sh.ldk;
+  {
+    const int64_t b = blockIdx.z;
+    q += b * sh.sq;
+    g += b * sh.sq;
+    k += b * sh.sk;
+    v += b * sh.sk;
+    bias += (b / sh.bdiv) * sh.sbias;
+    mask += b * sh.smask;
+    out += b * nq * HD;
+  }
   __shared__ float part_o[kAttnWaves][16 * DT][kAttnQ];
   __shared__ float part_m[kAttnWaves][kAttnQ], part_l[kAttnWaves][kAttnQ];
   const int h = blockIdx.y, q0 = blockIdx.x * kAttnQ;
   const int w = threadIdx.x >> 6, l = lane_id(), gi = l >> 4, c = l & 15;
-  const int qc = min(q0 + c, n - 1);  // rows past the end re-read the last one and are not stored
+  const int qc = min(q0 + c, nq - 1);  // rows past the end re-read the last one and are not stored
   float qf[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) qf[s] = q[(int64_t)qc * ld + h * D + KS * gi + s];
-  const float* brow = bias + ((int64_t)h * n + qc) * n;
+  for (int s = 0; s < KS; ++s) qf[s] = q[(int64_t)qc * ldq + h * D + KS * gi + s];
+  const float* brow = bias + ((int64_t)h * nq + qc) * nk;
   f32x4 o[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -3.4e38f, lsum = 0.f;
-  for (int key0 = w * kAttnStep; key0 < n; key0 += kAttnWaves * kAttnStep) {
-    const bool full = vec && key0 + kAttnStep <= n;
+  for (int key0 = w * kAttnStep; key0 < nk; key0 += kAttnWaves * kAttnStep) {
+    const bool full = vec && key0 + kAttnStep <= nk;
     f32x4 st[4];
     float tmax = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int kr = min(key0 + 16 * t + c, n - 1);
-      const float* krow = k + (int64_t)kr * ld + h * D + KS * gi;
+      const int kr = min(key0 + 16 * t + c, nk - 1);
+      const float* krow = k + (int64_t)kr * ldk + h * D + KS * gi;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s) acc = mfma16f32(krow[s], qf[s], acc);
@@ -136,14 +158,14 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          b4[r] = brow[min(kb + r, n - 1)];
-          m4[r] = mask[min(kb + r, n - 1)];
+          b4[r] = brow[min(kb + r, nk - 1)];
+          m4[r] = mask[min(kb + r, nk - 1)];
         }
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float x = (acc[r] * rscale + b4[r]) + (1.f - m4[r]) * -inf;
-        st[t][r] = kb + r < n ? x : -INFINITY;
+        st[t][r] = kb + r < nk ? x : -INFINITY;
         tmax = fmaxf(tmax, st[t][r]);
       }
     }
@@ -159,8 +181,8 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
       for (int s = 0; s < 4; ++s) {
         const float p = __builtin_amdgcn_exp2f((st[t][s] - mn) * kLog2e);
         lsum += p;
-        const int kr = min(key0 + 16 * t + 4 * gi + s, n - 1);
-        const float* vrow = v + (int64_t)kr * ld + h * D;
+        const int kr = min(key0 + 16 * t + 4 * gi + s, nk - 1);
+        const float* vrow = v + (int64_t)kr * ldk + h * D;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const int d = 16 * dt + c;
@@ -181,7 +203,7 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
   __syncthreads();
   // Merge: thread (query qi, dim group) finishes D / 16 dims per 16 threads.
   const int qi = threadIdx.x & 15, i = q0 + qi;
-  if (i < n) {
+  if (i < nq) {
     float mm = part_m[0][qi];
 #pragma unroll
     for (int u = 1; u < kAttnWaves; ++u) mm = fmaxf(mm, part_m[u][qi]);
@@ -195,10 +217,27 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
       float acc = 0.f;
 #pragma unroll
       for (int u = 0; u < kAttnWaves; ++u) acc += wt[u] * part_o[u][d][qi];
-      const float gate = sigmoid_f(g[(int64_t)i * ld + h * D + d]);
+      const float gate = sigmoid_f(g[(int64_t)i * ldq + h * D + d]);
       out[(int64_t)i * HD + h * D + d] = gate * (acc / ll);
     }
   }
+}
+
+int launch_seq_attention(const char* name, const float* q, const float* k, const float* v, const float* bias,
+                         const float* mask, const float* g, int64_t batch, const SeqAttnShape& sh, int heads,
+                         int head_dim, float inf, float* out, hipStream_t stream) {
+  // 16-byte bias / mask loads where every row start is aligned; scalar loads otherwise
+  const bool vec = sh.nk % 4 == 0 && sh.sbias % 4 == 0 && sh.smask % 4 == 0 && (uintptr_t)bias % 16 == 0 &&
+                   (uintptr_t)mask % 16 == 0;
+  const dim3 grid((unsigned)((sh.nq + kAttnQ - 1) / kAttnQ), (unsigned)heads, (unsigned)batch);
+  const float rscale = 1.f / sqrtf((float)head_dim);
+#define SEQ_ATTN(DIM) \
+  seq_attention_kernel<DIM><<<grid, 256, 0, stream>>>(q, k, v, bias, mask, g, sh, heads, inf, rscale, vec, out)
+  if (head_dim == 24) SEQ_ATTN(24);
+  else if (head_dim == 32) SEQ_ATTN(32);
+  else SEQ_ATTN(48);
+#undef SEQ_ATTN
+  return check_launch(name);
 }
 
 }  // namespace
@@ -233,15 +272,32 @@ int bmx_seq_attention_fwd(const float* q, const float* k, const float* v, const 
   BMX_REQUIRE(inf > 0.f, "bmx_seq_attention_fwd: inf must be positive");
   if (n == 0) return BMX_OK;
   BMX_REQUIRE(q && k && v && bias && mask && g && out, "bmx_seq_attention_fwd: null pointer");
-  // 16-byte bias / mask loads where every row start is aligned; scalar loads otherwise
-  const bool vec = n % 4 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)mask % 16 == 0;
-  const dim3 grid((unsigned)((n + kAttnQ - 1) / kAttnQ), (unsigned)heads);
-  const float rscale = 1.f / sqrtf((float)head_dim);
-  if (head_dim == 24)
-    seq_attention_kernel<24><<<grid, 256, 0, stream>>>(q, k, v, bias, mask, g, (int)n, ld, heads, inf, rscale, vec, out);
-  else
-    seq_attention_kernel<48><<<grid, 256, 0, stream>>>(q, k, v, bias, mask, g, (int)n, ld, heads, inf, rscale, vec, out);
-  return check_launch("bmx_seq_attention_fwd");
+  const SeqAttnShape sh{(int)n, (int)n, 1, ld, ld, 0, 0, 0, 0};
+  return launch_seq_attention("bmx_seq_attention_fwd", q, k, v, bias, mask, g, 1, sh, heads, head_dim, inf, out,
+                              stream);
+}
+
+int bmx_seq_attention_batched_fwd(const float* q, const float* k, const float* v, const float* bias,
+                                  const float* mask, const float* g, int64_t batch, int64_t nq, int64_t nk,
+                                  int64_t ldq, int64_t ldk, int64_t sq, int64_t sk, int64_t sbias, int64_t smask,
+                                  int64_t bias_div, int heads, int head_dim, float inf, float* out,
+                                  hipStream_t stream) {
+  BMX_REQUIRE(batch >= 0 && batch <= 65535, "bmx_seq_attention_batched_fwd: batch must be in [0, 65535]");
+  BMX_REQUIRE(nq >= 0 && nq <= (1 << 20) && nk >= 1 && nk <= (1 << 20),
+              "bmx_seq_attention_batched_fwd: need 0 <= nq <= 2^20 and 1 <= nk <= 2^20");
+  BMX_REQUIRE(head_dim == 24 || head_dim == 32 || head_dim == 48,
+              "bmx_seq_attention_batched_fwd: head_dim must be 24, 32 or 48 (got %d)", head_dim);
+  BMX_REQUIRE(heads >= 1 && heads <= 64, "bmx_seq_attention_batched_fwd: heads must be in [1, 64] (got %d)", heads);
+  BMX_REQUIRE(ldq >= (int64_t)heads * head_dim && ldk >= (int64_t)heads * head_dim,
+              "bmx_seq_attention_batched_fwd: row strides must be >= heads * head_dim");
+  BMX_REQUIRE(sq >= 0 && sk >= 0 && sbias >= 0 && smask >= 0 && bias_div >= 1,
+              "bmx_seq_attention_batched_fwd: strides must be >= 0 and bias_div >= 1");
+  BMX_REQUIRE(inf > 0.f, "bmx_seq_attention_batched_fwd: inf must be positive");
+  if (batch == 0 || nq == 0) return BMX_OK;
+  BMX_REQUIRE(q && k && v && bias && mask && g && out, "bmx_seq_attention_batched_fwd: null pointer");
+  const SeqAttnShape sh{(int)nq, (int)nk, (int)bias_div, ldq, ldk, sq, sk, sbias, smask};
+  return launch_seq_attention("bmx_seq_attention_batched_fwd", q, k, v, bias, mask, g, batch, sh, heads, head_dim,
+                              inf, out, stream);
 }
 
 }  // extern "C"

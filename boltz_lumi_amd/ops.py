@@ -513,6 +513,38 @@ def seq_attention(q, k, v, bias, mask, g, inf, out=None):
     return out
 
 
+def seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=1, out=None):
+    """``seq_attention`` for a batch in one launch (``bmx_seq_attention_batched_fwd``):
+    q, g [B, NQ, H * D] and k, v [B, NK, H * D] (D = 24, 32 or 48; unit column
+    stride; q and g share their strides, k and v theirs), bias
+    [B / bias_div, H, NQ, NK] with dense elements (element b uses bias
+    b // bias_div), mask [B or 1, NK] with unit stride.  Returns (or writes into
+    ``out``) a contiguous fp32 [B, NQ, H * D]."""
+    _cuda(q, k, v, bias, mask, g)
+    _check(q.dim() == 3 and k.dim() == 3 and bias.dim() == 4 and mask.dim() == 2, "expected 3-d q/k, 4-d bias, 2-d mask")
+    b, nq, width = q.shape
+    nk, heads = k.shape[1], bias.shape[1]
+    _check(width % heads == 0 and width // heads in (24, 32, 48), "expected H heads of 24, 32 or 48 dims")
+    _check(g.shape == q.shape and g.stride() == q.stride() and k.shape == (b, nk, width) and v.shape == k.shape
+           and v.stride() == k.stride(), "q / g and k / v must match in shape and strides")
+    for t in (q, k, v, g):
+        _check(t.dtype == torch.float32 and t.stride(2) == 1, "expected fp32 q / k / v / g with unit column stride")
+    _check(bias.dtype == torch.float32 and bias.shape[1:] == (heads, nq, nk) and bias.shape[0] * bias_div == b
+           and (bias.shape[0] == 0 or bias[0].is_contiguous()), "expected fp32 [B / bias_div, H, NQ, NK] dense bias")
+    _check(mask.dtype == torch.float32 and mask.shape[1] == nk and mask.shape[0] in (1, b) and mask.stride(1) == 1,
+           "expected an fp32 [B or 1, NK] mask")
+    if out is None:
+        out = torch.empty((b, nq, width), device=q.device, dtype=torch.float32)
+    _check(out.shape == (b, nq, width) and out.dtype == torch.float32 and out.is_contiguous(),
+           "out must be a contiguous fp32 [B, NQ, H * D]")
+    if b and nq:
+        N.call("bmx_seq_attention_batched_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(),
+               mask.data_ptr(), g.data_ptr(), b, nq, nk, q.stride(1), k.stride(1), q.stride(0), k.stride(0),
+               bias.stride(0), mask.stride(0) if mask.shape[0] > 1 else 0, bias_div, heads, width // heads,
+               float(inf), out.data_ptr(), _stream(q))
+    return out
+
+
 def adaln_modulate(a, scale, shift, eps):
     """``sigmoid(scale) * LN_noaffine(a) + shift`` in one pass."""
     _cuda(a, scale, shift)

@@ -7,12 +7,13 @@ Reference: src/boltz_lumi/pair_bias.py.
                               layer's [B, heads, Q, K] slice is dense.
   prepared_forward (:15-36)   the token transformer's AttentionPairBias
                               forward (installed at adapters.py:39-42).
-Here the logits / softmax / PV / gate part of both the token transformer's
-and the Pairformer trunk's AttentionPairBias runs as one kernel
-(``bmx_seq_attention_fwd``, 16 heads of 24 or 48 dims): the [B, H, N, N]
-logits never exist in HBM.  Projections stay on hipBLASLt; with
-``k_in is s`` the four input projections are one GEMM whose column slices the
-kernel reads in place.  In fp32 at 512 channels and up (the token
+Here the logits / softmax / PV / gate part of the token transformer's, the
+atom transformer's (windows of 32 queries over 128 ``to_keys`` rows) and the
+Pairformer trunk's AttentionPairBias runs as one kernel
+(``bmx_seq_attention_batched_fwd``, 24, 32 or 48 dims per head, every batch
+element in one launch): the [B, H, NQ, NK] logits never exist in HBM.
+Projections stay on hipBLASLt; with ``k_in is s`` the four input projections
+are one GEMM whose column slices the kernel reads in place.  In fp32 at 512 channels and up (the token
 transformer's 768) the projections are split-bf16 GEMMs with fp32
 accumulation (``ops.mm_x3``, about 2^-16 relative per product).
 """
@@ -37,17 +38,23 @@ def prepare_token_bias(value: torch.Tensor) -> torch.Tensor:
 
 def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
     """``sigmoid(proj_g(s)) * attention`` of an upstream-style AttentionPairBias
-    ``module`` before ``proj_o`` ([B, N, c_s], fp32), or None where the kernel
-    does not apply (CPU, grad, training, a head width other than 24 or 48).
+    ``module`` before ``proj_o`` ([B, NQ, c_s], fp32), or None where the kernel
+    does not apply (CPU, grad, training, a head width other than 24, 32 or 48,
+    shapes upstream would not broadcast the same way).
 
-    ``bias`` is ``module.proj_z(z)`` ([B, H, N, N]) when not given; batch
-    element i uses bias ``i // multiplicity`` (upstream ``repeat_interleave``,
-    pair_bias.py:26-27).  Under autocast the projections run in its dtype and
-    are widened to fp32 for the attention, as upstream does (:29-33)."""
+    ``bias`` is ``module.proj_z(z)`` ([B / multiplicity, H, NQ, NK]) when not
+    given; batch element i uses bias ``i // multiplicity`` (upstream
+    ``repeat_interleave``, pair_bias.py:26-27).  ``k_in`` may differ from ``s``
+    in length (the atom transformer's windows attend ``to_keys`` rows).  Under
+    autocast the projections run in its dtype and are widened to fp32 for the
+    attention, as upstream does (:29-33).  All batch elements run in one
+    launch."""
     heads, width = module.num_heads, module.c_s
-    if not (s.is_cuda and k_in.is_cuda and width % heads == 0 and width // heads in (24, 48) and heads <= 64
+    if not (s.is_cuda and k_in.is_cuda and s.dim() == 3 and k_in.dim() == 3 and k_in.shape[0] == s.shape[0]
+            and width % heads == 0 and width // heads in (24, 32, 48) and heads <= 64
             and not module.training and not torch.is_grad_enabled()):
         return None
+    batch, nq, nk = s.shape[0], s.shape[1], k_in.shape[1]
     if k_in is s:
         weights = (module.proj_q.weight, module.proj_k.weight, module.proj_v.weight, module.proj_g.weight)
         bq = ops.cached_weight(module, "qkvg_bias", (module.proj_q.bias,),
@@ -66,18 +73,24 @@ def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
     if bias is None:
         bias = module.proj_z(z)
     bias = bias.float()
+    if bias.dim() != 4 or bias.shape[0] * multiplicity != batch or tuple(bias.shape[1:]) != (heads, nq, nk):
+        return None
+    if not bias[0].is_contiguous():
+        bias = bias.contiguous()
     m = mask.float()
-    o = torch.empty(s.shape[:-1] + (width,), device=s.device, dtype=torch.float32)
-    for i in range(s.shape[0]):
-        mi = m[i if m.shape[0] > 1 else 0].contiguous()
-        ops.seq_attention(q[i], k[i], v[i], bias[i // multiplicity].contiguous(), mi, g[i], module.inf, out=o[i])
-    return o
+    if m.dim() != 2 or m.shape[1] != nk or m.shape[0] not in (1, batch):
+        return None
+    if m.stride(1) != 1:
+        m = m.contiguous()
+    return ops.seq_attention_batched(q, k, v, bias, m, g, module.inf, bias_div=multiplicity)
 
 
 def prepared_forward(module, s, z, mask, k_in, multiplicity=1):
-    """Drop-in for the token transformer's ``AttentionPairBias.forward``
-    (reference pair_bias.py:15-36); upstream forward under grad, in training,
-    for ``compute_pair_bias`` modules and where the kernel does not apply."""
+    """Drop-in for the score model's ``AttentionPairBias.forward`` (reference
+    pair_bias.py:15-36, installed there on the token transformer's; here also
+    on the atom transformer's windowed ones); upstream forward under grad, in
+    training, for ``compute_pair_bias`` modules and where the kernel does not
+    apply."""
     o = None
     if not (torch.is_grad_enabled() or module.training or module.compute_pair_bias):
         o = fused_attention(module, s, z, mask, k_in, multiplicity)

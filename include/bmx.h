@@ -189,6 +189,18 @@ int bmx_seq_attention_fwd(const float* q, const float* k, const float* v, const 
                           const float* g, int64_t n, int64_t ld, int heads, int head_dim, float inf, float* out,
                           bmx_stream_t stream);
 
+/* bmx_seq_attention_fwd over a batch of elements in one launch, with separate query and key
+ * counts (attention to other keys, as the atom transformer's windows: AttentionPairBias.forward
+ * with k_in != s) and head_dim D = 24, 32 or 48.  Element b: q, g [nq][heads * D] at row stride
+ * ldq, element stride sq; k, v [nk][heads * D] at ldk, sk; bias element b / bias_div ([heads][nq][nk]
+ * dense, element stride sbias; upstream repeat_interleave(multiplicity)); mask element b ([nk],
+ * stride smask, 0 to share one); out [batch][nq][heads * D] contiguous.  Replaces the same part of
+ * AttentionPairBias.forward (math as src/boltz_lumi/pair_bias.py:21-36). */
+int bmx_seq_attention_batched_fwd(const float* q, const float* k, const float* v, const float* bias, const float* mask,
+                                  const float* g, int64_t batch, int64_t nq, int64_t nk, int64_t ldq, int64_t ldk,
+                                  int64_t sq, int64_t sk, int64_t sbias, int64_t smask, int64_t bias_div, int heads,
+                                  int head_dim, float inf, float* out, bmx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -248,3 +248,60 @@ def test_seq_attention_head_dim_48_matches_fp64(gpu, heads, n):
     want = torch.sigmoid(gate.double()) * (torch.softmax(logits, -1) @ vh).transpose(0, 1).reshape(n, width)
     got = ops.seq_attention(*(t.to(gpu) for t in (q, k, v, bias, mask, gate)), 1e6)
     assert max_rel(got, want) < 1e-4
+
+
+def _gather_keys(x, index):
+    """[B, N, c] -> [B * NW, 128, c]: each window's 128 key rows (``to_keys``)."""
+    return x[:, index].reshape(-1, index.shape[1], x.shape[-1])
+
+
+@pytest.mark.parametrize("multiplicity,masked", [(1, False), (2, True)])
+def test_atom_window_attention_matches_upstream(gpu, multiplicity, masked):
+    """The atom transformer's windowed AttentionPairBias (4 heads x 32; windows
+    of 32 queries over 128 key rows chosen by ``to_keys``; bias per window,
+    shared by ``multiplicity`` samples) through prepared_forward, one batched
+    launch, against the fp32 upstream forward within 1e-4."""
+    import copy
+
+    from boltz_lumi_amd.pair_bias import prepared_forward
+
+    g = torch.Generator().manual_seed(40 + multiplicity)
+    ref = R.randomize(R.AttentionPairBias(128, num_heads=4, compute_pair_bias=False), generator=g).eval()
+    samples, n_atoms, w, h = 2 * multiplicity, 320, 32, 128
+    nw = n_atoms // w
+    # window i's keys: the 128 atoms centred on it, clamped to the structure
+    index = torch.stack([torch.clamp(torch.arange(h) + w * i - (h - w) // 2, 0, n_atoms - 1) for i in range(nw)])
+    a = torch.randn(samples, n_atoms, 128, generator=g)
+    s = a.view(samples * nw, w, 128)
+    k_in = _gather_keys(a, index)
+    bias = torch.randn(samples // multiplicity * nw, 4, w, h, generator=g)  # proj_z(z) of the windowed pair bias
+    mask = torch.ones(samples, n_atoms)
+    if masked:
+        mask[:, -17:] = 0
+    kmask = _gather_keys(mask[..., None], index)[..., 0]
+    with torch.no_grad():
+        want = ref(s, bias.movedim(1, -1), kmask, k_in, multiplicity=multiplicity)
+    mine = copy.deepcopy(ref).to(gpu)
+    with torch.no_grad():
+        got = prepared_forward(mine, s.to(gpu), bias.movedim(1, -1).to(gpu), kmask.to(gpu), k_in.to(gpu),
+                               multiplicity)
+    assert got.shape == want.shape
+    assert max_rel(got, want) < 1e-4
+
+
+def test_atom_window_attention_head_dim_32_matches_fp64(gpu):
+    """bmx_seq_attention_batched_fwd at head_dim 32 with NQ != NK, bias shared
+    by pairs of batch elements and one broadcast mask, against fp64."""
+    g = torch.Generator().manual_seed(32)
+    b, nq, nk, heads = 6, 32, 128, 4
+    width = heads * 32
+    q, gate = torch.randn(b, nq, width, generator=g), torch.randn(b, nq, width, generator=g)
+    k, v = torch.randn(b, nk, width, generator=g), torch.randn(b, nk, width, generator=g)
+    bias = torch.randn(b // 2, heads, nq, nk, generator=g)
+    mask = (torch.rand(1, nk, generator=g) > 0.2).float()
+    qh, kh, vh = (t.double().view(b, -1, heads, 32).transpose(1, 2) for t in (q, k, v))
+    logits = qh @ kh.transpose(-1, -2) / 32 ** 0.5 + bias.double().repeat_interleave(2, 0)
+    logits = logits + (1 - mask.double()[:, None, None]) * -1e6
+    want = torch.sigmoid(gate.double()) * (torch.softmax(logits, -1) @ vh).transpose(1, 2).reshape(b, nq, width)
+    got = ops.seq_attention_batched(*(t.to(gpu) for t in (q, k, v, bias, mask, gate)), 1e6, bias_div=2)
+    assert max_rel(got, want) < 1e-4
