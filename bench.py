@@ -24,6 +24,9 @@ import time
 
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+# Transcendental issue rate: one 64-lane v_exp_f32 per 8 cycles per SIMD
+# (probe on the box), 256 CUs x 4 SIMDs at 2.4 GHz.
+EXP_PER_SIMD_CYCLE, SIMDS, CLOCK_HZ = 64 / 8, 1024, 2.4e9
 
 
 def parse():
@@ -465,6 +468,16 @@ def main():
         "frac": d["frac"],
         "traffic": measured_traffic(dominant, n),
     }
+    if dominant == "triattn_core":
+        # Exp co-bound (H N^3 exponentials per direction): v_exp_f32 issues one
+        # wave instruction per 8 cycles per SIMD (measured on the box), and MFMA
+        # and VALU issue overlap little, so the core's issue floor is the sum.
+        exps = 4.0 * n ** 3
+        exp_ms = exps / (EXP_PER_SIMD_CYCLE * SIMDS * CLOCK_HZ) * 1e3
+        mfma_ms = table[dominant][0] / (PEAK_BF16_TFLOPS * 1e12) * 1e3
+        roofline["co_bound"] = {"exp_ms": round(exp_ms, 4), "mfma_ms": round(mfma_ms, 4),
+                                "issue_floor_ms": round(exp_ms + mfma_ms, 4),
+                                "issue_floor_frac": round((exp_ms + mfma_ms) / d["ms"], 4)}
     out = {
         "metric": "Pairformer layer ms @N=1024 bf16",
         "value": round(ms, 4),
