@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void pair_bias_kernel(const TIn* __restrict__ 
 //                              (rows past D are zero).
 // Every lane then holds whole columns (one query) of S and O^T, so the
 // running max and the rescale need only the xor-16 / xor-32 exchanges.
-constexpr int kAttnQ = 16, kAttnWaves = 4, kAttnStep = 64;
+constexpr int kAttnQ = 16, kAttnWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Batched shapes: element b of grid.z attends its nq query rows (q, g at row
@@ -102,7 +102,9 @@ struct SeqAttnShape {
   int64_t ldq, ldk, sq, sk, sbias, smask;
 };
 
-template <int D>
+// TILES 16-key tiles per wave and step: 4 (64 keys), or 2 for short key rows
+// (the atom transformer's 128 keys), so that all four waves get keys.
+template <int D, int TILES>
 __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                             const float* __restrict__ v,
                                                             const float* __restrict__ bias,
@@ -139,12 +141,13 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
 #pragma unroll
   for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -3.4e38f, lsum = 0.f;
-  for (int key0 = w * kAttnStep; key0 < nk; key0 += kAttnWaves * kAttnStep) {
-    const bool full = vec && key0 + kAttnStep <= nk;
-    f32x4 st[4];
+  constexpr int kStep = 16 * TILES;
+  for (int key0 = w * kStep; key0 < nk; key0 += kAttnWaves * kStep) {
+    const bool full = vec && key0 + kStep <= nk;
+    f32x4 st[TILES];
     float tmax = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < TILES; ++t) {
       const int kr = min(key0 + 16 * t + c, nk - 1);
       const float* krow = k + (int64_t)kr * ldk + h * D + KS * gi;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -176,7 +179,7 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[t] *= alpha;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < TILES; ++t) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const float p = __builtin_amdgcn_exp2f((st[t][s] - mn) * kLog2e);
@@ -231,11 +234,13 @@ int launch_seq_attention(const char* name, const float* q, const float* k, const
                    (uintptr_t)mask % 16 == 0;
   const dim3 grid((unsigned)((sh.nq + kAttnQ - 1) / kAttnQ), (unsigned)heads, (unsigned)batch);
   const float rscale = 1.f / sqrtf((float)head_dim);
-#define SEQ_ATTN(DIM) \
-  seq_attention_kernel<DIM><<<grid, 256, 0, stream>>>(q, k, v, bias, mask, g, sh, heads, inf, rscale, vec, out)
-  if (head_dim == 24) SEQ_ATTN(24);
-  else if (head_dim == 32) SEQ_ATTN(32);
-  else SEQ_ATTN(48);
+#define SEQ_ATTN(DIM, TILES) \
+  seq_attention_kernel<DIM, TILES><<<grid, 256, 0, stream>>>(q, k, v, bias, mask, g, sh, heads, inf, rscale, vec, out)
+  const bool short_keys = sh.nk <= kAttnWaves * 32;
+  if (head_dim == 24) SEQ_ATTN(24, 4);
+  else if (head_dim == 32 && short_keys) SEQ_ATTN(32, 2);
+  else if (head_dim == 32) SEQ_ATTN(32, 4);
+  else SEQ_ATTN(48, 4);
 #undef SEQ_ATTN
   return check_launch(name);
 }

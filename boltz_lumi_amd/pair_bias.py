@@ -36,6 +36,27 @@ def prepare_token_bias(value: torch.Tensor) -> torch.Tensor:
     return dense.movedim(1, -1)
 
 
+def _joint_projection(module, name, x, linears):
+    """``cat([lin(x) for lin in linears], -1)`` as one GEMM (fp32 result) with the
+    concatenated weights cached on ``module``: in the autocast dtype under
+    autocast, else fp32 (split-bf16 from ``ops.X3_MIN_K`` input channels up)."""
+    weights = tuple(lin.weight for lin in linears)
+    biases = [lin.bias for lin in linears]
+    bias = None
+    if any(b is not None for b in biases):
+        srcs = tuple(b for b in biases if b is not None)
+        bias = ops.cached_weight(module, name + "_bias", srcs, lambda *bs: torch.cat(
+            [b.float() if b is not None else lin.weight.new_zeros(lin.out_features, dtype=torch.float32)
+             for b, lin in zip(biases, linears)]))
+    if not torch.is_autocast_enabled() and x.shape[-1] >= ops.X3_MIN_K and x.shape[-1] % 4 == 0:
+        y = ops.mm_x3(x.reshape(-1, x.shape[-1]), ops.x3_weight(module, name + "_x3", *weights))
+        if bias is not None:
+            y += bias
+        return y.view(x.shape[:-1] + (y.shape[-1],))
+    w = ops.cached_weight(module, name, weights, lambda *ws: torch.cat(ws, 0).float())
+    return F.linear(x if torch.is_autocast_enabled() else x.float(), w, bias).float()
+
+
 def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
     """``sigmoid(proj_g(s)) * attention`` of an upstream-style AttentionPairBias
     ``module`` before ``proj_o`` ([B, NQ, c_s], fp32), or None where the kernel
@@ -67,9 +88,9 @@ def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
             w = ops.cached_weight(module, "qkvg", weights, lambda *ws: torch.cat(ws, 0).float())
             proj = F.linear(s if torch.is_autocast_enabled() else s.float(), w, bq).float()
         q, k, v, g = proj.split(width, dim=-1)
-    else:
-        q, k, v, g = (t.float().contiguous() for t in (module.proj_q(s), module.proj_k(k_in), module.proj_v(k_in),
-                                                        module.proj_g(s)))
+    else:  # q | g on the queries and k | v on the key rows, two GEMMs whose column slices the kernel reads
+        q, g = _joint_projection(module, "qg", s, (module.proj_q, module.proj_g)).split(width, dim=-1)
+        k, v = _joint_projection(module, "kv", k_in, (module.proj_k, module.proj_v)).split(width, dim=-1)
     if bias is None:
         bias = module.proj_z(z)
     bias = bias.float()
