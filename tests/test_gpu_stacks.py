@@ -136,3 +136,37 @@ def test_confidence_stack_runs_native(model, gpu, calls):
     # The sequence stack is not patched; under autocast it runs upstream's
     # own bf16 math, so only its finiteness is checked here.
     assert torch.isfinite(got_s).all()
+
+
+def test_batched_pair_modules_match_per_element_calls(model, gpu):
+    """Batch of two with different masks: every patched pair module loops over
+    the batch with one shared workspace, so element b of the batched call must
+    equal the call on element b alone, bit for bit, and both match upstream."""
+    layer = model.msa_module.layers[0].pairformer_layer
+    n = 72
+    z = torch.randn(2, n, n, 128, device=gpu) * 0.5
+    m = torch.ones(2, n, device=gpu)
+    m[0, -7:] = 0
+    m[1, :3] = 0
+    m[1, 40:45] = 0
+    pm = m[:, :, None] * m[:, None, :]
+    calls = {
+        "tri_mul_out": lambda mod, x, p: mod(x, p),
+        "tri_mul_in": lambda mod, x, p: mod(x, p),
+        "tri_att_start": lambda mod, x, p: mod(x, p, chunk_size=None),
+        "tri_att_end": lambda mod, x, p: mod(x, p, chunk_size=None),
+        "transition_z": lambda mod, x, p: mod(x),
+    }
+    with torch.inference_mode():
+        want = {k: f(getattr(layer, k), z, pm) for k, f in calls.items()}
+    adapters.install(model)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        for k, f in calls.items():
+            mod = getattr(layer, k)
+            got = f(mod, z, pm)
+            assert got.dtype == torch.bfloat16, k
+            for b in range(2):
+                alone = f(mod, z[b:b + 1].contiguous(), pm[b:b + 1].contiguous())
+                assert torch.equal(got[b], alone[0]), (k, b)
+                w = want[k][b].double()
+                assert ((got[b].double() - w).abs().max() / w.abs().max()).item() < TOL, (k, b)
