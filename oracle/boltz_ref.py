@@ -165,6 +165,33 @@ class TriangleAttention(nn.Module):
             out = out.transpose(-2, -3)
         return out
 
+    def forward_rows(self, x, mask, rows, chunk: int = 64):
+        """``forward(x, mask)`` restricted to the output pairs of the given
+        rows: ``[*, R, N, C]`` for the starting node (pairs ``(i, :)``) and
+        ``[*, N, R, C]`` for the ending node (pairs ``(:, i)``).  It is the
+        chunk path of :meth:`forward`, one selected row per chunk, with the
+        triangle bias (which needs all of ``x``) built from ``chunk`` rows of
+        ``x`` at a time, so no intermediate exceeds ``max(chunk, H) * N^2 * C``
+        elements."""
+        if mask is None:
+            mask = x.new_ones(x.shape[:-1])
+        if not self.starting:
+            x = x.transpose(-2, -3)
+            mask = mask.transpose(-1, -2)
+        n = x.shape[-3]
+        tri_bias = torch.cat(
+            [permute_final_dims(self.linear(self.layer_norm(x[..., s:s + chunk, :, :])), (2, 0, 1))
+             for s in range(0, n, chunk)], dim=-2).unsqueeze(-4)
+        mask_bias = (self.inf * (mask - 1))[..., :, None, None, :]
+        parts = []
+        for i in rows:
+            xi = self.layer_norm(x[..., i:i + 1, :, :])
+            parts.append(self.mha(xi, xi, tri_bias, mask_bias[..., i:i + 1, :, :, :], None))
+        out = torch.cat(parts, dim=-3)
+        if not self.starting:
+            out = out.transpose(-2, -3)
+        return out
+
 
 class TriangleAttentionEndingNode(TriangleAttention):
     def __init__(self, c_in, c_hidden, no_heads, inf=1e9):
@@ -211,6 +238,41 @@ class _TriangleMultiplication(nn.Module):
         else:
             x = torch.einsum("bkid,bkjd->bijd", a, b)
         return self.p_out(self.norm_out(x)) * self.g_out(x_in).sigmoid()
+
+    def _operands(self, x, mask):
+        x = self.norm_in(x)
+        x = self.p_in(x) * self.g_in(x).sigmoid()
+        return torch.chunk(_at_least_f32(x * mask.unsqueeze(-1)), 2, dim=-1)
+
+    def forward_rows(self, x, mask, rows, chunk: int = 256):
+        """``forward(x, mask)[..., rows, :, :]`` (output pairs ``(i, :)``,
+        ``i`` in ``rows``) without the ``N x N x 2C`` operands: the sum over
+        ``k`` runs over chunks of ``chunk`` tokens, each chunk's ``a`` / ``b``
+        computed from its slice of ``x`` by the same layers as
+        :meth:`forward` (outgoing: ``o_ijc = sum_k a_ikc b_jkc``, chunks of
+        ``j`` with every ``k``; incoming: ``o_ijc = sum_k a_kic b_kjc``, chunks
+        of ``k``).  Rows are gathered by slicing, and each intermediate holds
+        at most ``chunk * N * 2C`` elements."""
+        n = x.shape[-2]
+        x_rows = torch.cat([x[..., i:i + 1, :, :] for i in rows], dim=-3)
+        if self.outgoing:
+            a, _ = self._operands(x_rows, torch.cat([mask[..., i:i + 1, :] for i in rows], dim=-2))
+            parts = []
+            for start in range(0, n, chunk):
+                _, b = self._operands(x[..., start:start + chunk, :, :], mask[..., start:start + chunk, :])
+                parts.append(torch.einsum("bikd,bjkd->bijd", a, b))
+            o = torch.cat(parts, dim=-2)
+        else:
+            o = None
+            for start in range(0, n, chunk):
+                xs, ms = x[..., start:start + chunk, :, :], mask[..., start:start + chunk, :]
+                a, _ = self._operands(torch.cat([xs[..., i:i + 1, :] for i in rows], dim=-2),
+                                      torch.cat([ms[..., i:i + 1] for i in rows], dim=-1))
+                _, b = self._operands(xs, ms)
+                part = torch.einsum("bkid,bkjd->bijd", a, b)
+                o = part if o is None else o + part
+        x_in = self.norm_in(x_rows)
+        return self.p_out(self.norm_out(o)) * self.g_out(x_in).sigmoid()
 
 
 class TriangleMultiplicationOutgoing(_TriangleMultiplication):

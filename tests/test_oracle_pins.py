@@ -245,6 +245,46 @@ def test_triattn_chunking_does_not_change_math():
         assert _rel(m(x, mask, chunk_size=4), m(x, mask)) < 1e-6
 
 
+@pytest.mark.parametrize("starting", [True, False])
+def test_triattn_rows_are_rows_of_the_full_forward(starting):
+    """``forward_rows`` (the large-size checker) against the full forward,
+    in fp64, with masked rows among the selected ones."""
+    g = _gen(14)
+    m = R.randomize(R.TriangleAttention(16, 8, 2, starting=starting), generator=g).double()
+    n = 13
+    x = torch.randn(1, n, n, 16, generator=g, dtype=torch.float64)
+    tok = torch.ones(n, dtype=torch.float64)
+    tok[[2, 11]] = 0
+    mask = (tok[:, None] * tok[None, :])[None]
+    mask[0, 4, 6] = 0  # asymmetric
+    rows = [0, 2, 7, 12]
+    with torch.no_grad():
+        full = m(x, mask)
+        part = m.forward_rows(x, mask, rows, chunk=5)  # ragged last chunk
+    want = full[:, rows] if starting else full[:, :, rows]
+    assert part.shape == want.shape
+    assert _rel(part, want) < 1e-13
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_trimul_rows_are_rows_of_the_full_forward(outgoing):
+    """``forward_rows`` sums over k in chunks (here 4 tokens, the last one
+    ragged) with each chunk's operands computed separately; fp64 against
+    the full forward."""
+    g = _gen(15)
+    cls = R.TriangleMultiplicationOutgoing if outgoing else R.TriangleMultiplicationIncoming
+    m = R.randomize(cls(16), generator=g).double()
+    n = 11
+    x = torch.randn(1, n, n, 16, generator=g, dtype=torch.float64)
+    mask = (torch.rand(1, n, n, generator=g) > 0.25).double()
+    rows = [1, 5, 10]
+    with torch.no_grad():
+        want = m(x, mask)[:, rows]
+        part = m.forward_rows(x, mask, rows, chunk=4)
+    assert part.shape == want.shape
+    assert _rel(part, want) < 1e-13
+
+
 # ---------------------------------------------------------------- transition
 
 
