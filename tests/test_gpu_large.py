@@ -88,3 +88,28 @@ def test_trimul_largest_sizes(gpu, n, outgoing):
         want = m.forward_rows(x[None], mask[None], rows, chunk=64)[0]
     assert ok
     assert max_rel(got, want) < TOL
+
+
+def test_pair_transition_largest_size(gpu):
+    """N = 8191: 67,092,481 pair rows, the last 64-row tile holding one row.
+    The transition is per pair, so the oracle on the sampled rows alone is the
+    oracle's output there; the in-place fp32 accumulate mode is checked on the
+    same rows."""
+    n = 8191
+    print(f"pair_transition n={n}", flush=True)
+    torch.manual_seed(3)
+    m = R.randomize(R.Transition(128, 512)).to(gpu).eval()
+    x, _, rows = inputs(n, gpu)
+    with torch.inference_mode():
+        want = torch.stack([m(x[i]) for i in rows])
+        out = ops.pair_transition(m, x)
+        got = pick(out, rows)
+        ok = finite(out)
+        del out
+        torch.cuda.empty_cache()
+        base = pick(x, rows)
+        ops.pair_transition(m, x, ops.OUT_ACCUMULATE, out=x)  # x += transition(x), in place
+        res = pick(x, rows)
+    assert ok
+    assert max_rel(got, want) < TOL
+    assert max_rel(res - base, want) < TOL
