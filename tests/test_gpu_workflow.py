@@ -94,6 +94,22 @@ def test_ab_benchmark_report(model, gpu, tmp_path, monkeypatch):
     assert report["saved_s"] == pytest.approx(report["upstream_warm_mean_s"] - report["optimized_warm_mean_s"])
 
 
+def test_ab_benchmark_profiled_round(model, gpu, tmp_path):
+    """``profile=True`` adds one optimized round under torch.profiler: its calls
+    are marked profiled and left out of the warm means; the Chrome trace and
+    the GPU self-time table are written next to timings.json."""
+    report = ab_benchmark(model, step, candidates(gpu)[:1], repeats=1, fields=FIELDS, output=tmp_path,
+                          profile=True)
+    assert report["status"] == "complete"
+    profiled = [c for c in report["model_calls"] if c["profiled"]]
+    assert [(c["recipe"], c["iteration"]) for c in profiled] == [("optimized", 2)]
+    warm = [c["model_s"] for c in report["model_calls"] if c["recipe"] == "optimized" and c["iteration"] == 1]
+    assert report["optimized_warm_mean_s"] == pytest.approx(warm[0])
+    assert json.loads((tmp_path / "trace.json").read_text())["traceEvents"]
+    table = (tmp_path / "profile.txt").read_text().splitlines()
+    assert table[0].startswith("Operator or kernel") and len(table) > 1
+
+
 def test_ab_benchmark_flags_differences_and_failures(model, gpu, tmp_path):
     def shifted(m, batch):
         out = step(m, batch)
