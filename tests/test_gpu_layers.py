@@ -316,7 +316,9 @@ def test_trunk_error_does_not_compound(gpu):
     path's and under 2e-2, and the native s (fp32 sequence stack) stays under
     2e-2 where the bf16-mixed s exceeds it by the third block.  Measured on
     the box: z 0.0056 -> 0.0117 native against 0.0067 -> 0.0129 upstream bf16,
-    s 3.7e-4 against 2.8e-2 at the fourth block."""
+    s 3.7e-4 against 2.8e-2 at the fourth block.  A distogram-style head on
+    the output keeps the fp32 argmax bin on at least as many pairs as the
+    bf16-mixed path does."""
     torch.manual_seed(5)
     n, blocks = 96, 4
     refs = [R.randomize(R.PairformerLayer()).to(gpu).eval() for _ in range(blocks)]
@@ -345,3 +347,19 @@ def test_trunk_error_does_not_compound(gpu):
     for (ez, es), (mz, _) in zip(errs, mixed):
         assert ez < 2e-2 and es < 2e-2, errs
         assert ez <= 1.25 * mz, (errs, mixed)
+    # Argmax structure: a distogram-style head (64 bins over z + z^T, as
+    # upstream's DistogramModule) on the trunk output; the share of pairs whose
+    # argmax bin matches the fp32 path.
+    head = torch.nn.Linear(128, 64).to(gpu)
+    torch.nn.init.normal_(head.weight, std=0.08)
+
+    def bins(zz):
+        with torch.inference_mode():
+            return head((zz + zz.transpose(1, 2)).float()).argmax(-1)
+
+    ref_bins = bins(z_ref)
+    agree_native = (bins(z_got) == ref_bins).float().mean().item()
+    agree_mixed = (bins(z_mix) == ref_bins).float().mean().item()
+    print(f"distogram argmax agreement with fp32: native {agree_native:.4f}, upstream bf16 {agree_mixed:.4f}",
+          flush=True)
+    assert agree_native >= 0.97 and agree_native >= agree_mixed - 0.005  # measured 0.9888 and 0.9824
