@@ -69,3 +69,21 @@ def test_pair_transition_tile_edges(gpu, n):
         ops.pair_transition(m, acc, ops.OUT_ACCUMULATE, out=acc)
     assert max_rel(got, want) < TOL
     assert max_rel(acc - x, want) < TOL
+
+
+@pytest.mark.parametrize("n", [17, 65, 130])
+@pytest.mark.parametrize("starting", [True, False])
+def test_triattn_bf16_input(gpu, n, starting):
+    """bf16 x (the kernels' second input type) against the oracle on the same
+    bf16-rounded values, and the fp32 result modes on that input."""
+    g, x, mask = case(n, gpu)
+    xb = x.bfloat16()
+    m = R.randomize(R.TriangleAttention(128, 32, 4, starting=starting), generator=g).to(gpu).eval()
+    with torch.inference_mode():
+        want = m(xb.float()[None], mask[None])[0]
+        got = ops.triattn(m, xb, mask, starting)
+        got32 = ops.triattn(m, xb, mask, starting, ops.OUT_F32)
+    assert got.dtype == torch.bfloat16 and got32.dtype == torch.float32
+    assert max_rel(got, want) < TOL
+    assert max_rel(got32, want) < TOL
+    assert torch.equal(got32.bfloat16(), got)
