@@ -87,3 +87,43 @@ def test_triattn_bf16_input(gpu, n, starting):
     assert max_rel(got, want) < TOL
     assert max_rel(got32, want) < TOL
     assert torch.equal(got32.bfloat16(), got)
+
+
+@pytest.mark.parametrize("n", [65, 129])
+@pytest.mark.parametrize("op", ["trimul_out", "trimul_in", "triattn_start", "triattn_end", "transition"])
+def test_output_modes_are_exact_compositions(gpu, n, op):
+    """Every result mode of an op is its fp32 result y composed with fp32 adds:
+    bf16 = bf16(y) (y already holds bf16 values), residual out = x + y,
+    accumulate into another buffer out += y, accumulate in place x += y."""
+    g, x, mask = case(n, gpu)
+    if op.startswith("trimul"):
+        outgoing = op == "trimul_out"
+        cls = R.TriangleMultiplicationOutgoing if outgoing else R.TriangleMultiplicationIncoming
+        m = R.randomize(cls(128), generator=g).to(gpu).eval()
+
+        def run(xx, mode, out=None):
+            return ops.trimul(m, xx, mask, outgoing, mode, out)
+    elif op.startswith("triattn"):
+        starting = op == "triattn_start"
+        m = R.randomize(R.TriangleAttention(128, 32, 4, starting=starting), generator=g).to(gpu).eval()
+
+        def run(xx, mode, out=None):
+            return ops.triattn(m, xx, mask, starting, mode, out)
+    else:
+        m = R.randomize(R.Transition(128, 512), generator=g).to(gpu).eval()
+
+        def run(xx, mode, out=None):
+            return ops.pair_transition(m, xx, mode, out)
+
+    with torch.inference_mode():
+        y = run(x, ops.OUT_F32)
+        assert torch.equal(run(x, ops.OUT_BF16), y.bfloat16())
+        assert torch.equal(y.bfloat16().float(), y)
+        assert torch.equal(run(x, ops.OUT_RESIDUAL, torch.empty_like(x)), x + y)
+        other = torch.randn(x.shape, generator=g).to(gpu)
+        want = other + y
+        run(x, ops.OUT_ACCUMULATE, other)
+        assert torch.equal(other, want)
+        xi = x.clone()
+        run(xi, ops.OUT_ACCUMULATE, xi)
+        assert torch.equal(xi, x + y)
