@@ -39,6 +39,8 @@ SIGNATURES = {
     "bmx_trimul_workspace_bytes": (c_size_t, [c_int64]),
     "bmx_trimul_fwd": (c_int, [_P, _P, c_int64, c_int, _P, _P, c_float, _P, _P, _P, c_float, _P, _P, _P, c_int, _P,
                                c_size_t, c_int, _P]),
+    "bmx_trimul_fwd_noalloc": (c_int, [_P, _P, c_int64, c_int, _P, _P, c_float, _P, _P, _P, c_float, _P, _P, _P,
+                                       c_int, _P]),
     "bmx_triattn_workspace_bytes": (c_size_t, [c_int64]),
     "bmx_triattn_proj_rows": (c_int, []),
     "bmx_triattn_fwd": (c_int, [_P, c_int, _P, c_int64, c_int, c_float, _P, _P, c_float, _P, _P, _P, _P, _P, _P, c_int,

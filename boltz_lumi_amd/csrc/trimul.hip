@@ -20,6 +20,8 @@
 // so outgoing O = sum_k a[i,k] b[j,k] and incoming O = sum_k a[k,i] b[k,j]
 // (the reference's bmm operands, multiplication.py:105-116).  Padding columns
 // t >= n are written as zeros, so K2 runs unguarded over np.
+#include <mutex>
+
 #include "bmx_common.h"
 
 using namespace bmx;
@@ -437,36 +439,12 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
-}  // namespace
-
-extern "C" {
-
-size_t bmx_trimul_workspace_bytes(int64_t n) {
-  if (n <= 0) return 0;
-  int64_t np = round_up(n, kPlaneTile);
-  return (size_t)(3 * (int64_t)kC * np * np * (int64_t)sizeof(bf16));
-}
-
-int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, const float* norm_in_w,
-                   const float* norm_in_b, float eps_in, const void* w_in, const float* norm_out_w,
-                   const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
-                   int out_mode, void* workspace, size_t workspace_bytes, int stages, hipStream_t stream) {
-  BMX_REQUIRE(n >= 0 && n <= 16384, "bmx_trimul_fwd: n must be in [0, 16384] (got %lld)", (long long)n);
-  BMX_REQUIRE(out_mode >= 0 && out_mode <= 3,
-              "bmx_trimul_fwd: out_mode must be 0 (bf16), 1 (fp32), 2 (fp32 +=) or 3 (fp32 x + y)");
-  BMX_REQUIRE(stages >= 1 && stages <= 7, "bmx_trimul_fwd: stages must be a non-empty subset of 1|2|4");
-  BMX_REQUIRE(eps_in > 0.f && eps_out > 0.f, "bmx_trimul_fwd: eps must be positive");
-  if (n == 0) return BMX_OK;
-  BMX_REQUIRE(x && mask && norm_in_w && norm_in_b && w_in && norm_out_w && norm_out_b && w_pout && w_gout && out,
-              "bmx_trimul_fwd: null pointer");
-  BMX_REQUIRE(workspace && workspace_bytes >= bmx_trimul_workspace_bytes(n),
-              "bmx_trimul_fwd: workspace too small (%zu < %zu bytes)", workspace_bytes,
-              bmx_trimul_workspace_bytes(n));
-  BMX_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)workspace % 16 == 0 && (uintptr_t)w_in % 16 == 0 &&
-                  (uintptr_t)w_pout % 16 == 0 && (uintptr_t)w_gout % 16 == 0,
-              "bmx_trimul_fwd: x, weights and workspace must be 16-byte aligned");
-  const int ni = (int)n;
-  const int np = (int)round_up(n, kPlaneTile);
+// The three kernels of one module on `workspace` (3 planes of 128 x np x np bf16).
+int launch(const float* x, const float* mask, int ni, int outgoing, const float* norm_in_w, const float* norm_in_b,
+           float eps_in, const bf16* w_in, const float* norm_out_w, const float* norm_out_b, float eps_out,
+           const bf16* w_pout, const bf16* w_gout, void* out, int out_mode, void* workspace, int stages,
+           hipStream_t stream) {
+  const int np = (int)round_up(ni, kPlaneTile);
   const int64_t plane = (int64_t)np * np * kC;
   bf16* a_pl = (bf16*)workspace;
   bf16* b_pl = a_pl + plane;
@@ -475,8 +453,8 @@ int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, c
   if (stages & 1) {
     const int total = np * (np / kP1);
     const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
-    trimul_proj_kernel<<<dim3(grid), 256, 0, stream>>>(x, mask, norm_in_w, norm_in_b, eps_in, (const bf16*)w_in,
-                                                       a_pl, b_pl, ni, np, outgoing);
+    trimul_proj_kernel<<<dim3(grid), 256, 0, stream>>>(x, mask, norm_in_w, norm_in_b, eps_in, w_in, a_pl, b_pl, ni,
+                                                       np, outgoing);
     if (int rc = check_launch("trimul_proj")) return rc;
   }
   if (stages & 2) {
@@ -492,12 +470,118 @@ int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, c
   if (stages & 4) {
     const int total = ni * ((ni + kP3 - 1) / kP3);
     const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
-    trimul_out_kernel<<<dim3(grid), 256, 0, stream>>>(
-        x, o_pl, norm_in_w, norm_in_b, eps_in, norm_out_w, norm_out_b, eps_out, (const bf16*)w_pout,
-        (const bf16*)w_gout, out, out_mode, ni, np);
+    trimul_out_kernel<<<dim3(grid), 256, 0, stream>>>(x, o_pl, norm_in_w, norm_in_b, eps_in, norm_out_w, norm_out_b,
+                                                      eps_out, w_pout, w_gout, out, out_mode, ni, np);
     if (int rc = check_launch("trimul_out")) return rc;
   }
   return BMX_OK;
+}
+
+// Checks shared by both entry points (everything but the workspace).
+int check_args(const char* fn, const float* x, const float* mask, int64_t n, int64_t max_n, const float* norm_in_w,
+               const float* norm_in_b, float eps_in, const void* w_in, const float* norm_out_w,
+               const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, const void* out,
+               int out_mode) {
+  BMX_REQUIRE(n >= 0 && n <= max_n, "%s: n must be in [0, %lld] (got %lld)", fn, (long long)max_n, (long long)n);
+  BMX_REQUIRE(out_mode >= 0 && out_mode <= 3, "%s: out_mode must be 0 (bf16), 1 (fp32), 2 (fp32 +=) or 3 (fp32 x + y)",
+              fn);
+  BMX_REQUIRE(eps_in > 0.f && eps_out > 0.f, "%s: eps must be positive", fn);
+  if (n == 0) return BMX_OK;
+  BMX_REQUIRE(x && mask && norm_in_w && norm_in_b && w_in && norm_out_w && norm_out_b && w_pout && w_gout && out,
+              "%s: null pointer", fn);
+  BMX_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)w_in % 16 == 0 && (uintptr_t)w_pout % 16 == 0 &&
+                  (uintptr_t)w_gout % 16 == 0,
+              "%s: x and weights must be 16-byte aligned", fn);
+  return BMX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant.  Its operand planes live in `scratch`, a static
+// device array that every GPU the library runs on holds for the life of the
+// process.  Host code never passes `scratch` itself (in host code the name is
+// a host-side stand-in, not a device address): the device address is looked
+// up once per device with hipGetSymbolAddress, with that device current, and
+// kept in g_scratch.
+constexpr int kNoAllocMaxN = 256;
+constexpr size_t kScratchBytes = (size_t)3 * kC * kNoAllocMaxN * kNoAllocMaxN * sizeof(bf16);  // 48 MiB
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices] = {};
+
+}  // namespace
+
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+namespace {
+
+// Device address of this device's `scratch` (looked up on the first call on
+// the device), or nullptr with the error set.
+void* scratch_address(int* rc) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *rc = set_error(BMX_ELAUNCH, "bmx_trimul_fwd_noalloc: no usable current device (%s)", hipGetErrorString(e));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      *rc = set_error(BMX_ELAUNCH, "bmx_trimul_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                      hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch[dev] = ptr;
+  }
+  return g_scratch[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t bmx_trimul_workspace_bytes(int64_t n) {
+  if (n <= 0) return 0;
+  int64_t np = round_up(n, kPlaneTile);
+  return (size_t)(3 * (int64_t)kC * np * np * (int64_t)sizeof(bf16));
+}
+
+int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, const float* norm_in_w,
+                   const float* norm_in_b, float eps_in, const void* w_in, const float* norm_out_w,
+                   const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
+                   int out_mode, void* workspace, size_t workspace_bytes, int stages, hipStream_t stream) {
+  const char* fn = "bmx_trimul_fwd";
+  BMX_REQUIRE(stages >= 1 && stages <= 7, "bmx_trimul_fwd: stages must be a non-empty subset of 1|2|4");
+  if (int rc = check_args(fn, x, mask, n, 16384, norm_in_w, norm_in_b, eps_in, w_in, norm_out_w, norm_out_b, eps_out,
+                          w_pout, w_gout, out, out_mode))
+    return rc;
+  if (n == 0) return BMX_OK;
+  BMX_REQUIRE(workspace && workspace_bytes >= bmx_trimul_workspace_bytes(n),
+              "bmx_trimul_fwd: workspace too small (%zu < %zu bytes)", workspace_bytes,
+              bmx_trimul_workspace_bytes(n));
+  BMX_REQUIRE((uintptr_t)workspace % 16 == 0, "bmx_trimul_fwd: workspace must be 16-byte aligned");
+  return launch(x, mask, (int)n, outgoing, norm_in_w, norm_in_b, eps_in, (const bf16*)w_in, norm_out_w, norm_out_b,
+                eps_out, (const bf16*)w_pout, (const bf16*)w_gout, out, out_mode, workspace, stages, stream);
+}
+
+int bmx_trimul_fwd_noalloc(const float* x, const float* mask, int64_t n, int outgoing, const float* norm_in_w,
+                           const float* norm_in_b, float eps_in, const void* w_in, const float* norm_out_w,
+                           const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
+                           int out_mode, hipStream_t stream) {
+  const char* fn = "bmx_trimul_fwd_noalloc";
+  if (int rc = check_args(fn, x, mask, n, kNoAllocMaxN, norm_in_w, norm_in_b, eps_in, w_in, norm_out_w, norm_out_b,
+                          eps_out, w_pout, w_gout, out, out_mode))
+    return rc;
+  if (n == 0) return BMX_OK;
+  int rc = BMX_OK;
+  void* ws = scratch_address(&rc);
+  if (ws == nullptr) return rc;
+  // The projection writes every element of the A and B planes (padding as
+  // zeros) and the contraction every element of O, so nothing left in the
+  // scratch by an earlier call is read: no clearing is needed.
+  return launch(x, mask, (int)n, outgoing, norm_in_w, norm_in_b, eps_in, (const bf16*)w_in, norm_out_w, norm_out_b,
+                eps_out, (const bf16*)w_pout, (const bf16*)w_gout, out, out_mode, ws, 7, stream);
 }
 
 }  // extern "C"

@@ -114,6 +114,20 @@ int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, c
                    const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
                    int out_mode, void* workspace, size_t workspace_bytes, int stages, bmx_stream_t stream);
 
+/* bmx_trimul_fwd (all three stages) with no workspace argument and no allocation: the operand
+ * planes live in a static device array of the library (48 MiB = 3 planes of 128 x 256 x 256 bf16,
+ * held on every GPU the library runs on until the process ends), so n must be <= 256; larger n is
+ * rejected with BMX_EINVAL before any launch.  The first call on a device looks the array's device
+ * address up (hipGetSymbolAddress), so make one call per device before capturing it into a HIP graph.
+ * Calls that overlap on one GPU (other streams, other threads) share the array and race; serialise
+ * them.  Nothing left in the array by an earlier call is read.
+ * No counterpart in the reference: it serves callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int bmx_trimul_fwd_noalloc(const float* x, const float* mask, int64_t n, int outgoing, const float* norm_in_w,
+                           const float* norm_in_b, float eps_in, const void* w_in, const float* norm_out_w,
+                           const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
+                           int out_mode, bmx_stream_t stream);
+
 /* Workspace needed by bmx_triattn_fwd (bytes). */
 size_t bmx_triattn_workspace_bytes(int64_t n);
 
