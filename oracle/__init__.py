@@ -11,9 +11,6 @@ Contents
                lauritsf/boltz-lumi patches (same class names, parameter names
                and shapes, so state dicts move between the oracle and real
                Boltz modules).
-``mixed``      the same math with Boltz's bf16-mixed (autocast) rounding points
-               made explicit, used to report how far Boltz's own bf16 path
-               sits from fp32.
 ``brute``      fp64 pure-Python loop versions for tiny sizes; they pin the
                vectorised restatement.
 
@@ -33,8 +30,23 @@ Pinning status (each function's pin lives in ``tests/test_oracle_pins.py``):
 * AdaLN / ConditionedTransitionBlock / SwiGLU: fp64 loops, zero-weight closed
   forms, the reference epilogue formulas (``diffusion_hip.cu:14-27``).
 * AttentionPairBias: fp64 loops (math restated from ``pair_bias.py:21-36``).
-* PairformerLayer: composition order and the fp32 s-stack are **parity
-  unpinned** (only an import of upstream Boltz could pin them; the reference
-  corroborates them at ``multiplication.py:59``, ``triangle.py:113`` and
-  ``adapters.py:39-45``).  Its sub-blocks are pinned as above.
+* AttentionPairBias with the bias given directly (diffusion transformers,
+  separate key rows, multiplicity): fp64 loops (``brute.attention_pair_bias_keys``).
+* PairformerLayer: branch isolation (every pair branch but one silenced gives
+  ``z + branch(z)`` of the fp64 loop module), chained branches (the second
+  reads the z the first updated), the sequence stack on the updated z by fp64
+  loops, and the sequence stack in fp32 under bf16 autocast.  The op order
+  itself is a restatement of upstream (only an import of upstream Boltz could
+  show it); the reference corroborates it at ``multiplication.py:59``,
+  ``triangle.py:113`` and ``adapters.py:39-45``.
+* PairformerNoSeqLayer: bit-identical to the PairformerLayer pair stack.
+* DiffusionTransformerLayer: attention silenced gives ``a + transition(a, s)``;
+  transition silenced gives ``a + sigmoid(gate(s)) * attention(adaln(a, s))``
+  (with multiplicity); ``to_keys`` gathers keys and key mask alike (windows
+  written out by hand); upstream's output-gate initialisation.
+
+bf16-mixed reference: the GPU tests run these fp32 modules under
+``torch.autocast("cuda", dtype=torch.bfloat16)`` as upstream Boltz's own
+bf16-mixed inference path (its linears and matmuls autocast the same way; the
+Pairformer sequence stack disables autocast, as upstream does).
 """

@@ -7,8 +7,11 @@ Upstream Boltz (``boltz==2.2.1``, commit cb04aec, pinned by the reference at
 ``/root/reference`` and is not installed here.  Each class below restates the
 upstream module's published algorithm with the same class name, parameter
 names and shapes, and cites the reference lines that call or corroborate it.
-Forward passes run in fp32 (Boltz with autocast disabled); ``oracle.mixed``
-holds the bf16-mixed rounding points.
+Forward passes run in fp32 (Boltz with autocast disabled).  Under
+``torch.autocast(bf16)`` the same modules follow upstream's bf16-mixed
+inference (linears and matmuls autocast, LayerNorm and softmax in fp32, the
+Pairformer sequence stack with autocast disabled), which the GPU tests use as
+upstream's own bf16 path.
 """
 
 from __future__ import annotations
@@ -376,7 +379,7 @@ class AttentionPairBias(nn.Module):
 
 
 # --------------------------------------------------------------------------
-# Pairformer layer  (composition is parity unpinned)
+# Pairformer layer  
 # --------------------------------------------------------------------------
 
 
@@ -385,10 +388,13 @@ class PairformerLayer(nn.Module):
 
     Pair stack: ``z += tri_mul_out``, ``tri_mul_in``, ``tri_att_start``,
     ``tri_att_end``, ``transition_z`` (the eval dropout mask is ones).  Then
-    the fp32 sequence stack: ``s += attention(pre_norm_s(s), z)``, ``s +=
-    transition_s(s)``, ``s_post_norm`` (Identity in the trunk).  Composition
-    order is PARITY UNPINNED: only an upstream import could pin it; the
-    reference corroborates fp32 ``z`` inputs (``multiplication.py:59``,
+    the fp32 sequence stack with autocast disabled: ``s += attention(
+    pre_norm_s(s), z)``, ``s += transition_s(s)``, ``s_post_norm`` (Identity in
+    the trunk).  Pinned by branch isolation (every branch but one zeroed gives
+    ``z + branch(z)`` of the fp64 loop modules), chained branches, and the
+    sequence stack on the updated z in fp32 (``tests/test_oracle_pins.py``).
+    The op order itself is a restatement of upstream: the reference
+    corroborates fp32 ``z`` inputs (``multiplication.py:59``,
     ``triangle.py:113``) and an unpatched s-stack (``adapters.py:39-45``).
     """
 
@@ -413,11 +419,14 @@ class PairformerLayer(nn.Module):
         z = z + self.tri_att_start(z, mask=pair_mask, chunk_size=chunk_size_tri_attn)
         z = z + self.tri_att_end(z, mask=pair_mask, chunk_size=chunk_size_tri_attn)
         z = z + self.transition_z(z)
+        # Upstream runs the sequence stack in fp32 with autocast disabled, on
+        # the updated z (the reference leaves it unpatched, adapters.py:39-45).
         f = _at_least_f32
-        s_normed = self.pre_norm_s(f(s))
-        s = f(s) + self.attention(s=s_normed, z=f(z), mask=f(mask), k_in=s_normed)
-        s = s + self.transition_s(s)
-        s = self.s_post_norm(s)
+        with torch.autocast(device_type=s.device.type, enabled=False):
+            s_normed = self.pre_norm_s(f(s))
+            s = f(s) + self.attention(s=s_normed, z=f(z), mask=f(mask), k_in=s_normed)
+            s = s + self.transition_s(s)
+            s = self.s_post_norm(s)
         return s, z
 
 
@@ -427,8 +436,8 @@ class PairformerNoSeqLayer(nn.Module):
     builds one per ``MSALayer`` (``token_z`` 128) and one per template
     pairformer block (``template_dim`` 64).  The reference patches its modules
     by class name and by the ``.transition_z`` suffix (``adapters.py:24-45``),
-    as in the trunk.  Composition order is PARITY UNPINNED as for
-    ``PairformerLayer``; ``tests/test_oracle_pins.py`` ties the two together.
+    as in the trunk.  ``tests/test_oracle_pins.py`` checks it bit for bit
+    against the pair stack of ``PairformerLayer`` (pinned there).
     """
 
     def __init__(self, token_z=128, pairwise_head_width=32, pairwise_num_heads=4):

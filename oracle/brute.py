@@ -214,3 +214,33 @@ def attention_pair_bias(module, s, z, mask, k_in):
                 o[h * d + e] = sum(p[j] * v[j][h * d + e] for j in range(n))
         out.append(linear_vec([g[i][c] * o[c] for c in range(h_count * d)], wo))
     return np.array(out)[None]
+
+
+def attention_pair_bias_keys(module, s, k_in, bias, mask, multiplicity=1):
+    """Loops for ``AttentionPairBias`` with the bias given directly
+    (compute_pair_bias=False, as in the diffusion transformers): s [B, Q, D],
+    k_in [B, K, D], bias [B / multiplicity, Q, K, H] (the layout before
+    proj_z's Rearrange), mask [B, K]; batch element b uses bias
+    b // multiplicity (upstream ``repeat_interleave``)."""
+    h_count, d = module.num_heads, module.head_dim
+    wq, bq = _p(module, "proj_q.weight"), _p(module, "proj_q.bias")
+    wk, wv, wg, wo = (_p(module, f"proj_{t}.weight") for t in "kvgo")
+    out = np.zeros(s.shape[:2] + (wo.shape[0],))
+    for b in range(s.shape[0]):
+        nq, nk = s.shape[1], k_in.shape[1]
+        q = [linear_vec(list(s[b, i]), wq, bq) for i in range(nq)]
+        k = [linear_vec(list(k_in[b, j]), wk) for j in range(nk)]
+        v = [linear_vec(list(k_in[b, j]), wv) for j in range(nk)]
+        for i in range(nq):
+            g = [sigmoid(t) for t in linear_vec(list(s[b, i]), wg)]
+            o = [0.0] * (h_count * d)
+            for h in range(h_count):
+                logits = []
+                for j in range(nk):
+                    dot = sum(q[i][h * d + e] * k[j][h * d + e] for e in range(d)) / math.sqrt(d)
+                    logits.append(dot + bias[b // multiplicity, i, j, h] - (1.0 - mask[b, j]) * module.inf)
+                p = softmax_list(logits)
+                for e in range(d):
+                    o[h * d + e] = sum(p[j] * v[j][h * d + e] for j in range(nk))
+            out[b, i] = linear_vec([g[c] * o[c] for c in range(h_count * d)], wo)
+    return out

@@ -409,3 +409,225 @@ def test_pairformer_no_seq_layer_is_the_trunk_pair_stack(token_z):
         got = noseq(z, pair_mask)
     assert set(own) <= set(layer.state_dict())
     assert torch.equal(got, want)
+
+
+# -------------------------------------------- PairformerLayer composition
+#
+# The op order of upstream PairformerLayer is a restatement (only an import
+# of upstream Boltz could show it); what these pins fix is that each branch
+# is the pinned module applied to the current z and added to it, that the
+# branches chain (each reads the z its predecessor updated), and that the
+# sequence stack runs in fp32 on the updated z.
+
+_SMALL = dict(token_s=16, token_z=8, num_heads=2, pairwise_head_width=4, pairwise_num_heads=2)
+_BRANCHES = ("tri_mul_out", "tri_mul_in", "tri_att_start", "tri_att_end", "transition_z")
+
+
+def _small_layer(seed):
+    return R.randomize(R.PairformerLayer(**_SMALL), generator=_gen(seed)).double()
+
+
+def _silence(layer, names):
+    """Zero the final projection of each named branch (its output is then 0)."""
+    final = {"tri_mul_out": "p_out", "tri_mul_in": "p_out", "tri_att_start": "mha.linear_o",
+             "tri_att_end": "mha.linear_o", "transition_z": "fc3", "attention": "proj_o", "transition_s": "fc3"}
+    with torch.no_grad():
+        for name in names:
+            mod = getattr(layer, name)
+            for part in final[name].split("."):
+                mod = getattr(mod, part)
+            mod.weight.zero_()
+            if getattr(mod, "bias", None) is not None:
+                mod.bias.zero_()
+
+
+def _brute_branch(layer, name, z, pair_mask):
+    mod = getattr(layer, name)
+    if name.startswith("tri_mul"):
+        return B.triangle_multiplication(mod, z, pair_mask, outgoing=name.endswith("out"))
+    if name.startswith("tri_att"):
+        return B.triangle_attention(mod, z, pair_mask, starting=name.endswith("start"))
+    return B.transition(mod, z)
+
+
+def _small_inputs(seed, n=4):
+    g = _gen(seed)
+    s = torch.randn(1, n, _SMALL["token_s"], generator=g, dtype=torch.float64)
+    z = torch.randn(1, n, n, _SMALL["token_z"], generator=g, dtype=torch.float64)
+    mask = torch.ones(1, n, dtype=torch.float64)
+    mask[:, -1] = 0
+    return s, z, mask, mask[:, :, None] * mask[:, None, :]
+
+
+@pytest.mark.parametrize("branch", _BRANCHES)
+def test_pairformer_single_branch_is_residual_of_the_pinned_module(branch):
+    """Every pair branch but one silenced (and the sequence stack too): z_out
+    = z + branch(z) with the branch evaluated by the fp64 loops, s_out = s."""
+    layer = _small_layer(20)
+    _silence(layer, [b for b in _BRANCHES if b != branch] + ["attention", "transition_s"])
+    s, z, mask, pm = _small_inputs(21)
+    with torch.no_grad():
+        s2, z2 = layer(s, z, mask, pm)
+    want = z[0].numpy() + _brute_branch(layer, branch, z[0].numpy(), pm[0].numpy())
+    assert _rel(z2[0], want) < 1e-10
+    assert torch.equal(s2, s)
+
+
+@pytest.mark.parametrize("first,second", [("tri_mul_out", "tri_att_end"), ("tri_mul_in", "transition_z"),
+                                          ("tri_att_start", "tri_att_end")])
+def test_pairformer_branches_chain_on_the_updated_z(first, second):
+    """Two active branches: the second reads the z the first updated
+    (z1 = z + f(z), z2 = z1 + g(z1)), not the layer input."""
+    layer = _small_layer(22)
+    _silence(layer, [b for b in _BRANCHES if b not in (first, second)] + ["attention", "transition_s"])
+    s, z, mask, pm = _small_inputs(23)
+    with torch.no_grad():
+        _, z2 = layer(s, z, mask, pm)
+    z0, m = z[0].numpy(), pm[0].numpy()
+    z1 = z0 + _brute_branch(layer, first, z0, m)
+    want = z1 + _brute_branch(layer, second, z1, m)
+    parallel = z0 + _brute_branch(layer, first, z0, m) + _brute_branch(layer, second, z0, m)
+    assert _rel(z2[0], want) < 1e-10
+    assert _rel(want, parallel) > 1e-6  # far above the 1e-10 bar: the check tells chained from parallel
+
+
+def test_pairformer_sequence_stack_runs_on_the_updated_z():
+    """With the pair stack reduced to its transition, s_out = s1 + transition_s(s1),
+    s1 = s + attention(pre_norm_s(s), z_out, mask, k_in=pre_norm_s(s)), every
+    module by the fp64 loops: the sequence stack follows the pair stack and
+    reads its result."""
+    layer = _small_layer(24)
+    _silence(layer, [b for b in _BRANCHES if b != "transition_z"])
+    s, z, mask, pm = _small_inputs(25)
+    with torch.no_grad():
+        s2, z2 = layer(s, z, mask, pm)
+    z_out = z[0].numpy() + B.transition(layer.transition_z, z[0].numpy())
+    assert _rel(z2[0], z_out) < 1e-10
+    sn = np.array([B.layer_norm_vec(list(r), B._p(layer, "pre_norm_s.weight"), B._p(layer, "pre_norm_s.bias"),
+                                    layer.pre_norm_s.eps) for r in s[0].numpy()])[None]
+    s1 = s.numpy() + B.attention_pair_bias(layer.attention, sn, z_out[None], mask.numpy(), sn)
+    want = s1 + B.transition(layer.transition_s, s1)
+    assert _rel(s2, want) < 1e-10
+    stale = s.numpy() + B.attention_pair_bias(layer.attention, sn, z.numpy(), mask.numpy(), sn)
+    assert _rel(stale + B.transition(layer.transition_s, stale), want) > 1e-7  # reading the old z would show
+
+
+def test_pairformer_sequence_stack_is_fp32_under_autocast():
+    """Under bf16 autocast the pair stack autocasts, but the sequence stack
+    runs with autocast disabled: s_out equals the fp32 sequence stack applied
+    to the (bf16-path) z_out, far inside the bf16 rounding it would show
+    otherwise."""
+    layer = R.randomize(R.PairformerLayer(**_SMALL), generator=_gen(26))
+    g = _gen(27)
+    n = 6
+    s = torch.randn(1, n, 16, generator=g)
+    z = torch.randn(1, n, n, 8, generator=g)
+    mask = torch.ones(1, n)
+    pm = mask[:, :, None] * mask[:, None, :]
+    with torch.no_grad(), torch.autocast("cpu", dtype=torch.bfloat16):
+        s_mix, z_mix = layer(s, z, mask, pm)
+    with torch.no_grad():
+        sn = layer.pre_norm_s(s)
+        s1 = s + layer.attention(s=sn, z=z_mix.float(), mask=mask, k_in=sn)
+        want = s1 + layer.transition_s(s1)
+        # what the same stack gives when it autocasts
+        with torch.autocast("cpu", dtype=torch.bfloat16):
+            sn_b = layer.pre_norm_s(s)
+            s1_b = s + layer.attention(s=sn_b, z=z_mix.float(), mask=mask, k_in=sn_b)
+            bf16_stack = s1_b + layer.transition_s(s1_b)
+    assert z_mix.dtype == torch.float32 and s_mix.dtype == torch.float32
+    assert _rel(s_mix, want) < 1e-6
+    assert _rel(bf16_stack, want) > 2e-5  # 20x the bar: a bf16 stack would fail it
+
+
+# ------------------------------------ DiffusionTransformerLayer composition
+
+
+def _dtl(seed, dim=8, heads=2, cond=6):
+    layer = R.randomize(R.DiffusionTransformerLayer(heads, dim, cond), generator=_gen(seed)).double()
+    return layer
+
+
+def _dtl_inputs(seed, batch=2, n=5, dim=8, cond=6, heads=2, nk=None, bias_batch=None):
+    g = _gen(seed)
+    nk = n if nk is None else nk
+    a = torch.randn(batch, n, dim, generator=g, dtype=torch.float64)
+    s = torch.randn(batch, n, cond, generator=g, dtype=torch.float64)
+    bias = torch.randn(bias_batch or batch, n, nk, heads, generator=g, dtype=torch.float64)
+    mask = torch.ones(batch, n, dtype=torch.float64)
+    mask[0, -2:] = 0
+    return a, s, bias, mask
+
+
+def test_diffusion_layer_without_attention_is_residual_transition():
+    """pair_bias_attn.proj_o zeroed: out = a + transition(a, s), the
+    conditioned transition by the fp64 loops (it acts on the updated a)."""
+    layer = _dtl(30)
+    with torch.no_grad():
+        layer.pair_bias_attn.proj_o.weight.zero_()
+    a, s, bias, mask = _dtl_inputs(31)
+    with torch.no_grad():
+        got = layer(a, s, bias=bias, mask=mask)
+    want = a.numpy() + B.conditioned_transition(layer.transition, a.numpy(), s.numpy())
+    assert _rel(got, want) < 1e-10
+
+
+@pytest.mark.parametrize("multiplicity", [1, 2])
+def test_diffusion_layer_without_transition_is_gated_attention(multiplicity):
+    """transition.b_to_a zeroed: out = a + sigmoid(output_projection_linear(s))
+    * attention(adaln(a, s), k_in=adaln(a, s)), AdaLN and the attention by the
+    fp64 loops; with multiplicity m, sample b uses bias b // m."""
+    layer = _dtl(32)
+    with torch.no_grad():
+        layer.transition.b_to_a.weight.zero_()
+    a, s, bias, mask = _dtl_inputs(33, batch=2, bias_batch=2 // multiplicity)
+    with torch.no_grad():
+        got = layer(a, s, bias=bias, mask=mask, multiplicity=multiplicity)
+    ad = B.adaln(layer.adaln, a.numpy(), s.numpy())
+    att = B.attention_pair_bias_keys(layer.pair_bias_attn, ad, ad, bias.numpy(), mask.numpy(), multiplicity)
+    w, b = B._p(layer, "output_projection_linear.weight"), B._p(layer, "output_projection_linear.bias")
+    gate = np.array([[[B.sigmoid(t) for t in B.linear_vec(list(r), w, b)] for r in sb] for sb in s.numpy()])
+    assert _rel(got, a.numpy() + gate * att) < 1e-10
+
+
+def test_diffusion_layer_gathers_keys_and_their_mask():
+    """With ``to_keys`` (the atom transformer's windows) the keys are the
+    gathered AdaLN rows and the mask is gathered the same way: here windows
+    of 2 queries over 4 keys of one 8-atom sample, the key indices written out
+    by hand and clamped at the ends, with the transition silenced."""
+    layer = _dtl(34)
+    with torch.no_grad():
+        layer.transition.b_to_a.weight.zero_()
+    g = _gen(35)
+    atoms, w, h = 8, 2, 4
+    nw = atoms // w
+    a = torch.randn(nw, w, 8, generator=g, dtype=torch.float64)
+    s = torch.randn(nw, w, 6, generator=g, dtype=torch.float64)
+    bias = torch.randn(nw, w, h, 2, generator=g, dtype=torch.float64)
+    atom_mask = torch.tensor([1, 1, 1, 0, 1, 1, 0, 1], dtype=torch.float64)
+    keys = [[max(0, min(atoms - 1, w * i + t - 1)) for t in range(h)] for i in range(nw)]  # centred, clamped
+    index = torch.tensor(keys)
+
+    def to_keys(x):
+        return x.reshape(1, atoms, -1)[:, index].reshape(nw, h, -1)
+
+    with torch.no_grad():
+        got = layer(a, s, bias=bias, mask=atom_mask.view(nw, w), to_keys=to_keys)
+    ad = B.adaln(layer.adaln, a.numpy(), s.numpy())  # [nw, w, 8]
+    flat = ad.reshape(atoms, 8)
+    k_in = np.array([[flat[keys[i][t]] for t in range(h)] for i in range(nw)])
+    kmask = np.array([[atom_mask[keys[i][t]].item() for t in range(h)] for i in range(nw)])
+    att = B.attention_pair_bias_keys(layer.pair_bias_attn, ad, k_in, bias.numpy(), kmask)
+    wl, bl = B._p(layer, "output_projection_linear.weight"), B._p(layer, "output_projection_linear.bias")
+    gate = np.array([[[B.sigmoid(t) for t in B.linear_vec(list(r), wl, bl)] for r in sb] for sb in s.numpy()])
+    assert _rel(got, a.numpy() + gate * att) < 1e-10
+    # the masked atoms 3 and 6 are masked as keys wherever a window gathers them
+    assert kmask.tolist() == [[1, 1, 1, 1], [1, 1, 0, 1], [0, 1, 1, 0], [1, 0, 1, 1]]
+
+
+def test_diffusion_layer_default_gate_init():
+    """Upstream initialises both output gates to weight 0, bias -2
+    (sigmoid(-2) ~ 0.119 on every channel before training)."""
+    layer = R.DiffusionTransformerLayer(2, 8, 6)
+    for lin in (layer.output_projection_linear, layer.transition.output_projection[0]):
+        assert not lin.weight.any() and torch.all(lin.bias == -2.0)
