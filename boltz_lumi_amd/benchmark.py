@@ -1,27 +1,36 @@
-"""A/B harness: upstream forwards against the native ones, same inputs, same seeds.
+"""A/B timing of Boltz inference: upstream forwards against this package's.
 
-Reference: src/boltz_lumi/benchmark.py.  The model-independent part is
-:class:`ABRecorder` (per-call timing with GPU-event stage timers, peak memory,
-finiteness and the comparison of every output with the first upstream call
-of the same candidate, the ``timings.json`` report), driven either by
-:func:`ab_benchmark` (any model and step callable) or by :func:`main`, which
-binds it to Boltz's ``predict`` CLI as the reference does
-(benchmark.py:273-325; Boltz 2.2.1 and pytorch_lightning required).
+Reference: src/boltz_lumi/benchmark.py (the ``timings.json`` report and the
+``python -m ... benchmark predict ...`` entry).  The design here:
 
-Report schema (reference benchmark.py:56-150, 197-214): the run settings,
-``torch`` / ``hip`` / ``gpu``, ``model_calls`` (recipe, iteration, first,
-profiled, candidate, model_s, peak_allocated_bytes, stages_s), ``rounds``
-(recipe, iteration, candidates, round_s), ``errors`` (recipe, iteration,
-candidate, field, max_absolute_error, relative_l2_error, atol, rtol,
-failing_values), ``upstream_warm_mean_s`` / ``optimized_warm_mean_s``,
-``saved_s``, ``saved_percent`` and ``status`` (running / complete /
-numerical_difference / failed, with ``error``).
+* :class:`StageClock` times the top-level stages of a Boltz-2 model with GPU
+  events, attached as forward hooks (and a wrapper of
+  ``structure_module.sample``), detached again on exit;
+* :class:`Tolerance` turns an output field and its upstream value into one
+  error record;
+* :class:`Report` is the ``timings.json`` document: it collects call, round
+  and error records and works out the warm means, the saving and the status;
+* :class:`ABSession` runs the recipes, upstream first and then with the native
+  forwards installed, over one fixed list of candidates with the seed reset
+  before every round and every call;
+* :func:`ab_benchmark` drives a session with any model and step callable,
+  :func:`main` with Boltz's ``predict`` CLI (Boltz 2.2.1 and
+  pytorch_lightning required).
 
-One difference on purpose: the native kernels compute in bf16 with their own
-summation order, so an output counts as failing where
-``|x - upstream| > atol + rtol * |upstream|`` (default 1e-2 each, the
-end-to-end bar of the port); the reference counts every value that is not
-bit-identical (atol = rtol = 0, which ``--atol 0 --rtol 0`` restores).
+``timings.json`` keys (the reference's schema, kept so that its readers work):
+the run settings, ``torch`` / ``hip`` / ``gpu`` / ``slurm_job``,
+``model_calls`` (recipe, iteration, first, profiled, candidate, model_s,
+peak_allocated_bytes, stages_s), ``rounds`` (recipe, iteration, first,
+profiled, candidates, round_s), ``errors`` (recipe, iteration, first,
+profiled, candidate, field, max_absolute_error, relative_l2_error, atol, rtol,
+failing_values), ``feature_load_s`` (CLI runs), ``upstream_warm_mean_s``,
+``optimized_warm_mean_s``, ``saved_s``, ``saved_percent`` and ``status``
+(running, complete, numerical_difference or failed with ``error``).
+
+Outputs count as different where ``|x - upstream| > atol + rtol * |upstream|``
+(default 1e-2 each): the native kernels round in bf16 in their own order.
+The reference counts every value that is not bit-identical; ``--atol 0
+--rtol 0`` asks for that.
 """
 
 from __future__ import annotations
@@ -33,9 +42,9 @@ import os
 import random
 import statistics
 import time
-from contextlib import ExitStack, contextmanager
+from contextlib import contextmanager
+from dataclasses import dataclass
 from pathlib import Path
-from unittest.mock import patch
 
 import numpy as np
 import torch
@@ -46,8 +55,8 @@ RECIPES = ("upstream", "optimized")
 ATOL = 1e-2
 RTOL = 1e-2
 
-# Module paths timed as stages, plus the structure module's ``sample``
-# (reference benchmark.py:36-52).
+# Top-level modules of a Boltz-2 model timed as stages; ``diffusion_sample``
+# is the structure module's ``sample`` method.
 STAGES = (
     "input_embedder",
     "template_module",
@@ -56,8 +65,9 @@ STAGES = (
     "diffusion_conditioning",
     "confidence_module",
 )
+SAMPLE_STAGE = "diffusion_sample"
 
-# Prediction outputs compared between the recipes (reference benchmark.py:108-127).
+# Prediction outputs compared between the recipes, where present.
 FIELDS = (
     "coords",
     "plddt",
@@ -75,79 +85,140 @@ FIELDS = (
     "affinity_probability_binary2",
 )
 
-# Fields of a confidence summary file (reference benchmark.py:243-246).
+# Scalars every confidence summary of a structure prediction must hold.
 CONFIDENCE_FIELDS = (
     "confidence_score", "ptm", "iptm", "ligand_iptm", "protein_iptm",
     "complex_plddt", "complex_iplddt", "complex_pde", "complex_ipde",
 )
+AFFINITY_FIELDS = ("affinity_pred_value", "affinity_probability_binary")
 
 
 def seed_all(seed: int) -> None:
-    """Seed Python, NumPy and torch (all devices) with one value."""
+    """One seed for Python's, NumPy's and torch's generators (all devices)."""
     random.seed(seed)
     np.random.seed(seed % 2**32)
     torch.manual_seed(seed)
 
 
-@contextmanager
-def stage_timers(model, events: list):
-    """Time the stage modules' forwards and ``structure_module.sample`` with GPU
-    events on the current stream; each call appends ``(name, start, end)`` to
-    ``events``.  The wrappers are removed on exit (instance attributes that
-    existed before, such as an installed ``sample``, are restored)."""
+# ------------------------------------------------------------- stage timing
 
-    def wrap(original, name):
-        def timed(*args, **kwargs):
-            start = torch.cuda.Event(enable_timing=True)
+
+class StageClock:
+    """GPU-event timing of a model's stages.
+
+    While active, every call of a stage module (by ``named_modules`` name, in
+    :data:`STAGES`) and of ``structure_module.sample`` appends
+    ``(stage, start_event, end_event)`` to :attr:`spans`; :meth:`seconds`
+    sums them per stage once the work has finished.  Modules are timed by
+    forward pre- and post-hooks, the sampler by an instance attribute that
+    shadows the method; both are removed on exit, restoring any instance
+    attribute that was there before."""
+
+    def __init__(self, model):
+        self.model = model
+        self.spans = []
+        self._open = {}
+        self._handles = []
+        self._sampler = None
+
+    def _start(self, stage):
+        event = torch.cuda.Event(enable_timing=True)
+        event.record()
+        self._open.setdefault(stage, []).append(event)
+
+    def _stop(self, stage):
+        pending = self._open.get(stage)
+        if pending:
             end = torch.cuda.Event(enable_timing=True)
-            start.record()
-            try:
-                with torch.profiler.record_function(name):
-                    return original(*args, **kwargs)
-            finally:
-                end.record()
-                events.append((name, start, end))
+            end.record()
+            self.spans.append((stage, pending.pop(), end))
 
-        return timed
-
-    with ExitStack() as stack:
-        for name, module in model.named_modules():
+    def __enter__(self):
+        for name, module in self.model.named_modules():
             if name in STAGES:
-                stack.enter_context(patch.object(module, "forward", wrap(module.forward, name)))
-        sampler = getattr(model, "structure_module", None)
-        if sampler is not None and hasattr(sampler, "sample"):
-            stack.enter_context(patch.object(sampler, "sample", wrap(sampler.sample, "diffusion_sample")))
-        yield
+                self._handles.append(module.register_forward_pre_hook(lambda m, a, s=name: self._start(s)))
+                self._handles.append(module.register_forward_hook(lambda m, a, o, s=name: self._stop(s)))
+        sampler = getattr(self.model, "structure_module", None)
+        if sampler is not None and callable(getattr(sampler, "sample", None)):
+            previous = vars(sampler).get("sample")
+            inner = sampler.sample
+
+            def timed_sample(*args, **kwargs):
+                self._start(SAMPLE_STAGE)
+                try:
+                    with torch.profiler.record_function(SAMPLE_STAGE):
+                        return inner(*args, **kwargs)
+                finally:
+                    self._stop(SAMPLE_STAGE)
+
+            sampler.sample = timed_sample
+            self._sampler = (sampler, previous)
+        return self
+
+    def __exit__(self, *exc):
+        for handle in self._handles:
+            handle.remove()
+        self._handles.clear()
+        if self._sampler is not None:
+            sampler, previous = self._sampler
+            if previous is None:
+                del sampler.sample
+            else:
+                sampler.sample = previous
+            self._sampler = None
+        self._open.clear()
+        return False
+
+    def reset(self):
+        self.spans.clear()
+        self._open.clear()
+
+    def seconds(self) -> dict:
+        totals = {}
+        for stage, start, end in self.spans:
+            totals[stage] = totals.get(stage, 0.0) + start.elapsed_time(end) / 1e3
+        return totals
+
+
+# ------------------------------------------------------------ comparisons
+
+
+@dataclass(frozen=True)
+class Tolerance:
+    """Elementwise bar ``|x - expected| <= atol + rtol |expected|``."""
+
+    atol: float = ATOL
+    rtol: float = RTOL
+
+    def record(self, value: torch.Tensor, expected: torch.Tensor) -> dict:
+        """Error record of ``value`` against ``expected`` (NaN counts as failing)."""
+        x, e = value.detach().double(), expected.detach().double()
+        diff = (x - e).abs()
+        within = diff <= self.atol + self.rtol * e.abs()
+        norm = e.norm().item()
+        return {
+            "max_absolute_error": diff.max().item() if diff.numel() else 0.0,
+            "relative_l2_error": (x - e).norm().item() / norm if norm else None,
+            "atol": self.atol,
+            "rtol": self.rtol,
+            "failing_values": int(diff.numel() - within.sum().item()),
+        }
 
 
 def compare(value: torch.Tensor, expected: torch.Tensor, atol: float, rtol: float) -> dict:
     """Error record of one output field against its upstream value."""
-    value, expected = value.double(), expected.double()
-    delta = value - expected
-    denominator = expected.norm().item()
-    failing = ~(delta.abs() <= atol + rtol * expected.abs())
-    return dict(
-        max_absolute_error=delta.abs().max().item() if delta.numel() else 0.0,
-        relative_l2_error=delta.norm().item() / denominator if denominator else None,
-        atol=atol,
-        rtol=rtol,
-        failing_values=int(failing.sum()),
-    )
+    return Tolerance(atol, rtol).record(value, expected)
 
 
-class ABRecorder:
-    """Accumulates the report of one A/B run (reference benchmark.py:56-150)."""
+# ------------------------------------------------------------------ report
 
-    def __init__(self, model, *, seed: int, atol: float = ATOL, rtol: float = RTOL, fields=FIELDS,
-                 settings=None, output: Path | None = None):
-        self.model = model
-        self.seed = seed
-        self.atol, self.rtol = atol, rtol
-        self.fields = tuple(fields)
-        self.output = None if output is None else Path(output)
-        self.report = dict(
-            settings or {},
-            seed=seed,
+
+class Report(dict):
+    """The ``timings.json`` document of one A/B run."""
+
+    def __init__(self, settings=None, path: Path | None = None):
+        super().__init__(settings or {})
+        self.update(
             torch=torch.__version__,
             hip=torch.version.hip,
             gpu=torch.cuda.get_device_name(0) if torch.cuda.is_available() else None,
@@ -157,257 +228,315 @@ class ABRecorder:
             errors=[],
             status="running",
         )
-        self.references = {}
-        self.events = []
-        self.current = {}
+        self.path = None if path is None else Path(path)
 
-    def save(self) -> None:
-        if self.output is not None:
-            self.output.mkdir(parents=True, exist_ok=True)
-            (self.output / "timings.json").write_text(json.dumps(self.report, indent=2) + "\n")
+    def write(self) -> None:
+        if self.path is not None:
+            self.path.mkdir(parents=True, exist_ok=True)
+            (self.path / "timings.json").write_text(json.dumps(self, indent=2) + "\n")
 
-    def measured_call(self, candidate: str, call, *args, **kwargs):
-        """Run one model call with the seed reset, time it and compare its
-        outputs with the first upstream call of ``candidate``."""
+    def warm_times(self, recipe: str):
+        return [c["model_s"] for c in self["model_calls"]
+                if c["recipe"] == recipe and not c["first"] and not c["profiled"]]
+
+    def conclude(self) -> bool:
+        """Fill in the warm means, the saving and the status; True when no
+        output field failed its tolerance."""
+        for recipe in RECIPES:
+            warm = self.warm_times(recipe)
+            if warm:
+                self[f"{recipe}_warm_mean_s"] = statistics.mean(warm)
+        base, new = self.get("upstream_warm_mean_s"), self.get("optimized_warm_mean_s")
+        if base and new is not None:
+            self["saved_s"] = base - new
+            self["saved_percent"] = 100.0 * (base - new) / base
+        agree = not any(e["failing_values"] for e in self["errors"])
+        self["status"] = "complete" if agree else "numerical_difference"
+        self.write()
+        return agree
+
+    def failed(self, error: BaseException) -> None:
+        if self["status"] == "running":
+            self["status"] = "failed"
+            self["error"] = str(error)
+            self.write()
+
+
+# ----------------------------------------------------------------- session
+
+
+class ABSession:
+    """Rounds of model calls under the two recipes.
+
+    A round is one pass over the candidates (ids in a fixed order).  Every
+    round and every call starts from ``seed``; a call's outputs (``fields``
+    present in its result dict) are compared with the first upstream call of
+    the same candidate."""
+
+    def __init__(self, model, *, seed: int, tolerance: Tolerance = Tolerance(), fields=FIELDS, settings=None,
+                 output=None):
+        self.model = model
+        self.seed = seed
+        self.tolerance = tolerance
+        self.fields = tuple(fields)
+        self.report = Report(dict(settings or {}, seed=seed), output)
+        self.clock = StageClock(model)
+        self.baseline = {}
+        self.tags = {}
+
+    # one model call -------------------------------------------------------
+    def call(self, candidate: str, fn, *args, **kwargs):
         seed_all(self.seed)
-        self.events.clear()
+        self.clock.reset()
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
-        begin = time.perf_counter()
-        output = call(*args, **kwargs)
+        t0 = time.perf_counter()
+        result = fn(*args, **kwargs)
         torch.cuda.synchronize()
-        elapsed = time.perf_counter() - begin
-        if output.get("exception"):
-            raise RuntimeError("Prediction failed; inspect the preceding log")
-        stages = {}
-        for name, start, end in self.events:
-            stages[name] = stages.get(name, 0.0) + start.elapsed_time(end) / 1000
+        seconds = time.perf_counter() - t0
+        if result.get("exception"):
+            raise RuntimeError(f"the model call for {candidate} reported an exception (see the log above)")
         self.report["model_calls"].append(dict(
-            self.current,
-            candidate=candidate,
-            model_s=elapsed,
-            peak_allocated_bytes=torch.cuda.max_memory_allocated(),
-            stages_s=stages,
-        ))
-        values = {k: output[k].detach().cpu() for k in self.fields if k in output}
-        bad = [k for k, v in values.items() if not torch.isfinite(v).all()]
-        if bad:
-            raise RuntimeError(f"Nonfinite prediction: {', '.join(bad)}")
-        expected = self.references.setdefault(candidate, values)
-        if expected.keys() != values.keys():
-            raise RuntimeError(f"Output fields changed for {candidate}")
-        for key, value in values.items():
-            if value.shape != expected[key].shape:
-                raise RuntimeError(f"Output shape of {key} changed for {candidate}")
-            self.report["errors"].append(dict(
-                self.current, candidate=candidate, field=key,
-                **compare(value, expected[key], self.atol, self.rtol)))
-        return output
-
-    def run_round(self, recipe: str, iteration: int, body, candidates, profiled: bool = False):
-        """Run ``body()`` (which makes the model calls of one round) and check
-        that it called every candidate once, in order."""
-        self.current.update(recipe=recipe, iteration=iteration, first=iteration == 0, profiled=profiled)
-        seed_all(self.seed)
-        before = len(self.report["model_calls"])
-        torch.cuda.synchronize()
-        begin = time.perf_counter()
-        result = body()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - begin
-        called = [c["candidate"] for c in self.report["model_calls"][before:]]
-        if called != list(candidates):
-            raise RuntimeError("Missing or reordered prediction calls")
-        self.report["rounds"].append(dict(self.current, candidates=list(candidates), round_s=elapsed))
-        self.save()
+            self.tags, candidate=candidate, model_s=seconds,
+            peak_allocated_bytes=torch.cuda.max_memory_allocated(), stages_s=self.clock.seconds()))
+        self._check(candidate, result)
         return result
 
-    def finish(self) -> dict:
-        """Warm means, savings and status; raises when outputs differ beyond
-        the tolerance (the report is saved first)."""
-        report = self.report
-        for recipe in RECIPES:
-            warm = [c["model_s"] for c in report["model_calls"]
-                    if c["recipe"] == recipe and not c["first"] and not c["profiled"]]
-            if warm:
-                report[recipe + "_warm_mean_s"] = statistics.mean(warm)
-        upstream = report.get("upstream_warm_mean_s")
-        optimized = report.get("optimized_warm_mean_s")
-        if upstream and optimized is not None:
-            report.update(saved_s=upstream - optimized, saved_percent=100 * (upstream - optimized) / upstream)
-        differs = any(e["failing_values"] for e in report["errors"])
-        report["status"] = "numerical_difference" if differs else "complete"
-        self.save()
-        if differs:
-            raise RuntimeError("Predictions differ; see timings.json for absolute and relative errors")
-        return report
+    def _check(self, candidate, result):
+        values = {key: result[key].detach().cpu() for key in self.fields if key in result}
+        broken = [key for key, v in values.items() if not torch.isfinite(v).all()]
+        if broken:
+            raise RuntimeError(f"non-finite output field(s) for {candidate}: {', '.join(broken)}")
+        baseline = self.baseline.setdefault(candidate, values)
+        if set(baseline) != set(values):
+            raise RuntimeError(f"{candidate} returned fields {sorted(values)}, the first call {sorted(baseline)}")
+        for key, value in values.items():
+            if value.shape != baseline[key].shape:
+                raise RuntimeError(f"{candidate}: {key} changed shape from {tuple(baseline[key].shape)} "
+                                   f"to {tuple(value.shape)}")
+            self.report["errors"].append(dict(self.tags, candidate=candidate, field=key,
+                                              **self.tolerance.record(value, baseline[key])))
 
-    def fail(self, error: BaseException) -> None:
-        self.report.update(status="failed", error=str(error))
-        self.save()
+    # one round --------------------------------------------------------------
+    def round(self, recipe: str, iteration: int, run, candidates, profiled: bool = False):
+        """``run()`` makes the round's model calls (through :meth:`call`); it
+        must call every candidate exactly once, in order."""
+        self.tags = dict(recipe=recipe, iteration=iteration, first=iteration == 0, profiled=profiled)
+        seed_all(self.seed)
+        done = len(self.report["model_calls"])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        result = run()
+        torch.cuda.synchronize()
+        seconds = time.perf_counter() - t0
+        seen = [c["candidate"] for c in self.report["model_calls"][done:]]
+        if seen != list(candidates):
+            raise RuntimeError(f"round {recipe}/{iteration} called {seen}, expected {list(candidates)}")
+        self.report["rounds"].append(dict(self.tags, candidates=list(candidates), round_s=seconds))
+        self.report.write()
+        return result
+
+    def run(self, candidates, one_round, repeats: int, profile: bool = False, install_kwargs=None):
+        """Upstream rounds 0..repeats, ``install``, optimized rounds
+        0..repeats, then an optional profiled optimized round.  Raises when
+        outputs differ beyond the tolerance (the report is written first)."""
+        if repeats < 1:
+            raise ValueError("at least one warm repeat is needed")
+        result = None
+        try:
+            for recipe in RECIPES:
+                if recipe == "optimized":
+                    install(self.model, **(install_kwargs or {}))
+                with self.clock:  # entered after install, which rebinds structure_module.sample
+                    for iteration in range(repeats + 1):
+                        result = self.round(recipe, iteration, lambda: one_round(recipe, iteration, False),
+                                            candidates)
+            if profile:
+                with self.clock:
+                    profiled_round(lambda: self.round(RECIPES[-1], repeats + 1,
+                                                      lambda: one_round(RECIPES[-1], repeats + 1, True),
+                                                      candidates, profiled=True), self.report.path)
+            agree = self.report.conclude()
+        except BaseException as error:
+            self.report.failed(error)
+            raise
+        if not agree:
+            raise RuntimeError("optimized outputs differ from upstream beyond the tolerance; the error records "
+                               "are in timings.json")
+        return result
 
 
-def profile_round(run, output: Path | None):
-    """One profiled round under ``torch.profiler``: a Chrome trace and the 20
-    entries with the most GPU self time (reference benchmark.py:180-196)."""
-    activities = [torch.profiler.ProfilerActivity.CPU, torch.profiler.ProfilerActivity.CUDA]
-    with torch.profiler.profile(activities=activities) as profiler:
+def profiled_round(run, directory: Path | None):
+    """``run()`` under torch.profiler; writes ``trace.json`` (Chrome trace)
+    and ``profile.txt`` (the 20 entries with the most GPU self time)."""
+    kinds = [torch.profiler.ProfilerActivity.CPU, torch.profiler.ProfilerActivity.CUDA]
+    with torch.profiler.profile(activities=kinds) as prof:
         run()
-    if output is None:
+    if directory is None:
         return
-    profiler.export_chrome_trace(str(output / "trace.json"))
-    entries = sorted(profiler.key_averages(), key=lambda e: e.self_device_time_total, reverse=True)
-    lines = ["Operator or kernel                         GPU self seconds    Calls"]
-    lines += [f"{e.key[:42]:42} {e.self_device_time_total / 1e6:15.6f} {e.count:8}" for e in entries[:20]]
-    (output / "profile.txt").write_text("\n".join(lines) + "\n")
+    prof.export_chrome_trace(str(directory / "trace.json"))
+    top = sorted(prof.key_averages(), key=lambda e: e.self_device_time_total, reverse=True)[:20]
+    rows = [f"{'Operator or kernel':42} {'GPU self seconds':>16} {'Calls':>8}"]
+    rows += [f"{e.key[:42]:42} {e.self_device_time_total / 1e6:16.6f} {e.count:8d}" for e in top]
+    (directory / "profile.txt").write_text("\n".join(rows) + "\n")
 
 
 def ab_benchmark(model, step, candidates, *, repeats: int = 3, seed: int = 42, atol: float = ATOL,
                  rtol: float = RTOL, fields=FIELDS, output=None, profile: bool = False, settings=None,
                  install_kwargs=None) -> dict:
-    """Upstream rounds, then ``install(model)`` and optimized rounds, each of
-    ``repeats`` warm rounds after one first round, over ``candidates`` (pairs
-    of ``(id, batch)``); ``step(model, batch)`` makes one model call and
-    returns a dict of output tensors.  Returns the report (also written to
-    ``output/timings.json`` when ``output`` is given)."""
-    if repeats < 1:
-        raise ValueError("Use at least one warm repeat")
+    """A/B run of ``step(model, batch)`` (one model call returning a dict of
+    output tensors) over ``candidates``, pairs ``(id, batch)`` with unique
+    ids.  Returns the report, also written to ``output/timings.json`` when
+    ``output`` is given."""
     candidates = list(candidates)
-    ids = [c for c, _ in candidates]
+    ids = [cid for cid, _ in candidates]
     if len(set(ids)) != len(ids):
-        raise ValueError("Candidate ids must be unique")
-    recorder = ABRecorder(model, seed=seed, atol=atol, rtol=rtol, fields=fields, settings=settings,
-                          output=output)
+        raise ValueError("candidate ids must be unique")
+    session = ABSession(model, seed=seed, tolerance=Tolerance(atol, rtol), fields=fields, settings=settings,
+                        output=output)
 
-    def body():
-        for candidate, batch in candidates:
-            recorder.measured_call(candidate, step, model, batch)
+    def one_round(recipe, iteration, profiled):
+        for cid, batch in candidates:
+            session.call(cid, step, model, batch)
 
-    try:
-        for recipe in RECIPES:
-            if recipe == "optimized":
-                install(model, **(install_kwargs or {}))
-            with stage_timers(model, recorder.events):
-                for iteration in range(repeats + 1):
-                    recorder.run_round(recipe, iteration, body, ids)
-        if profile:
-            with stage_timers(model, recorder.events):
-                profile_round(lambda: recorder.run_round(RECIPES[-1], repeats + 1, body, ids, True),
-                              recorder.output)
-        return recorder.finish()
-    except BaseException as error:
-        if recorder.report["status"] == "running":
-            recorder.fail(error)
-        raise
+    session.run(ids, one_round, repeats, profile=profile, install_kwargs=install_kwargs)
+    return session.report
+
+
+# ------------------------------------------------------ output validation
+
+
+def _expected_outputs(directory: Path, candidate: str, samples: int, output_format: str, affinity: bool):
+    """(structure file or None, summary file, required fields, label) per
+    output Boltz writes for one candidate."""
+    folder = directory / candidate
+    if affinity:
+        yield None, folder / f"affinity_{candidate}.json", AFFINITY_FIELDS, f"{candidate} affinity"
+        return
+    ext = ".pdb" if output_format == "pdb" else ".cif"
+    for rank in range(samples):
+        stem = f"{candidate}_model_{rank}"
+        yield folder / f"{stem}{ext}", folder / f"confidence_{stem}.json", CONFIDENCE_FIELDS, stem
+
+
+def _finite_number(value) -> bool:
+    return isinstance(value, (int, float)) and not isinstance(value, bool) and math.isfinite(value)
 
 
 def validate_outputs(directory, candidates, samples, output_format="mmcif", affinity=False):
-    """Every candidate has its structure files and finite confidence (or
-    affinity) summaries (reference benchmark.py:249-270)."""
-    directory = Path(directory)
+    """Check that Boltz wrote every output of every candidate: a non-empty
+    structure file per sample (mmCIF, or PDB when ``output_format == "pdb"``)
+    with a confidence summary of finite scalars, or one affinity summary per
+    candidate when ``affinity``."""
+    candidates = list(candidates)
     if not candidates:
-        raise RuntimeError("No inputs were predicted")
-    suffix = ".pdb" if output_format == "pdb" else ".cif"
+        raise RuntimeError("no candidate was predicted")
+    directory = Path(directory)
     for candidate in candidates:
-        for rank in range(1 if affinity else samples):
-            stem = f"{candidate}_model_{rank}"
-            if affinity:
-                summary = directory / candidate / f"affinity_{candidate}.json"
-                fields = ("affinity_pred_value", "affinity_probability_binary")
-            else:
-                structure = directory / candidate / (stem + suffix)
-                if not structure.is_file() or structure.stat().st_size == 0:
-                    raise RuntimeError(f"Missing output for {stem}")
-                summary = directory / candidate / f"confidence_{stem}.json"
-                fields = CONFIDENCE_FIELDS
+        for structure, summary, fields, label in _expected_outputs(directory, candidate, samples, output_format,
+                                                                    affinity):
+            if structure is not None and (not structure.is_file() or structure.stat().st_size == 0):
+                raise RuntimeError(f"prediction output missing or empty: {structure.name} ({label})")
             if not summary.is_file():
-                raise RuntimeError(f"Missing output for {stem}")
-            values = json.loads(summary.read_text())
-            for key in fields:
-                value = values.get(key)
-                if isinstance(value, bool) or not isinstance(value, (int, float)) or not math.isfinite(value):
-                    raise RuntimeError(f"Invalid confidence summary for {stem}")
+                raise RuntimeError(f"prediction output missing: {summary.name} ({label})")
+            data = json.loads(summary.read_text())
+            bad = [key for key in fields if not _finite_number(data.get(key))]
+            if bad:
+                raise RuntimeError(f"summary {summary.name} ({label}) lacks finite values for {', '.join(bad)}")
 
 
-def _boltz_predict(args, settings_base):
-    """``Trainer.predict`` replacement that runs the A/B rounds over Boltz's
-    own preprocessed batches (reference benchmark.py:55-240, 300-320)."""
-    from boltz.data.write.writer import BoltzAffinityWriter, BoltzWriter
-    from torch.utils.data import DataLoader
+# --------------------------------------------------------------- Boltz CLI
 
-    from .__main__ import InferenceAdapter
 
-    def predict(original, trainer, model, *positional, **keywords):
-        writers = [c for c in trainer.callbacks if isinstance(c, (BoltzWriter, BoltzAffinityWriter))]
+def _option(arguments, name, default=None):
+    """Value of ``--name value`` / ``--name=value`` in a Boltz argument list."""
+    for index, arg in enumerate(arguments):
+        if arg == name and index + 1 < len(arguments):
+            return arguments[index + 1]
+        if arg.startswith(name + "="):
+            return arg.split("=", 1)[1]
+    return default
+
+
+class _BoltzAB:
+    """``Trainer.predict`` stand-in that runs the A/B session over the
+    batches Boltz's own data module prepared (loaded once, so every round
+    sees the same features)."""
+
+    def __init__(self, args, settings, original_predict):
+        self.args = args
+        self.settings = settings
+        self.original = original_predict
+
+    def __call__(self, trainer, model, *positional, **keywords):
+        from boltz.data.write.writer import BoltzAffinityWriter, BoltzWriter
+        from torch.utils.data import DataLoader
+
+        from .__main__ import InferenceAdapter
+
+        writers = [cb for cb in trainer.callbacks if isinstance(cb, (BoltzWriter, BoltzAffinityWriter))]
         if len(writers) != 1:
-            raise RuntimeError("Expected one Boltz prediction writer")
+            raise RuntimeError(f"expected exactly one Boltz writer callback, found {len(writers)}")
         writer = writers[0]
         phase = "affinity" if isinstance(writer, BoltzAffinityWriter) else "structure"
-        output = writer.output_dir.parent / "benchmark" / phase
-        output.mkdir(parents=True)
-        samples = model.predict_args["diffusion_samples"]
-        settings = dict(settings_base, phase=phase, prediction_settings=model.predict_args)
-        recorder = ABRecorder(model, seed=args.seed, atol=args.atol, rtol=args.rtol, settings=settings,
-                              output=output)
-        datamodule = keywords["datamodule"]
-        started = time.perf_counter()
-        batches = list(datamodule.predict_dataloader())  # the same features for every round
+        out_dir = writer.output_dir.parent / "benchmark" / phase
+        out_dir.mkdir(parents=True)
+        session = ABSession(model, seed=self.args.seed, tolerance=Tolerance(self.args.atol, self.args.rtol),
+                            settings=dict(self.settings, phase=phase, prediction_settings=model.predict_args),
+                            output=out_dir)
+        data = keywords["datamodule"]
+        t0 = time.perf_counter()
+        batches = list(data.predict_dataloader())
         ids = [record.id for batch in batches for record in batch["record"]]
-        if ids != [r.id for r in datamodule.manifest.records]:
-            raise RuntimeError("Prediction loader changed candidate identity or order")
-        recorder.report["feature_load_s"] = time.perf_counter() - started
-        step = model.predict_step
-        normal_output = writer.output_dir
-        adapter = InferenceAdapter(optimize=False)  # --no_kernels and failure checks only
-        trainer.callbacks.append(adapter)
+        if ids != [record.id for record in data.manifest.records]:
+            raise RuntimeError("the prediction loader reordered or dropped candidates")
+        session.report["feature_load_s"] = time.perf_counter() - t0
+        final_dir = writer.output_dir
+        raw_step = model.predict_step
 
-        def measured_step(batch, *a, **kw):
+        def step(batch, *a, **kw):
             if len(batch["record"]) != 1:
-                raise RuntimeError("Only one input per model call is supported")
-            return recorder.measured_call(batch["record"][0].id, step, batch, *a, **kw)
+                raise RuntimeError("the A/B run needs one candidate per model call (batch size 1)")
+            return session.call(batch["record"][0].id, raw_step, batch, *a, **kw)
 
-        def one_round(recipe, iteration, profiled=False):
-            final = recipe == "optimized" and iteration == args.repeats and not profiled
-            # The last optimized round writes where Boltz's affinity stage reads.
-            writer.output_dir = normal_output if final else (
-                output / recipe / ("profile" if profiled else f"round-{iteration:02}"))
+        def one_round(recipe, iteration, profiled):
+            last = recipe == RECIPES[-1] and iteration == self.args.repeats and not profiled
+            # the last optimized round writes where Boltz's next stage reads
+            writer.output_dir = final_dir if last else out_dir / recipe / (
+                "profile" if profiled else f"round-{iteration:02}")
             writer.output_dir.mkdir(parents=True, exist_ok=True)
-
-            def body():
-                return original(trainer, model, *positional, **keywords)
-
-            result = recorder.run_round(recipe, iteration, body, ids, profiled)
-            validate_outputs(writer.output_dir, ids, samples,
-                             output_format=getattr(writer, "output_format", "mmcif"),
-                             affinity=phase == "affinity")
+            result = self.original(trainer, model, *positional, **keywords)
+            validate_outputs(writer.output_dir, ids, model.predict_args["diffusion_samples"],
+                             output_format=getattr(writer, "output_format", "mmcif"), affinity=phase == "affinity")
             return result
 
-        result = None
+        checks = InferenceAdapter(optimize=False)  # --no_kernels on the model and the failure checks
+        trainer.callbacks.append(checks)
         try:
-            with patch.object(datamodule, "predict_dataloader",
-                              lambda: DataLoader(batches, batch_size=None, num_workers=0)), \
-                    patch.object(model, "predict_step", measured_step):
-                for recipe in RECIPES:
-                    if recipe == "optimized":
-                        install(model)
-                    with stage_timers(model, recorder.events):
-                        for iteration in range(args.repeats + 1):
-                            result = one_round(recipe, iteration)
-                if args.profile:
-                    with stage_timers(model, recorder.events):
-                        profile_round(lambda: one_round(RECIPES[-1], args.repeats + 1, True), output)
-            recorder.finish()
-        except BaseException as error:
-            if recorder.report["status"] == "running":
-                recorder.fail(error)
-            raise
+            with _shadowed(data, "predict_dataloader", lambda: DataLoader(batches, batch_size=None, num_workers=0)), \
+                    _shadowed(model, "predict_step", step):
+                result = session.run(ids, one_round, self.args.repeats, profile=self.args.profile)
         finally:
-            writer.output_dir = normal_output
-            trainer.callbacks.remove(adapter)
-        print(output / "timings.json")
+            writer.output_dir = final_dir
+            trainer.callbacks.remove(checks)
+        print(out_dir / "timings.json")
         return result
 
-    return predict
+
+@contextmanager
+def _shadowed(obj, name, value):
+    """``obj.name = value`` as an instance attribute for the duration, then
+    whatever instance attribute (or none) was there before."""
+    missing = object()
+    before = vars(obj).get(name, missing)
+    setattr(obj, name, value)
+    try:
+        yield
+    finally:
+        if before is missing:
+            delattr(obj, name)
+        else:
+            setattr(obj, name, before)
 
 
 def main(arguments=None):
@@ -416,34 +545,30 @@ def main(arguments=None):
     from .__main__ import require_boltz
 
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0], allow_abbrev=False)
-    parser.add_argument("--repeats", type=int, default=3)
-    parser.add_argument("--profile", action="store_true")
+    parser.add_argument("--repeats", type=int, default=3, help="warm rounds per recipe (after one first round)")
+    parser.add_argument("--profile", action="store_true", help="add one optimized round under torch.profiler")
     parser.add_argument("--atol", type=float, default=ATOL)
     parser.add_argument("--rtol", type=float, default=RTOL)
-    args, rest = parser.parse_known_args(arguments)
+    args, boltz_args = parser.parse_known_args(arguments)
     if args.repeats < 1:
-        parser.error("Use at least one warm repeat")
-    found = require_boltz()
+        parser.error("--repeats must be at least 1")
+    boltz_version = require_boltz()
     if torch.cuda.device_count() != 1:
-        raise RuntimeError("Run the comparison with one visible GPU")
+        raise RuntimeError(f"the A/B run needs exactly one visible GPU, found {torch.cuda.device_count()}")
     from boltz.main import cli
     from pytorch_lightning import Trainer
 
-    if rest[:1] == ["predict"]:
-        rest.pop(0)
-    with cli.commands["predict"].make_context("predict", list(rest)) as context:
-        options = context.params
-    args.seed = options["seed"] if options["seed"] is not None else 42
-    rest += ["--seed", str(args.seed), "--no_kernels"]
-    settings = dict(boltz=found, input=str(options["data"]), seed=args.seed)
-    ab = _boltz_predict(args, settings)
-    original = Trainer.predict
-
-    def predict(trainer, model, *positional, **keywords):
-        return ab(original, trainer, model, *positional, **keywords)
-
-    with patch.object(Trainer, "predict", predict):
-        cli(["predict", *rest], standalone_mode=False)
+    if boltz_args[:1] == ["predict"]:
+        boltz_args = boltz_args[1:]
+    data = boltz_args[0] if boltz_args and not boltz_args[0].startswith("-") else None
+    args.seed = int(_option(boltz_args, "--seed", 42))
+    if _option(boltz_args, "--seed") is None:
+        boltz_args += ["--seed", str(args.seed)]  # the upstream and optimized runs share it
+    if "--no_kernels" not in boltz_args:
+        boltz_args.append("--no_kernels")
+    ab = _BoltzAB(args, dict(boltz=boltz_version, input=data, seed=args.seed), Trainer.predict)
+    with _shadowed(Trainer, "predict", lambda trainer, model, *p, **k: ab(trainer, model, *p, **k)):
+        cli(["predict", *boltz_args], standalone_mode=False)
 
 
 if __name__ == "__main__":

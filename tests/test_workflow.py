@@ -33,22 +33,22 @@ def test_every_candidate_and_sample_is_required(tmp_path):
     validate_outputs(tmp_path, ["first", "second"], 2)
     confidence = tmp_path / "second/confidence_second_model_1.json"
     confidence.unlink()
-    with pytest.raises(RuntimeError, match="Missing output for second_model_1"):
+    with pytest.raises(RuntimeError, match=r"missing: confidence_second_model_1\.json"):
         validate_outputs(tmp_path, ["first", "second"], 2)
     confidence.write_text(json.dumps(dict.fromkeys(CONFIDENCE_FIELDS, float("nan"))))
-    with pytest.raises(RuntimeError, match="Invalid confidence"):
+    with pytest.raises(RuntimeError, match="lacks finite values for confidence_score"):
         validate_outputs(tmp_path, ["first", "second"], 2)
     (tmp_path / "first/first_model_0.cif").write_text("")
-    with pytest.raises(RuntimeError, match="Missing output for first_model_0"):
+    with pytest.raises(RuntimeError, match=r"missing or empty: first_model_0\.cif"):
         validate_outputs(tmp_path, ["first"], 1)
-    with pytest.raises(RuntimeError, match="No inputs"):
+    with pytest.raises(RuntimeError, match="no candidate was predicted"):
         validate_outputs(tmp_path, [], 1)
 
 
 def test_pdb_and_affinity_outputs(tmp_path):
     write_prediction(tmp_path, "ligand", 1, suffix=".pdb")
     validate_outputs(tmp_path, ["ligand"], 1, output_format="pdb")
-    with pytest.raises(RuntimeError, match="Missing output for ligand_model_0"):
+    with pytest.raises(RuntimeError, match=r"missing or empty: ligand_model_0\.cif"):
         validate_outputs(tmp_path, ["ligand"], 1)  # mmCIF expected, PDB written
     affinity = tmp_path / "ligand/affinity_ligand.json"
     affinity.write_text(json.dumps(dict(affinity_pred_value=-2.0, affinity_probability_binary=0.8)))
@@ -56,7 +56,7 @@ def test_pdb_and_affinity_outputs(tmp_path):
     for bad in ('{"affinity_pred_value": -2}', '{"affinity_pred_value": -2, "affinity_probability_binary": true}',
                 '{"affinity_pred_value": "x", "affinity_probability_binary": 0.5}'):
         affinity.write_text(bad)
-        with pytest.raises(RuntimeError, match="Invalid confidence"):
+        with pytest.raises(RuntimeError, match="lacks finite values for affinity_"):
             validate_outputs(tmp_path, ["ligand"], 5, affinity=True)
 
 
@@ -178,3 +178,21 @@ def test_compare_counts_values_outside_the_tolerance():
     assert compare(value, expected, 2e-2, 1e-2)["failing_values"] == 0
     assert compare(torch.tensor([float("nan")]), torch.tensor([1.0]), 1.0, 1.0)["failing_values"] == 1
     assert compare(torch.zeros(3), torch.zeros(3), 0.0, 0.0)["relative_l2_error"] is None
+
+
+def test_benchmark_cli_shares_the_seed_and_restores_predict(fake_boltz, monkeypatch):
+    """``benchmark.main`` hands Boltz's CLI its own arguments plus one seed
+    for both recipes (42 unless given) and ``--no_kernels``; while the CLI
+    runs, ``Trainer.predict`` is the A/B stand-in, afterwards the original."""
+    monkeypatch.setattr(torch.cuda, "device_count", lambda: 1)
+    original = fake_boltz.Trainer.predict
+    seen = []
+    fake_boltz.cli.side_effect = lambda argv, **kw: seen.append((argv, fake_boltz.Trainer.predict is original))
+    benchmark.main(["predict", "input.yaml", "--out_dir", "out", "--repeats", "2"])
+    benchmark.main(["predict", "input.yaml", "--seed=7", "--no_kernels", "--profile"])
+    assert seen[0] == (["predict", "input.yaml", "--out_dir", "out", "--seed", "42", "--no_kernels"], False)
+    assert seen[1] == (["predict", "input.yaml", "--seed=7", "--no_kernels"], False)
+    assert fake_boltz.Trainer.predict is original
+    monkeypatch.setattr(torch.cuda, "device_count", lambda: 2)
+    with pytest.raises(RuntimeError, match="exactly one visible GPU"):
+        benchmark.main(["predict", "input.yaml"])
