@@ -1,54 +1,69 @@
 #!/usr/bin/env python
-"""Benchmark: one Boltz-2 PairformerLayer forward at N=1024 on one MI355X.
+"""Benchmark of the gfx950 hot path on one MI355X.
 
-Metric: "Pairformer layer ms @N=1024 bf16; tri-attn/mult % of
-MFMA/HBM roofline".  A step is one full PairformerLayer forward (v2, eval):
-tri_mul_out, tri_mul_in, tri_att_start, tri_att_end, transition_z on the fp32
-pair stream with the bf16 gfx950 kernels, then the fp32 sequence stack.  Inputs
-(z [1,N,N,128], s [1,N,384], masks all ones) and random-init weights (seed 0,
-N(0, 0.08), norm weights N(1, 0.08)) are resident in HBM before timing.
+Default workload (BASELINE.json metric "Pairformer layer ms @N=1024 bf16;
+tri-attn/mult % of MFMA/HBM roofline"): one Boltz-2 PairformerLayer forward
+at N=1024 (configs[3], one of the 64 trunk blocks): tri_mul_out, tri_mul_in,
+tri_att_start, tri_att_end, transition_z on the fp32 pair stream with the bf16
+gfx950 kernels, then the fp32 sequence stack.  Inputs (z [1,N,N,128],
+s [1,N,384], masks all ones) and random-init weights (seed 0, N(0, 0.08),
+norm weights N(1, 0.08)) are resident in HBM before timing.
+
+Other workloads (--workload), each on one BASELINE config:
+  trimul           configs[2]: TriangleMultiplication out and in, N=768, 5% of tokens masked
+  triattn          configs[1]: TriangleAttention start and end, N=512, last 51 tokens masked
+  trunk            configs[3]: the 64-block PairformerModule at N=1024
+  diffusion-step   configs[4]: 20 consecutive denoiser steps of the score model's transformer
+                   stacks (atom encoder / decoder 3 + 3 blocks at 5 x 8192 atoms, token
+                   transformer 24 blocks at 5 x 1024 tokens), fp32 as the reference runs them
+  token-attention, diffusion   single diffusion modules at configs[4] shapes
 
 Prints one JSON line.  ``roofline`` covers the kernel with the largest share
-of the layer, timed with HIP events on the launch stream; ``breakdown`` lists
-every kernel.  ``cpu_baseline`` times the CPU oracle on the host cores for one
-layer at --cpu-n (default: the benchmark N) -- a reported baseline only.
+of the step, timed with HIP events on the launch stream; its ``bound`` is
+whichever of flop time (at the MFMA peak) and byte time (at 8 TB/s) is larger.
+``modules`` gives each triangle module's time against its roofline T* =
+max(F / 2.5 PFLOP/s, B / 8 TB/s) (F, B as in BASELINE.md section 2).
+``cpu_baseline`` times the CPU oracle on the host cores (a reported baseline,
+not the target), following BASELINE.md section 3.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
+import statistics
 import sys
 import time
 
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 # Transcendental issue rate: one 64-lane v_exp_f32 per 8 cycles per SIMD
 # (probe on the box), 256 CUs x 4 SIMDs at 2.4 GHz.
 EXP_PER_SIMD_CYCLE, SIMDS, CLOCK_HZ = 64 / 8, 1024, 2.4e9
+ROOT = os.path.dirname(os.path.abspath(__file__))
+WORKLOADS = ("pairformer", "trunk", "trimul", "triattn", "diffusion-step", "token-attention", "diffusion")
 
 
 def parse():
-    p = argparse.ArgumentParser(description=__doc__)
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--steps", type=int, default=None, help="timed steps (default depends on the workload)")
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--n", type=int, default=1024)
-    p.add_argument("--cpu-n", type=int, default=None, help="token count of the CPU sample (default: --n)")
+    p.add_argument("--n", type=int, default=None, help="token count (default: the workload's config)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--kernel-reps", type=int, default=3, help="repetitions of the per-kernel timing pass")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first copy 1 GiB device-to-device (a kernel of known traffic for scaling PMC byte counters)")
-    p.add_argument("--workload", choices=("pairformer", "token-attention", "diffusion"), default="pairformer",
-                   help="pairformer: the headline PairformerLayer line (default); token-attention: the diffusion "
-                        "token transformer's AttentionPairBias (16 x 48 heads, 5 samples, prepacked bias); "
-                        "diffusion: the score model's AdaLN / ConditionedTransitionBlock forwards and their fused "
-                        "kernels at the token and atom transformer shapes")
+    p.add_argument("--workload", choices=WORKLOADS, default="pairformer")
     return p.parse_args()
 
 
 def init_weights(module, seed: int):
+    """Every parameter N(0, 0.08), norm weights N(1, 0.08) (the reference
+    tests' convention, tests/test_operator_additions.py:43-47)."""
     import torch
 
     g = torch.Generator().manual_seed(seed)
@@ -59,26 +74,72 @@ def init_weights(module, seed: int):
     return module
 
 
+def fan_in_weights(module, seed: int):
+    """Weights N(0, 1 / fan_in), norm weights N(1, 0.08), vectors N(0, 0.08):
+    keeps 24 residual blocks of width 768 bounded (the 0.08 convention
+    amplifies each such block's output about a hundredfold)."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in module.named_parameters():
+            if "norm" in name and name.endswith("weight"):
+                p.copy_(1 + 0.08 * torch.randn(p.shape, generator=g))
+            elif p.dim() == 2:
+                p.copy_(torch.randn(p.shape, generator=g) / math.sqrt(p.shape[1]))
+            else:
+                p.copy_(0.08 * torch.randn(p.shape, generator=g))
+    return module
+
+
+# ----------------------------------------------------------------- rooflines
+
+
+def tri_module_cost(kind: str, n: int):
+    """(F flops, B compulsory bytes) of one triangle module direction
+    tri-attention F = 512 N^3 + 164864 N^2,
+    tri-multiplication F = 256 N^3 + 196608 N^2; B = N^2 (128*4 + 4 + 128*2)
+    (fp32 z and mask in, bf16 out)."""
+    n2, n3 = float(n) ** 2, float(n) ** 3
+    f = 512 * n3 + 164864 * n2 if kind == "triattn" else 256 * n3 + 196608 * n2
+    return f, n2 * (128 * 4 + 4 + 128 * 2)
+
+
+def t_star_ms(flops, nbytes, peak_tflops=PEAK_BF16_TFLOPS):
+    return max(flops / (peak_tflops * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) * 1e3
+
+
 def kernel_table(n: int):
     """Algorithmic flops and compulsory HBM bytes per launch, per kernel."""
     n2, n3 = float(n) ** 2, float(n) ** 3
     return {
-        # name: (flops, bytes, bound)
-        "trimul_proj": (2 * n2 * 128 * 512, n2 * (512 + 4 + 2 * 256), "hbm"),
-        "trimul_contract": (2 * 128 * n3, n2 * 128 * 2 * 3, "mfma"),
-        "trimul_out": (2 * n2 * 128 * 256, n2 * (256 + 512 + 512), "hbm"),
-        "triattn_proj": (2 * n2 * 128 * 388, n2 * (512 + 4 + 3 * 256 + 16), "hbm"),
-        "triattn_core": (4 * 4 * 32 * n3, n2 * 4 * 3 * 64 + n2 * 256, "mfma"),
-        "triattn_out": (2 * n2 * 128 * 256, n2 * (512 + 256 + 512), "hbm"),
-        "pair_transition": (2 * n2 * 128 * (1536 + 16), n2 * (1024 + 64), "hbm"),  # + the fused pair bias
+        "trimul_proj": (2 * n2 * 128 * 512, n2 * (512 + 4 + 2 * 256)),
+        "trimul_contract": (2 * 128 * n3, n2 * 128 * 2 * 3),
+        "trimul_out": (2 * n2 * 128 * 256, n2 * (256 + 512 + 512)),
+        "triattn_proj": (2 * n2 * 128 * 388, n2 * (512 + 4 + 3 * 256 + 16)),
+        "triattn_core": (4 * 4 * 32 * n3, n2 * 4 * 3 * 64 + n2 * 256),
+        "triattn_out": (2 * n2 * 128 * 256, n2 * (512 + 256 + 512)),
+        "pair_transition": (2 * n2 * 128 * (1536 + 16), n2 * (1024 + 64)),  # + the fused pair bias
     }
+
+
+def roofline_of(flops, nbytes, ms, peak_tflops=PEAK_BF16_TFLOPS):
+    """Bound, achieved rate and fraction of peak of one launch; the bound is
+    whichever of flop time and byte time is larger."""
+    mfma = flops / (peak_tflops * 1e12) >= nbytes / (PEAK_HBM_GBS * 1e9)
+    if mfma:
+        achieved, peak, unit = flops / (ms * 1e-3) / 1e12, peak_tflops, "TFLOP/s"
+    else:
+        achieved, peak, unit = nbytes / (ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+    return {"bound": "mfma" if mfma else "hbm", "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4)}
 
 
 def measured_traffic(kernel: str, n: int):
     """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter
     summary (FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy), when it was
     taken at this N; None otherwise."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"hbm_traffic_n{n}.json")
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_n{n}.json")
     try:
         with open(path) as f:
             data = json.load(f)
@@ -87,329 +148,142 @@ def measured_traffic(kernel: str, n: int):
     return data.get("bytes_per_launch", {}).get(kernel) if data.get("n") == n else None
 
 
-def per_kernel_times(layer, s, z, mask, pair_mask, z_out, ws, reps):
-    """Average ms per launch of every kernel of the layer, from HIP events
-    recorded on torch's current stream (the stream the kernels launch on)."""
-    import torch
-    from boltz_lumi_amd import ops
+def exp_co_bound(n, core_ms):
+    """Exp co-bound of the attention core (H N^3 exponentials per direction at
+    the measured v_exp_f32 issue rate) and its MFMA+exp issue floor."""
+    exps = 4.0 * n ** 3
+    exp_ms = exps / (EXP_PER_SIMD_CYCLE * SIMDS * CLOCK_HZ) * 1e3
+    mfma_ms = 4 * 4 * 32 * float(n) ** 3 / (PEAK_BF16_TFLOPS * 1e12) * 1e3
+    return {"exp_ms": round(exp_ms, 4), "mfma_ms": round(mfma_ms, 4), "issue_floor_ms": round(exp_ms + mfma_ms, 4),
+            "issue_floor_frac": round((exp_ms + mfma_ms) / core_ms, 4)}
 
-    zi, zo, mb = z[0], z_out[0], pair_mask[0].float().contiguous()
-    plan = []
-    for mod, outgoing, first in ((layer.tri_mul_out, True, True), (layer.tri_mul_in, False, False)):
-        mode = ops.OUT_RESIDUAL if first else ops.OUT_ACCUMULATE
-        src = zi if first else zo
-        for stage, name in ((1, "trimul_proj"), (2, "trimul_contract"), (4, "trimul_out")):
-            plan.append((name, lambda m=mod, o=outgoing, md=mode, x=src, st=stage:
-                         ops.trimul(m, x, mb, o, md, zo, ws, stages=st)))
-    for mod, starting in ((layer.tri_att_start, True), (layer.tri_att_end, False)):
-        for stage, name in ((1, "triattn_proj"), (2, "triattn_core"), (4, "triattn_out")):
-            plan.append((name, lambda m=mod, st_=starting, st=stage:
-                         ops.triattn(m, zo, mb, st_, ops.OUT_ACCUMULATE, zo, ws, stages=st)))
-    # the transition's epilogue also writes the sequence stack's pair bias, as in PairformerLayer.forward
-    bias = torch.empty((1, 16) + zo.shape[:2], device=zo.device)
-    pb = (layer.attention.proj_z[0], layer.attention.proj_z[1], bias[0])
-    plan.append(("pair_transition", lambda: ops.pair_transition(layer.transition_z, zo, ops.OUT_ACCUMULATE, zo,
-                                                                pair_bias=pb)))
-    plan.append(("sequence_stack", lambda: layer.sequence_stack(s, z_out, mask, pair_bias=bias)))
-    totals = {}
-    counts = {}
-    for _ in range(reps):
-        events = []
-        for name, fn in plan:
+
+def event_timer():
+    import torch
+
+    class Timer:
+        def __init__(self):
+            self.spans = []
+
+        def run(self, name, fn):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             fn()
             e1.record()
-            events.append((name, e0, e1))
-        torch.cuda.synchronize()
-        for name, e0, e1 in events:
-            totals[name] = totals.get(name, 0.0) + e0.elapsed_time(e1)
-            counts[name] = counts.get(name, 0) + 1
-    return {k: (totals[k] / counts[k], counts[k] // reps) for k in totals}
+            self.spans.append((name, e0, e1))
 
-
-def cpu_baseline(n: int, seed: int):
-    import torch
-
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import boltz_ref as R  # the checker, timed as the reference CPU path
-
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    layer = init_weights(R.PairformerLayer(), seed).eval()
-    g = torch.Generator().manual_seed(seed)
-    z = torch.randn(1, n, n, 128, generator=g)
-    s = torch.randn(1, n, 384, generator=g)
-    mask, pm = torch.ones(1, n), torch.ones(1, n, n)
-    with torch.inference_mode():
-        layer(s[:, :32], z[:, :32, :32], mask[:, :32], pm[:, :32, :32], chunk_size_tri_attn=32)  # thread warm-up
-        t0 = time.perf_counter()
-        layer(s, z, mask, pm, chunk_size_tri_attn=64)
-        dt = time.perf_counter() - t0
-    return dt * 1e3, cores
-
-
-PEAK_FP32_TFLOPS = 157.3
-
-
-def token_attention(args):
-    """One token-transformer AttentionPairBias forward (c_s 768, 16 heads x 48)
-    over 5 samples of N tokens sharing one prepacked [1, N, N, 24 * 16] bias
-    (BASELINE configs[4] shape, one of the 24 layers), through the drop-in
-    ``prepared_forward``.  The roofline covers the fused attention kernel: fp32
-    MFMA flops 4 * 16 * 48 * N^2 per sample."""
-    import torch
-    from boltz_lumi_amd import layers, ops
-    from boltz_lumi_amd.pair_bias import prepare_token_bias, prepared_forward
-
-    dev = torch.device("cuda:0")
-    n, samples, heads, width = args.n, 5, 16, 768
-    module = init_weights(layers.AttentionPairBias(width, num_heads=heads, compute_pair_bias=False), 0).to(dev).eval()
-    g = torch.Generator().manual_seed(0)
-    s = torch.randn(samples, n, width, generator=g).to(dev)
-    bias = prepare_token_bias(torch.randn(1, n, n, 24 * heads, generator=g).to(dev))[..., :heads]
-    mask = torch.ones(samples, n, device=dev)
-
-    def step():
-        prepared_forward(module, s, bias, mask, s, multiplicity=samples)
-
-    with torch.inference_mode():
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(args.steps):
-            step()
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / args.steps
-        # the attention kernel alone, on the same inputs
-        proj = torch.randn(n, 4 * width, generator=g).to(dev)
-        q, k, v, gl = proj.split(width, dim=-1)
-        b0, m0 = bias[0].movedim(-1, 0), mask[0]
-        out = torch.empty(n, width, device=dev)
-        reps = max(args.steps, 10) * samples
-        ops.seq_attention(q, k, v, b0, m0, gl, module.inf, out=out)
-        e0.record()
-        for _ in range(reps):
-            ops.seq_attention(q, k, v, b0, m0, gl, module.inf, out=out)
-        e1.record()
-        torch.cuda.synchronize()
-        kms = e0.elapsed_time(e1) / reps
-    flops = 4.0 * heads * 48 * n * n
-    achieved = flops / (kms * 1e-3) / 1e12
-    out_line = {
-        "metric": "token-transformer AttentionPairBias ms @N=1024, 5 samples",
-        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic (s ~ N(0,1), bias ~ N(0,1) prepacked, masks ones; weights seed 0)",
-        "config": {"workload": f"diffusion token-transformer AttentionPairBias forward (prepared_forward), "
-                               f"c_s=768, 16 heads x 48, {samples} samples x N={n} (BASELINE configs[4] shape)",
-                   "n_tokens": n, "samples": samples},
-        "roofline": {"kernel": "seq_attention", "bound": "mfma", "achieved": round(achieved, 2),
-                     "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-                     "traffic": None, "kernel_ms_per_sample": round(kms, 4)},
-    }
-    if not args.no_cpu_baseline:
-        out_line["cpu_baseline"] = token_attention_cpu(min(n, args.cpu_n or n))
-    print(json.dumps(out_line), flush=True)
-
-
-def token_attention_cpu(n: int):
-    import torch
-
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import boltz_ref as R  # the checker, timed as the reference CPU path
-
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    module = init_weights(R.AttentionPairBias(768, num_heads=16, compute_pair_bias=False), 0).eval()
-    g = torch.Generator().manual_seed(0)
-    s = torch.randn(1, n, 768, generator=g)
-    bias = torch.randn(1, n, n, 16, generator=g)
-    mask = torch.ones(1, n)
-    with torch.inference_mode():
-        module(s[:, :32], bias[:, :32, :32], mask[:, :32], s[:, :32])
-        t0 = time.perf_counter()
-        module(s, bias, mask, s)
-        dt = time.perf_counter() - t0
-    return {"value": round(dt * 1e3 * 5, 1), "unit": "ms per 5-sample forward (1 sample timed, x5)",
-            "cores": cores, "kind": "port",
-            "sample": f"one sample of the fp32 CPU oracle AttentionPairBias at N={n} (oracle/boltz_ref.py), "
-                      f"{cores} threads, scaled x5"}
-
-
-def diffusion(args):
-    """The diffusion score model's per-layer modules at BASELINE configs[4]
-    shapes (5 samples; token transformer 1024 tokens x 768 with 16 heads,
-    atom transformer 8192 atoms x 128 with 4 heads in windows of 32 queries
-    over 128 keys): the AdaLN, AttentionPairBias (prepared_forward, the fused
-    batched attention) and ConditionedTransitionBlock forwards of one layer of
-    each transformer, fp32 as the reference runs them (diffusion.py:37-68,
-    pair_bias.py:15-36), plus the fused elementwise kernels alone (bmx_adaln,
-    the GATED_SWIGLU and GATE epilogues) against the 8 TB/s HBM roofline.
-    Bytes per launch: AdaLN 16 M D (a, scale, shift in, out), GATED_SWIGLU
-    16 M Di (u [M, 2 Di] and b in, out), GATE 12 M D."""
-    import torch
-    from boltz_lumi_amd import layers, ops
-    from boltz_lumi_amd.pair_bias import prepare_token_bias, prepared_forward
-
-    dev = torch.device("cuda:0")
-    samples = 5
-    shapes = {"token": (samples * args.n, 768, 768), "atom": (samples * 8192, 128, 128)}
-    g = torch.Generator().manual_seed(0)
-
-    def timed(fn, reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        fn()
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps
-
-    kernels, blocks = {}, {}
-    heads = {"token": 16, "atom": 4}
-    modules = {name: (init_weights(layers.AdaLN(d, dc), 0).to(dev).eval(),
-                      init_weights(layers.AttentionPairBias(d, num_heads=heads[name], compute_pair_bias=False), 2)
-                      .to(dev).eval(),
-                      init_weights(layers.ConditionedTransitionBlock(d, dc), 1).to(dev).eval())
-               for name, (m, d, dc) in shapes.items()}
-    with torch.inference_mode():
-        for name, (m, d, dc) in shapes.items():
-            di = 2 * d
-            adaln, apb, ctb = modules[name]
-            a = torch.randn(m, d, generator=g).to(dev)
-            c = torch.randn(m, dc, generator=g).to(dev)
-            if name == "token":  # 5 samples sharing one prepacked layer bias
-                qs = a.view(samples, args.n, d)
-                ks, mult = qs, samples
-                z = prepare_token_bias(torch.randn(1, args.n, args.n, heads[name], generator=g).to(dev))
-                kmask = torch.ones(samples, args.n, device=dev)
-            else:  # windows of 32 atoms over the 128 atoms centred on them (to_keys)
-                nw, w, h = 8192 // 32, 32, 128
-                index = torch.stack([torch.clamp(torch.arange(h) + w * i - (h - w) // 2, 0, 8191)
-                                     for i in range(nw)]).to(dev)
-                qs = a.view(samples * nw, w, d)
-                ks, mult = a.view(samples, 8192, d)[:, index].reshape(samples * nw, h, d), 1
-                z = torch.randn(samples * nw, heads[name], w, h, generator=g).to(dev).movedim(1, -1)
-                kmask = torch.ones(samples * nw, h, device=dev)
-
-            gate = init_weights(torch.nn.Linear(dc, d), 3).to(dev)
-
-            def layer():  # upstream DiffusionTransformerLayer.forward
-                b = adaln(a, c)
-                bq = b.view(qs.shape)
-                if name == "token":
-                    k_in = bq
-                else:
-                    k_in = b.view(samples, 8192, d)[:, index].reshape(samples * nw, h, d)
-                o = prepared_forward(apb, bq, z, kmask, k_in, mult).reshape(a.shape)
-                x = a + torch.sigmoid(ops.linear_fp32(c, gate)) * o
-                return x + ctb(x, c)
-
-            for _ in range(args.warmup):
-                layer()
+        def averages(self):
             torch.cuda.synchronize()
-            blocks[name] = timed(layer, args.steps)
-            blocks[name + "_attention"] = timed(lambda: prepared_forward(apb, qs, z, kmask, ks, mult), args.steps)
-            # Each kernel cycles over enough input sets that successive launches
-            # do not find their operands in the 256 MB Infinity Cache.
-            sets = 1 + (768 << 20) // (16 * m * d)
-            bufs = [{"a": torch.randn(m, d, generator=g).to(dev), "scale": torch.randn(m, d, generator=g).to(dev),
-                     "shift": torch.randn(m, d, generator=g).to(dev), "u": torch.randn(m, 2 * di, generator=g).to(dev),
-                     "b": torch.randn(m, di, generator=g).to(dev), "g": torch.randn(m, d, generator=g).to(dev),
-                     "y": torch.randn(m, d, generator=g).to(dev)} for _ in range(sets)]
-            reps = sets * max(1, max(args.steps, 10) // sets)
-            turn = [0]
+            tot, cnt = {}, {}
+            for name, e0, e1 in self.spans:
+                tot[name] = tot.get(name, 0.0) + e0.elapsed_time(e1)
+                cnt[name] = cnt.get(name, 0) + 1
+            return {k: tot[k] / cnt[k] for k in tot}, cnt
 
-            def nxt():
-                turn[0] = (turn[0] + 1) % sets
-                return bufs[turn[0]]
-
-            for kname, fn, nbytes in (
-                    ("adaln", lambda: (lambda t: ops.adaln_modulate(t["a"], t["scale"], t["shift"], 1e-5))(nxt()),
-                     16 * m * d),
-                    ("gated_swiglu", lambda: (lambda t: ops.epilogue(t["u"], t["b"], None, ops.GATED_SWIGLU))(nxt()),
-                     16 * m * di),
-                    ("gate", lambda: (lambda t: ops.epilogue(t["g"], t["y"], None, ops.GATE))(nxt()), 12 * m * d)):
-                ms = timed(fn, reps)
-                gbs = nbytes / (ms * 1e-3) / 1e9
-                kernels[f"{kname}_{name}"] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(gbs, 1),
-                                              "frac": round(gbs / PEAK_HBM_GBS, 4), "input_sets": sets}
-            del bufs
-    ms = blocks["token"] + blocks["atom"]
-    dom = kernels["gated_swiglu_token"]
-    out_line = {
-        "metric": "diffusion score-model modules (AdaLN + AttentionPairBias + ConditionedTransitionBlock) ms per "
-                  "token + atom layer, 5 samples; AdaLN/gating kernels % of HBM roofline",
-        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic (activations and conditioning ~ N(0,1); weights seeds 0 and 1)",
-        "config": {"workload": f"diffusion score-model AdaLN + AttentionPairBias + ConditionedTransitionBlock "
-                               f"forwards, token layer ({samples} x {args.n} x 768, 16 heads, one shared bias) + "
-                               f"atom layer ({samples} x 8192 x 128, 4 heads, windows of 32 queries x 128 keys), "
-                               f"BASELINE configs[4] shapes",
-                   "n_tokens": args.n, "n_atoms": 8192, "samples": samples,
-                   "block_ms": {k: round(v, 4) for k, v in blocks.items()}},
-        "roofline": {"kernel": "gated_swiglu (token)", "bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": dom["frac"], "traffic": None, "kernels": kernels},
-    }
-    if not args.no_cpu_baseline:
-        out_line["cpu_baseline"] = diffusion_cpu(args.n)
-    print(json.dumps(out_line), flush=True)
+    return Timer()
 
 
-def diffusion_cpu(n: int):
+def timed_loop(fn, steps, warmup, warm_s=0.25):
+    """ms per call of ``fn`` over ``steps`` calls after ``warmup`` untimed ones
+    (continued until ``warm_s`` seconds have passed, so that the GPU has left
+    its idle clocks on the measured work itself), between device
+    synchronisations, by HIP events on the current stream."""
     import torch
 
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import boltz_ref as R  # the checker, timed as the reference CPU path
+    t0 = time.perf_counter()
+    done = 0
+    while done < warmup or (warmup and time.perf_counter() - t0 < warm_s):
+        fn()
+        done += 1
+        if done >= warmup:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, time.perf_counter() - wall0
 
+
+def line(metric, value, unit, args, steps, dtype, data, config, higher_is_better=False, **extra):
+    out = {"metric": metric, "value": round(value, 4), "unit": unit, "n_gpus": 1, "steps": steps,
+           "warmup": args.warmup, "ms_per_step": round(value, 4) if unit == "ms" else None,
+           "higher_is_better": higher_is_better, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+           "data": data, "config": config}
+    out.update(extra)
+    return out
+
+
+# ------------------------------------------------------------ CPU baselines
+
+
+def _cpu_setup():
+    import torch
+
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    return cores
+
+
+def _median_ms(fn, reps, warm=None):
+    if warm is not None:
+        warm()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times), times
+
+
+def cpu_pairformer(n_layer=1024, n_small=128):
+    """one PairformerLayer of the
+    fp32 oracle at N=128 (2 warm-ups, median of 10) and at N=1024 (one
+    warm-up at N=256, median of 2; x64 reported as the extrapolated trunk)."""
+    import torch
+
+    cores = _cpu_setup()
+    from oracle import boltz_ref as R  # the checker, timed as the reference CPU path
+
+    layer = init_weights(R.PairformerLayer(), 0).eval()
     g = torch.Generator().manual_seed(0)
-    total = 0.0
+
+    def inputs(n):
+        return (torch.randn(1, n, 384, generator=g), torch.randn(1, n, n, 128, generator=g), torch.ones(1, n),
+                torch.ones(1, n, n))
+
     with torch.inference_mode():
-        for m, d, heads in ((n, 768, 16), (8192, 128, 4)):
-            layer = init_weights(R.DiffusionTransformerLayer(heads, d, d), 0).eval()
-            a, c = torch.randn(1, m, d, generator=g), torch.randn(1, m, d, generator=g)
-            if d == 768:
-                z, mask, to_keys, a, c = torch.randn(1, m, m, heads, generator=g), torch.ones(1, m), None, a, c
-            else:  # windows of 32 atoms over the 128 atoms centred on them
-                nw, w, h = m // 32, 32, 128
-                index = torch.stack([torch.clamp(torch.arange(h) + w * i - (h - w) // 2, 0, m - 1) for i in range(nw)])
-                to_keys = lambda x: x.view(1, m, -1)[:, index].reshape(nw, h, -1)
-                z, mask = torch.randn(nw, w, h, heads, generator=g), torch.ones(nw, w)
-                a, c = a.view(nw, w, d), c.view(nw, w, d)
-            t0 = time.perf_counter()
-            layer(a, c, bias=z, mask=mask, to_keys=to_keys)
-            total += time.perf_counter() - t0
-    return {"value": round(total * 1e3 * 5, 1), "unit": "ms per token + atom layer, 5 samples (1 sample timed, x5)",
-            "cores": cores, "kind": "port",
-            "sample": f"one sample of the fp32 CPU oracle DiffusionTransformerLayer (oracle/boltz_ref.py) at {n} "
-                      f"tokens x 768 (16 heads) and 8192 atoms x 128 (4 heads, 32 x 128 windows), {cores} threads, "
-                      f"scaled x5"}
+        small = inputs(n_small)
+        run_small = lambda: layer(*small, chunk_size_tri_attn=64)
+        cfg1, _ = _median_ms(run_small, 10, warm=lambda: (run_small(), run_small()))
+        big = inputs(n_layer)
+        warm = inputs(256)
+        cfg4, times = _median_ms(lambda: layer(*big, chunk_size_tri_attn=64), 2,
+                                 warm=lambda: layer(*warm, chunk_size_tri_attn=64))
+    flops1 = 2.22e10
+    return {"value": round(cfg4, 1), "unit": "ms per layer", "cores": cores, "kind": "port",
+            "sample": f"fp32 CPU oracle (oracle/boltz_ref.py) PairformerLayer at N={n_layer}, median of 2 after a "
+                      f"warm-up at N=256, tri-attention chunked 64 rows, {cores} threads",
+            "runs_ms": [round(t, 1) for t in times],
+            "trunk_64_ms_extrapolated": round(64 * cfg4, 1),
+            "config1_n128_ms": round(cfg1, 2), "config1_gflops": round(flops1 / (cfg1 * 1e-3) / 1e9, 1)}
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(multi-GPU sharding of the pair stack is a design note, not built)"}))
-        sys.exit(2)
-    if args.workload == "token-attention":
-        return token_attention(args)
-    if args.workload == "diffusion":
-        return diffusion(args)
+# ----------------------------------------------------------- the workloads
+
+
+def pairformer(args):
     import torch
     from boltz_lumi_amd import layers, ops
 
     dev = torch.device("cuda:0")
-    n = args.n
+    n = args.n or 1024
+    steps = args.steps or 10
     if args.calibrate_copy:
         src = torch.ones(1 << 28, device=dev)  # 1 GiB of fp32
         dst = torch.empty_like(src)
@@ -425,91 +299,556 @@ def main():
     pair_mask = torch.ones(1, n, n, device=dev)
     ws = ops.new_workspace(n, dev)
     z_out = torch.empty_like(z)
-
-    def step():
-        layer(s, z, mask, pair_mask, z_out=z_out, workspace=ws)
-
     with torch.inference_mode():
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        wall0 = time.perf_counter()
-        e0.record()
-        for _ in range(args.steps):
-            step()
-        e1.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - wall0
-        ms = e0.elapsed_time(e1) / args.steps
-        kt = per_kernel_times(layer, s, z, mask, pair_mask, z_out, ws, args.kernel_reps)
-
+        ms, wall = timed_loop(lambda: layer(s, z, mask, pair_mask, z_out=z_out, workspace=ws), steps, args.warmup)
+        kt, modules_ms = per_kernel_times(layer, s, z, mask, pair_mask, z_out, ws, args.kernel_reps)
     table = kernel_table(n)
     breakdown = {}
     for name, (avg_ms, launches) in kt.items():
         entry = {"ms": round(avg_ms, 4), "launches_per_layer": launches}
         if name in table:
-            flops, nbytes, bound = table[name]
-            entry["tflops"] = round(flops / (avg_ms * 1e-3) / 1e12, 2)
-            entry["gbs"] = round(nbytes / (avg_ms * 1e-3) / 1e9, 1)
-            entry["bound"] = bound
-            entry["frac"] = round(entry["tflops"] / PEAK_BF16_TFLOPS if bound == "mfma"
-                                  else entry["gbs"] / PEAK_HBM_GBS, 4)
+            flops, nbytes = table[name]
+            entry.update(roofline_of(flops, nbytes, avg_ms))
         breakdown[name] = entry
     dominant = max((k for k in breakdown if k in table),
                    key=lambda k: breakdown[k]["ms"] * breakdown[k]["launches_per_layer"])
     d = breakdown[dominant]
-    roofline = {
-        "kernel": dominant,
-        "bound": d["bound"],
-        "achieved": d["tflops"] if d["bound"] == "mfma" else d["gbs"],
-        "peak": PEAK_BF16_TFLOPS if d["bound"] == "mfma" else PEAK_HBM_GBS,
-        "unit": "TFLOP/s" if d["bound"] == "mfma" else "GB/s",
-        "frac": d["frac"],
-        "traffic": measured_traffic(dominant, n),
-    }
+    roofline = {"kernel": dominant, **{k: d[k] for k in ("bound", "achieved", "peak", "unit", "frac")},
+                "traffic": measured_traffic(dominant, n), "kernel_ms": d["ms"]}
     if dominant == "triattn_core":
-        # Exp co-bound (H N^3 exponentials per direction): v_exp_f32 issues one
-        # wave instruction per 8 cycles per SIMD (measured on the box), and MFMA
-        # and VALU issue overlap little, so the core's issue floor is the sum.
-        exps = 4.0 * n ** 3
-        exp_ms = exps / (EXP_PER_SIMD_CYCLE * SIMDS * CLOCK_HZ) * 1e3
-        mfma_ms = table[dominant][0] / (PEAK_BF16_TFLOPS * 1e12) * 1e3
-        roofline["co_bound"] = {"exp_ms": round(exp_ms, 4), "mfma_ms": round(mfma_ms, 4),
-                                "issue_floor_ms": round(exp_ms + mfma_ms, 4),
-                                "issue_floor_frac": round((exp_ms + mfma_ms) / d["ms"], 4)}
-    out = {
-        "metric": "Pairformer layer ms @N=1024 bf16",
-        "value": round(ms, 4),
-        "unit": "ms",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (z, s ~ N(0,1); masks ones; random-init weights seed 0)",
-        "config": {"workload": f"PairformerLayer forward, N={n}, c_z=128, c_s=384, tri-att 4x32, "
-                               f"tri-mult 128, transition x4, single attention 16 heads (BASELINE configs[3], "
-                               f"one of 64 blocks)", "n_tokens": n, "batch": 1},
-        "wall_s": round(wall, 3),
-        "roofline": roofline,
-        "breakdown": breakdown,
-    }
+        roofline["co_bound"] = exp_co_bound(n, d["ms"])
+    modules = {}
+    for name, mod_ms in modules_ms.items():
+        f, b = tri_module_cost("triattn" if name.startswith("triattn") else "trimul", n)
+        ts = t_star_ms(f, b)
+        modules[name] = {"ms": round(mod_ms, 4), "t_star_ms": round(ts, 4), "frac": round(ts / mod_ms, 4)}
+    layer_f = 2.831e12 * (n / 1024) ** 3  # BASELINE.md section 2, configs[3] (dominated by the N^3 terms)
+    modules["layer"] = {"ms": round(ms, 4), "t_star_ms": round(t_star_ms(layer_f, 0), 4),
+                        "frac": round(t_star_ms(layer_f, 0) / ms, 4)}
+    out = line("Pairformer layer ms @N=1024 bf16", ms, "ms", args, steps, "bf16",
+               "synthetic (z, s ~ N(0,1); masks ones; random-init weights seed 0)",
+               {"workload": f"PairformerLayer forward, N={n}, c_z=128, c_s=384, tri-att 4x32, tri-mult 128, "
+                            f"transition x4, single attention 16 heads (BASELINE configs[3], one of 64 blocks)",
+                "n_tokens": n, "batch": 1},
+               wall_s=round(wall, 3), roofline=roofline, modules=modules, breakdown=breakdown)
     if not args.no_cpu_baseline:
-        cpu_n = args.cpu_n or n
-        cpu_ms, cores = cpu_baseline(cpu_n, 0)
-        out["cpu_baseline"] = {
-            "value": round(cpu_ms, 1),
-            "unit": "ms per layer",
-            "cores": cores,
-            "kind": "port",
-            "sample": f"one PairformerLayer forward at N={cpu_n}, fp32 CPU oracle (oracle/boltz_ref.py), "
-                      f"tri-attention chunked 64 rows, {cores} threads",
-        }
+        out["cpu_baseline"] = cpu_pairformer(n)
     print(json.dumps(out), flush=True)
+
+
+def per_kernel_times(layer, s, z, mask, pair_mask, z_out, ws, reps):
+    """Average ms per launch of every kernel of the layer (each stage launched
+    on its own) and per module (stages 1|2|4 in one call), from HIP events on
+    torch's current stream (the stream the kernels launch on)."""
+    import torch
+    from boltz_lumi_amd import ops
+
+    zi, zo, mb = z[0], z_out[0], pair_mask[0].float().contiguous()
+    plan = []
+    modules = []
+    for mod, outgoing, first, mname in ((layer.tri_mul_out, True, True, "trimul_out"),
+                                        (layer.tri_mul_in, False, False, "trimul_in")):
+        mode = ops.OUT_RESIDUAL if first else ops.OUT_ACCUMULATE
+        src = zi if first else zo
+        for stage, name in ((1, "trimul_proj"), (2, "trimul_contract"), (4, "trimul_out")):
+            plan.append((name, lambda m=mod, o=outgoing, md=mode, x=src, st=stage:
+                         ops.trimul(m, x, mb, o, md, zo, ws, stages=st)))
+        modules.append((mname, lambda m=mod, o=outgoing, md=mode, x=src: ops.trimul(m, x, mb, o, md, zo, ws)))
+    for mod, starting, mname in ((layer.tri_att_start, True, "triattn_start"),
+                                 (layer.tri_att_end, False, "triattn_end")):
+        for stage, name in ((1, "triattn_proj"), (2, "triattn_core"), (4, "triattn_out")):
+            plan.append((name, lambda m=mod, st_=starting, st=stage:
+                         ops.triattn(m, zo, mb, st_, ops.OUT_ACCUMULATE, zo, ws, stages=st)))
+        modules.append((mname, lambda m=mod, st_=starting: ops.triattn(m, zo, mb, st_, ops.OUT_ACCUMULATE, zo, ws)))
+    # the transition's epilogue also writes the sequence stack's pair bias, as in PairformerLayer.forward
+    bias = torch.empty((1, 16) + zo.shape[:2], device=zo.device)
+    pb = (layer.attention.proj_z[0], layer.attention.proj_z[1], bias[0])
+    plan.append(("pair_transition", lambda: ops.pair_transition(layer.transition_z, zo, ops.OUT_ACCUMULATE, zo,
+                                                                pair_bias=pb)))
+    plan.append(("sequence_stack", lambda: layer.sequence_stack(s, z_out, mask, pair_bias=bias)))
+    timer = event_timer()
+    for _ in range(reps):
+        for name, fn in plan:
+            timer.run(name, fn)
+        for name, fn in modules:
+            timer.run("module:" + name, fn)
+    avg, cnt = timer.averages()
+    kernels = {k: (v, cnt[k] // reps) for k, v in avg.items() if not k.startswith("module:")}
+    mods = {k[len("module:"):]: v for k, v in avg.items() if k.startswith("module:")}
+    return kernels, mods
+
+
+def trunk(args):
+    """configs[3] in full: the 64-block PairformerModule at N=1024, layer l's
+    weights from seed l; ping-pong pair buffers and one workspace."""
+    import torch
+    from boltz_lumi_amd import layers
+
+    dev = torch.device("cuda:0")
+    n = args.n or 1024
+    steps = args.steps or 3
+    module = layers.PairformerModule(num_blocks=64)
+    for idx, layer in enumerate(module.layers):
+        init_weights(layer, idx)
+    module = module.to(dev).eval()
+    g = torch.Generator().manual_seed(0)
+    z = torch.randn(1, n, n, 128, generator=g).to(dev)
+    s = torch.randn(1, n, 384, generator=g).to(dev)
+    mask = torch.ones(1, n, device=dev)
+    pair_mask = torch.ones(1, n, n, device=dev)
+    with torch.inference_mode():
+        ms, wall = timed_loop(lambda: module(s, z, mask, pair_mask), steps, min(args.warmup, 1))
+        s_out, z_out = module(s, z, mask, pair_mask)
+        finite = bool(torch.isfinite(z_out).all()) and bool(torch.isfinite(s_out).all())
+    layer_f = 2.831e12 * (n / 1024) ** 3
+    ts = 64 * t_star_ms(layer_f, 0)
+    out = line("Pairformer trunk (64 blocks) ms @N=1024 bf16", ms, "ms", args, steps, "bf16",
+               "synthetic (z, s ~ N(0,1); masks ones; random-init weights, layer l from seed l)",
+               {"workload": f"PairformerModule, 64 PairformerLayers, N={n} (BASELINE configs[3] in full)",
+                "n_tokens": n, "blocks": 64, "ms_per_layer": round(ms / 64, 4), "outputs_finite": finite},
+               wall_s=round(wall, 3),
+               modules={"trunk": {"ms": round(ms, 3), "t_star_ms": round(ts, 3), "frac": round(ts / ms, 4)}})
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_pairformer(n)
+    print(json.dumps(out), flush=True)
+
+
+def token_mask_config(n, masked_tokens, seed=0):
+    """Token mask with ``masked_tokens`` tokens set to 0: the last ones
+    (``last``) or a random choice (``random``, randperm seed 0)."""
+    import torch
+
+    kind, count = masked_tokens
+    m = torch.ones(n)
+    if kind == "last":
+        m[n - count:] = 0
+    else:
+        m[torch.randperm(n, generator=torch.Generator().manual_seed(seed))[:count]] = 0
+    return m
+
+
+def isolated_module(args, kind):
+    """configs[1] (triattn: N=512, last 51 tokens masked) or configs[2]
+    (trimul: N=768, 38 random tokens (5%) masked): both directions of the
+    module under bf16 autocast on an fp32 z (the upstream bf16-mixed call),
+    through the Boltz-compatible modules."""
+    import torch
+    from boltz_lumi_amd import layers, ops
+
+    dev = torch.device("cuda:0")
+    if kind == "triattn":
+        n = args.n or 512
+        masked = ("last", 51 * n // 512)
+        mods = {"start": layers.TriangleAttention(), "end": layers.TriangleAttentionEndingNode()}
+        core = "triattn_core"
+    else:
+        n = args.n or 768
+        masked = ("random", round(0.05 * n))
+        mods = {"out": layers.TriangleMultiplicationOutgoing(), "in": layers.TriangleMultiplicationIncoming()}
+        core = "trimul_contract"
+    steps = args.steps or 20
+    for i, m in enumerate(mods.values()):
+        init_weights(m, i)
+    mods = {k: m.to(dev).eval() for k, m in mods.items()}
+    g = torch.Generator().manual_seed(0)
+    z = torch.randn(1, n, n, 128, generator=g)
+    tok = token_mask_config(n, masked)
+    pm = (tok[:, None] * tok[None, :])[None]
+    zd, pmd = z.to(dev), pm.to(dev)
+    ws = ops.new_workspace(n, dev)
+    times, kernel_ms = {}, {}
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        for name, m in mods.items():
+            fn = (lambda m=m: m(zd, pmd, workspace=ws)) if kind == "trimul" else \
+                (lambda m=m: m(zd, pmd, workspace=ws))
+            times[name], _ = timed_loop(fn, steps, args.warmup)
+            # the dominant kernel alone (stage 2), after a full call filled the workspace
+            x = zd[0].contiguous()
+            mb = pmd[0].contiguous()
+            if kind == "trimul":
+                kfn = lambda m=m, nm=name: ops.trimul(m, x, mb, nm == "out", ops.OUT_BF16, None, ws, stages=2)
+            else:
+                kfn = lambda m=m, nm=name: ops.triattn(m, x, mb, nm == "start", ops.OUT_BF16, None, ws, stages=2)
+            kfn()
+            kernel_ms[name], _ = timed_loop(kfn, steps, 1)
+    f, b = tri_module_cost(kind, n)
+    ts = t_star_ms(f, b)
+    modules = {f"{kind}_{k}": {"ms": round(v, 4), "t_star_ms": round(ts, 4), "frac": round(ts / v, 4)}
+               for k, v in times.items()}
+    kf, kb = kernel_table(n)[core]
+    kms = statistics.mean(kernel_ms.values())
+    roofline = {"kernel": core, **roofline_of(kf, kb, kms), "traffic": measured_traffic(core, n),
+                "kernel_ms": round(kms, 4), "kernel_ms_per_direction": {k: round(v, 4) for k, v in kernel_ms.items()}}
+    if kind == "triattn":
+        roofline["co_bound"] = exp_co_bound(n, kms)
+    value = statistics.mean(times.values())
+    title = {"triattn": "TriangleAttention (start, end) ms per direction @N=512, 10% padded, bf16",
+             "trimul": "TriangleMultiplication (out, in) ms per direction @N=768, 5% masked, bf16"}[kind]
+    desc = {"triattn": f"isolated TriangleAttention starting and ending node, N={n}, 4 heads x 32, last "
+                       f"{masked[1]} tokens masked (BASELINE configs[1])",
+            "trimul": f"isolated TriangleMultiplication outgoing and incoming, N={n}, {masked[1]} random tokens "
+                      f"masked (BASELINE configs[2])"}[kind]
+    out = line(title, value, "ms", args, steps, "bf16",
+               "synthetic (z ~ N(0,1); random-init weights; token mask as stated)",
+               {"workload": desc, "n_tokens": n, "masked_tokens": masked[1]},
+               roofline=roofline, modules=modules)
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_isolated(kind, n, masked)
+    print(json.dumps(out), flush=True)
+
+
+def cpu_isolated(kind, n, masked):
+    """the fp32 oracle module per
+    direction, one warm-up at a quarter of N, median of 3."""
+    import torch
+
+    cores = _cpu_setup()
+    from oracle import boltz_ref as R
+
+    if kind == "triattn":
+        mods = {"start": R.TriangleAttention(128, 32, 4), "end": R.TriangleAttentionEndingNode(128, 32, 4)}
+    else:
+        mods = {"out": R.TriangleMultiplicationOutgoing(128), "in": R.TriangleMultiplicationIncoming(128)}
+    for i, m in enumerate(mods.values()):
+        init_weights(m, i)
+    g = torch.Generator().manual_seed(0)
+    z = torch.randn(1, n, n, 128, generator=g)
+    tok = token_mask_config(n, masked)
+    pm = (tok[:, None] * tok[None, :])[None]
+    small = n // 4
+    per = {}
+    with torch.inference_mode():
+        for name, m in mods.items():
+            kw = {"chunk_size": 64} if kind == "triattn" else {}
+            per[name], _ = _median_ms(lambda m=m: m(z, pm, **kw), 3,
+                                      warm=lambda m=m: m(z[:, :small, :small], pm[:, :small, :small], **kw))
+    f, _ = tri_module_cost(kind, n)
+    value = statistics.mean(per.values())
+    return {"value": round(value, 1), "unit": "ms per direction", "cores": cores, "kind": "port",
+            "sample": f"fp32 CPU oracle (oracle/boltz_ref.py) {kind} at N={n} with the same mask, each direction "
+                      f"median of 3 after a warm-up at N={small}, {cores} threads",
+            "per_direction_ms": {k: round(v, 1) for k, v in per.items()},
+            "gflops": round(f / (value * 1e-3) / 1e9, 1)}
+
+
+def diffusion_step(args):
+    """``--steps`` (default 20) consecutive denoiser steps of the
+    score model's transformer stacks (oracle.boltz_ref.DiffusionStacks at
+    their Boltz module paths, the native forwards installed by
+    ``install``): atom encoder and decoder (3 blocks each, 4 heads, 128
+    channels, windows of 32 queries over 128 keys, 5 x 8192 atoms) and the
+    token transformer (24 blocks, 16 heads x 48, 5 x 1024 tokens, one
+    prepacked bias shared by the samples), fp32 with autocast off as the
+    reference runs the score model (diffusion.py:37-49).  Each step feeds
+    the coordinate update back into the coordinates."""
+    import torch
+    from torch import nn
+    from boltz_lumi_amd import adapters, ops
+    from boltz_lumi_amd.pair_bias import prepare_token_bias
+
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    from oracle import boltz_ref as R  # the stacks' module structure (upstream Boltz classes, restated)
+
+    dev = torch.device("cuda:0")
+    samples, tokens, atoms, w, h = 5, args.n or 1024, 8192, 32, 128
+    nw = atoms // w
+    steps = args.steps or 20
+    host = nn.Module()
+    host.structure_module = nn.Module()
+    host.structure_module.score_model = fan_in_weights(R.DiffusionStacks(), 0).to(dev).eval()
+    stacks = host.structure_module.score_model
+    patched = adapters.install(host, require_boltz2=False)
+    g = torch.Generator().manual_seed(0)
+    t = dict(r=torch.randn(samples, atoms, 3, generator=g) * 160.0, q=torch.randn(samples, atoms, 128, generator=g),
+             c=torch.randn(samples, atoms, 128, generator=g), atom_mask=torch.ones(samples, atoms),
+             enc_bias=torch.randn(1, nw, w, h, 12, generator=g), dec_bias=torch.randn(1, nw, w, h, 12, generator=g),
+             a=torch.randn(samples, tokens, 768, generator=g), s=torch.randn(samples, tokens, 768, generator=g),
+             token_bias=torch.randn(1, tokens, tokens, 24 * 16, generator=g), token_mask=torch.ones(samples, tokens))
+    t = {k: v.to(dev) for k, v in t.items()}
+    index = R.get_indexing_matrix(nw, w, h, device=dev)
+    packed = prepare_token_bias(t["token_bias"])
+
+    def to_keys(x):
+        return R.single_to_keys(x, index, w, h)
+
+    state = {"r": t["r"]}
+
+    def step():
+        upd, _, _ = stacks(state["r"], t["q"], t["c"], t["atom_mask"], t["enc_bias"], t["dec_bias"], to_keys, t["a"],
+                           t["s"], packed, t["token_mask"], multiplicity=samples)
+        state["r"] = state["r"] + 0.1 * upd
+
+    with torch.inference_mode():
+        ms, wall = timed_loop(step, steps, args.warmup)
+        # per-stack times and the fused kernels of one step, by HIP events
+        timer = event_timer()
+        enc, dec = stacks.atom_attention_encoder.atom_encoder, stacks.atom_attention_decoder.atom_decoder
+        for _ in range(3):
+            timer.run("atom_encoder", lambda: enc(t["q"], t["c"], t["enc_bias"], to_keys, t["atom_mask"], samples))
+            timer.run("token_transformer", lambda: stacks.token_transformer(t["a"], t["s"], packed, t["token_mask"],
+                                                                            multiplicity=samples))
+            timer.run("atom_decoder", lambda: dec(t["q"], t["c"], t["dec_bias"], to_keys, t["atom_mask"], samples))
+        block_ms, _ = timer.averages()
+        kernels = diffusion_kernel_times(stacks, t, packed, samples, tokens)
+    dominant = max(kernels, key=lambda k: kernels[k]["ms"] * kernels[k]["launches_per_step"])
+    d = kernels[dominant]
+    roofline = {"kernel": dominant, **{k: d[k] for k in ("bound", "achieved", "peak", "unit", "frac")},
+                "traffic": None, "kernel_ms": d["ms"]}
+    out = line("diffusion denoiser step ms (configs[4]: 5 samples, 24 token + 3 + 3 atom blocks)", ms, "ms", args,
+               steps, "f32", "synthetic (coords ~ N(0, 160^2), activations / conditioning / biases ~ N(0,1); "
+                              "weights N(0, 1/fan_in))",
+               {"workload": f"score-model transformer stacks, {steps} consecutive steps: atom encoder + token "
+                            f"transformer + atom decoder, {samples} samples, {tokens} tokens x 768 (16 heads), "
+                            f"{atoms} atoms x 128 (4 heads, windows 32 x 128), fp32 as the reference runs them "
+                            f"(BASELINE configs[4])",
+                "samples": samples, "n_tokens": tokens, "n_atoms": atoms, "patched_modules": patched,
+                "ms_for_all_steps": round(ms * steps, 2),
+                "stack_ms": {k: round(v, 4) for k, v in block_ms.items()}},
+               wall_s=round(wall, 3), roofline=roofline, kernels=kernels)
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_diffusion_step(tokens, steps)
+    print(json.dumps(out), flush=True)
+
+
+def diffusion_kernel_times(stacks, t, packed, samples, tokens):
+    """Each fused kernel of one step at the step's shapes, timed alone:
+    the token attention (fp32 MFMA, 16 x 48), the windowed atom attention
+    (4 x 32), AdaLN and the conditioned-transition epilogues at the token
+    shape; launches per step count every layer."""
+    import torch
+    from boltz_lumi_amd import ops
+
+    dev = t["a"].device
+    g = torch.Generator().manual_seed(1)
+    out = {}
+
+    def rate(name, fn, flops, nbytes, launches, peak=PEAK_FP32_TFLOPS):
+        ms, _ = timed_loop(fn, 10, 2)
+        out[name] = {"ms": round(ms, 4), "launches_per_step": launches, **roofline_of(flops, nbytes, ms, peak)}
+
+    m, d = samples * tokens, 768
+    q = torch.randn(samples, tokens, 4 * d, generator=g).to(dev)
+    qq, kk, vv, gg = q.split(d, dim=-1)
+    bias = packed[..., :16].movedim(-1, 1)
+    mask = torch.ones(samples, tokens, device=dev)
+    rate("seq_attention (token, 16 x 48)",
+         lambda: ops.seq_attention_batched(qq, kk, vv, bias, mask, gg, 1e6, bias_div=samples),
+         4.0 * 16 * 48 * tokens * tokens * samples, samples * tokens * d * 16 + 16 * tokens * tokens * 4, 24)
+    nw = 8192 // 32
+    aq = torch.randn(samples * nw, 32, 2 * 128, generator=g).to(dev)
+    ak = torch.randn(samples * nw, 128, 2 * 128, generator=g).to(dev)
+    ab = torch.randn(samples * nw, 4, 32, 128, generator=g).to(dev)
+    am = torch.ones(samples * nw, 128, device=dev)
+    rate("seq_attention (atom windows, 4 x 32)",
+         lambda: ops.seq_attention_batched(aq[..., :128], ak[..., :128], ak[..., 128:], ab, am, aq[..., 128:], 1e6),
+         4.0 * 4 * 32 * 32 * 128 * samples * nw, samples * nw * (32 * 512 + 128 * 1024 + 4 * 32 * 128 * 4), 6)
+    x = [torch.randn(m, d, generator=g).to(dev) for _ in range(3)]
+    rate("adaln (token)", lambda: ops.adaln_modulate(x[0], x[1], x[2], 1e-5), 0, 16 * m * d, 48, PEAK_BF16_TFLOPS)
+    u = torch.randn(m, 4 * d, generator=g).to(dev)
+    b = torch.randn(m, 2 * d, generator=g).to(dev)
+    rate("gated_swiglu (token)", lambda: ops.epilogue(u, b, None, ops.GATED_SWIGLU), 0, 16 * m * 2 * d, 24,
+         PEAK_BF16_TFLOPS)
+    rate("gate (token)", lambda: ops.epilogue(x[0], x[1], None, ops.GATE), 0, 12 * m * d, 24, PEAK_BF16_TFLOPS)
+    return out
+
+
+def cpu_diffusion_step(tokens, steps):
+    """one denoiser step of the fp32
+    oracle stacks for one of the 5 samples (x5), reported x``steps`` as
+    extrapolated."""
+    import torch
+
+    cores = _cpu_setup()
+    from oracle import boltz_ref as R
+
+    atoms, w, h = 8192, 32, 128
+    nw = atoms // w
+    stacks = fan_in_weights(R.DiffusionStacks(), 0).eval()
+    g = torch.Generator().manual_seed(0)
+    index = R.get_indexing_matrix(nw, w, h)
+    args = (torch.randn(1, atoms, 3, generator=g) * 160.0, torch.randn(1, atoms, 128, generator=g),
+            torch.randn(1, atoms, 128, generator=g), torch.ones(1, atoms), torch.randn(1, nw, w, h, 12, generator=g),
+            torch.randn(1, nw, w, h, 12, generator=g), lambda x: R.single_to_keys(x, index, w, h),
+            torch.randn(1, tokens, 768, generator=g), torch.randn(1, tokens, 768, generator=g),
+            torch.randn(1, tokens, tokens, 384, generator=g), torch.ones(1, tokens))
+    with torch.inference_mode():
+        one, _ = _median_ms(lambda: stacks(*args), 1)
+    step_ms = 5 * one
+    return {"value": round(step_ms, 1), "unit": "ms per step, 5 samples (1 sample timed, x5)", "cores": cores,
+            "kind": "port",
+            "sample": f"fp32 CPU oracle (oracle/boltz_ref.py DiffusionStacks) one step for one sample at {tokens} "
+                      f"tokens / {atoms} atoms, x5 samples, {cores} threads",
+            f"{steps}_steps_ms_extrapolated": round(steps * step_ms, 1)}
+
+
+# ------------------------------------------ single-module diffusion lines
+
+
+def token_attention(args):
+    """One token-transformer AttentionPairBias forward (c_s 768, 16 heads x 48)
+    over 5 samples of N tokens sharing one prepacked [1, N, N, 24 * 16] bias
+    (BASELINE configs[4] shape, one of the 24 layers), through the drop-in
+    ``prepared_forward``.  The roofline covers the fused attention kernel: fp32
+    MFMA flops 4 * 16 * 48 * N^2 per sample."""
+    import torch
+    from boltz_lumi_amd import layers, ops
+    from boltz_lumi_amd.pair_bias import prepare_token_bias, prepared_forward
+
+    dev = torch.device("cuda:0")
+    n, samples, heads, width = args.n or 1024, 5, 16, 768
+    steps = args.steps or 10
+    module = init_weights(layers.AttentionPairBias(width, num_heads=heads, compute_pair_bias=False), 0).to(dev).eval()
+    g = torch.Generator().manual_seed(0)
+    s = torch.randn(samples, n, width, generator=g).to(dev)
+    bias = prepare_token_bias(torch.randn(1, n, n, 24 * heads, generator=g).to(dev))[..., :heads]
+    mask = torch.ones(samples, n, device=dev)
+    with torch.inference_mode():
+        ms, _ = timed_loop(lambda: prepared_forward(module, s, bias, mask, s, multiplicity=samples), steps,
+                           args.warmup)
+        proj = torch.randn(n, 4 * width, generator=g).to(dev)
+        q, k, v, gl = proj.split(width, dim=-1)
+        b0, m0 = bias[0].movedim(-1, 0), mask[0]
+        out = torch.empty(n, width, device=dev)
+        kms, _ = timed_loop(lambda: ops.seq_attention(q, k, v, b0, m0, gl, module.inf, out=out),
+                            max(steps, 10) * samples, 1)
+    flops = 4.0 * heads * 48 * n * n
+    out_line = line("token-transformer AttentionPairBias ms @N=1024, 5 samples", ms, "ms", args, steps, "f32",
+                    "synthetic (s ~ N(0,1), bias ~ N(0,1) prepacked, masks ones; weights seed 0)",
+                    {"workload": f"diffusion token-transformer AttentionPairBias forward (prepared_forward), "
+                                 f"c_s=768, 16 heads x 48, {samples} samples x N={n} (BASELINE configs[4] shape)",
+                     "n_tokens": n, "samples": samples},
+                    roofline={"kernel": "seq_attention", **roofline_of(flops, n * n * heads * 4, kms,
+                                                                       PEAK_FP32_TFLOPS),
+                              "traffic": None, "kernel_ms_per_sample": round(kms, 4)})
+    if not args.no_cpu_baseline:
+        out_line["cpu_baseline"] = token_attention_cpu(n)
+    print(json.dumps(out_line), flush=True)
+
+
+def token_attention_cpu(n: int):
+    import torch
+
+    cores = _cpu_setup()
+    from oracle import boltz_ref as R  # the checker, timed as the reference CPU path
+
+    module = init_weights(R.AttentionPairBias(768, num_heads=16, compute_pair_bias=False), 0).eval()
+    g = torch.Generator().manual_seed(0)
+    s = torch.randn(1, n, 768, generator=g)
+    bias = torch.randn(1, n, n, 16, generator=g)
+    mask = torch.ones(1, n)
+    with torch.inference_mode():
+        one, _ = _median_ms(lambda: module(s, bias, mask, s), 3, warm=lambda: module(s[:, :32], bias[:, :32, :32],
+                                                                                        mask[:, :32], s[:, :32]))
+    return {"value": round(one * 5, 1), "unit": "ms per 5-sample forward (1 sample timed, x5)", "cores": cores,
+            "kind": "port",
+            "sample": f"one sample of the fp32 CPU oracle AttentionPairBias at N={n} (oracle/boltz_ref.py), "
+                      f"median of 3, {cores} threads, scaled x5"}
+
+
+def diffusion(args):
+    """One token-transformer layer and one atom-transformer layer of the
+    score model (AdaLN, AttentionPairBias through prepared_forward,
+    ConditionedTransitionBlock) at configs[4] shapes, fp32, plus the fused
+    elementwise kernels alone against the 8 TB/s roofline (input sets larger
+    than the 256 MB Infinity Cache).  Bytes per launch: AdaLN 16 M D,
+    GATED_SWIGLU 16 M Di, GATE 12 M D."""
+    import torch
+    from boltz_lumi_amd import layers, ops
+    from boltz_lumi_amd.pair_bias import prepare_token_bias, prepared_forward
+
+    dev = torch.device("cuda:0")
+    samples, n = 5, args.n or 1024
+    steps = args.steps or 10
+    shapes = {"token": (samples * n, 768, 768), "atom": (samples * 8192, 128, 128)}
+    g = torch.Generator().manual_seed(0)
+    kernels, blocks = {}, {}
+    heads = {"token": 16, "atom": 4}
+    modules = {name: (init_weights(layers.AdaLN(d, dc), 0).to(dev).eval(),
+                      init_weights(layers.AttentionPairBias(d, num_heads=heads[name], compute_pair_bias=False), 2)
+                      .to(dev).eval(),
+                      init_weights(layers.ConditionedTransitionBlock(d, dc), 1).to(dev).eval())
+               for name, (m, d, dc) in shapes.items()}
+    with torch.inference_mode():
+        for name, (m, d, dc) in shapes.items():
+            di = 2 * d
+            adaln, apb, ctb = modules[name]
+            a = torch.randn(m, d, generator=g).to(dev)
+            c = torch.randn(m, dc, generator=g).to(dev)
+            if name == "token":  # 5 samples sharing one prepacked layer bias
+                qs = a.view(samples, n, d)
+                ks, mult = qs, samples
+                z = prepare_token_bias(torch.randn(1, n, n, heads[name], generator=g).to(dev))
+                kmask = torch.ones(samples, n, device=dev)
+                index = None
+            else:  # windows of 32 atoms over 128 keys centred on them (clamped at the ends)
+                nw, w, h = 8192 // 32, 32, 128
+                index = torch.stack([torch.clamp(torch.arange(h) + w * i - (h - w) // 2, 0, 8191)
+                                     for i in range(nw)]).to(dev)
+                qs = a.view(samples * nw, w, d)
+                ks, mult = a.view(samples, 8192, d)[:, index].reshape(samples * nw, h, d), 1
+                z = torch.randn(samples * nw, heads[name], w, h, generator=g).to(dev).movedim(1, -1)
+                kmask = torch.ones(samples * nw, h, device=dev)
+            gate = init_weights(torch.nn.Linear(dc, d), 3).to(dev)
+
+            def layer(a=a, c=c, qs=qs, z=z, kmask=kmask, mult=mult, index=index, name=name, d=d):
+                b = adaln(a, c)
+                bq = b.view(qs.shape)
+                k_in = bq if name == "token" else b.view(samples, 8192, d)[:, index].reshape(qs.shape[0], 128, d)
+                o = prepared_forward(apb, bq, z, kmask, k_in, mult).reshape(a.shape)
+                x = a + torch.sigmoid(ops.linear_fp32(c, gate)) * o
+                return x + ctb(x, c)
+
+            blocks[name], _ = timed_loop(layer, steps, args.warmup)
+            blocks[name + "_attention"], _ = timed_loop(lambda: prepared_forward(apb, qs, z, kmask, ks, mult), steps, 1)
+            sets = 1 + (768 << 20) // (16 * m * d)
+            bufs = [{"a": torch.randn(m, d, generator=g).to(dev), "scale": torch.randn(m, d, generator=g).to(dev),
+                     "shift": torch.randn(m, d, generator=g).to(dev), "u": torch.randn(m, 2 * di, generator=g).to(dev),
+                     "b": torch.randn(m, di, generator=g).to(dev), "g": torch.randn(m, d, generator=g).to(dev),
+                     "y": torch.randn(m, d, generator=g).to(dev)} for _ in range(sets)]
+            reps = sets * max(1, max(steps, 10) // sets)
+            turn = [0]
+
+            def nxt():
+                turn[0] = (turn[0] + 1) % sets
+                return bufs[turn[0]]
+
+            for kname, fn, nbytes in (
+                    ("adaln", lambda: (lambda t: ops.adaln_modulate(t["a"], t["scale"], t["shift"], 1e-5))(nxt()),
+                     16 * m * d),
+                    ("gated_swiglu", lambda: (lambda t: ops.epilogue(t["u"], t["b"], None, ops.GATED_SWIGLU))(nxt()),
+                     16 * m * di),
+                    ("gate", lambda: (lambda t: ops.epilogue(t["g"], t["y"], None, ops.GATE))(nxt()), 12 * m * d)):
+                ms, _ = timed_loop(fn, reps, 1)
+                gbs = nbytes / (ms * 1e-3) / 1e9
+                kernels[f"{kname}_{name}"] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(gbs, 1),
+                                              "frac": round(gbs / PEAK_HBM_GBS, 4), "input_sets": sets}
+            del bufs
+    ms = blocks["token"] + blocks["atom"]
+    dom = kernels["gated_swiglu_token"]
+    out_line = line("diffusion score-model modules (AdaLN + AttentionPairBias + ConditionedTransitionBlock) ms per "
+                    "token + atom layer, 5 samples", ms, "ms", args, steps, "f32",
+                    "synthetic (activations and conditioning ~ N(0,1); weights seeds 0 and 1)",
+                    {"workload": f"one token layer ({samples} x {n} x 768, 16 heads, one shared bias) + one atom "
+                                 f"layer ({samples} x 8192 x 128, 4 heads, windows of 32 queries x 128 keys), "
+                                 f"BASELINE configs[4] shapes",
+                     "n_tokens": n, "n_atoms": 8192, "samples": samples,
+                     "block_ms": {k: round(v, 4) for k, v in blocks.items()}},
+                    roofline={"kernel": "gated_swiglu (token)", "bound": "hbm", "achieved": dom["gbs"],
+                              "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": dom["frac"], "traffic": None,
+                              "kernels": kernels})
+    print(json.dumps(out_line), flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding of the pair stack is a design note, not built)"}))
+        sys.exit(2)
+    {"pairformer": pairformer, "trunk": trunk, "trimul": lambda a: isolated_module(a, "trimul"),
+     "triattn": lambda a: isolated_module(a, "triattn"), "diffusion-step": diffusion_step,
+     "token-attention": token_attention, "diffusion": diffusion}[args.workload](args)
 
 
 if __name__ == "__main__":

@@ -67,8 +67,10 @@ def adaln_forward(self, a, s):
 
 
 def transition_forward(self, a, s):
-    """Drop-in for ``ConditionedTransitionBlock.forward(a, s)``."""
-    if not eligible(self, a, s):
+    """Drop-in for ``ConditionedTransitionBlock.forward(a, s)``.  The fused
+    epilogues take widths that are multiples of 4 (every Boltz-2 width is);
+    other widths run the class forward."""
+    if not eligible(self, a, s) or a.shape[-1] % 4 or self.a_to_b.weight.shape[0] % 4:
         return type(self).forward(self, a, s)
     a = self.adaln(a, s)
     b = ops.epilogue(_linear(self.swish_gate[0], a), _linear(self.a_to_b, a), None, ops.GATED_SWIGLU)

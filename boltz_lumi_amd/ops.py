@@ -17,6 +17,8 @@ raises.
 
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _native as N
@@ -245,12 +247,27 @@ def mm_x3(x, w3):
 # transformer's 768 / 1536) the split form is ~1.5x faster per block.
 X3_MIN_K = 512
 
+# Set BMX_EXACT_FP32_LINEARS=1 (or call exact_fp32_linears(True)) to run every
+# fp32 linear of the diffusion blocks as a true fp32 GEMM, as the reference
+# does, instead of the split-bf16 form (about 2^-16 relative per product).
+_EXACT_FP32 = [os.environ.get("BMX_EXACT_FP32_LINEARS", "0") not in ("", "0")]
+
+
+def exact_fp32_linears(enabled: bool = True) -> bool:
+    """Switch ``linear_fp32`` between the split-bf16 GEMM (False, default) and
+    the plain fp32 GEMM (True) for the whole process; returns the previous
+    setting."""
+    before = _EXACT_FP32[0]
+    _EXACT_FP32[0] = bool(enabled)
+    return before
+
 
 def linear_fp32(x, linear):
     """``linear(x)`` for fp32 x: ``linear_x3`` for input widths >= X3_MIN_K
-    (multiples of 4), else the fp32 GEMM."""
+    (multiples of 4) unless exact fp32 linears are switched on, else the fp32
+    GEMM."""
     k = x.shape[-1]
-    if k >= X3_MIN_K and k % 4 == 0:
+    if not _EXACT_FP32[0] and k >= X3_MIN_K and k % 4 == 0:
         return linear_x3(x, linear)
     return torch.nn.functional.linear(x, linear.weight, linear.bias)
 

@@ -559,3 +559,123 @@ def randomize(module: nn.Module, std: float = 0.08, generator=None):
             mean = 1.0 if "norm" in name and name.endswith("weight") else 0.0
             p.copy_(torch.randn(p.shape, generator=generator) * std + mean)
     return module
+
+
+# --------------------------------------------------------------------------
+# Diffusion transformer stacks
+# --------------------------------------------------------------------------
+
+
+class DiffusionTransformer(nn.Module):
+    """Upstream ``transformersv2.DiffusionTransformer``: ``depth``
+    DiffusionTransformerLayers; the pair bias ``[B, N, M, depth * heads]`` is
+    split into per-layer ``[B, N, M, heads]`` slices, layer ``i`` taking
+    channels ``i * heads .. (i + 1) * heads - 1`` (the layout
+    ``prepare_token_bias`` packs densely, reference ``pair_bias.py:6-13``)."""
+
+    def __init__(self, depth, heads, dim=384, dim_single_cond=None):
+        super().__init__()
+        self.heads = heads
+        self.layers = nn.ModuleList([DiffusionTransformerLayer(heads, dim, dim_single_cond) for _ in range(depth)])
+
+    def forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity=1):
+        b, n, m, d = bias.shape
+        bias = bias.view(b, n, m, len(self.layers), d // len(self.layers))
+        for i, layer in enumerate(self.layers):
+            a = layer(a, s, bias[:, :, :, i], mask, to_keys, multiplicity)
+        return a
+
+
+def get_indexing_matrix(k_windows, w, h, device=None):
+    """Upstream ``encodersv2.get_indexing_matrix``: the one-hot [2K, (H / (W/2)) K]
+    map from half-windows of W/2 atoms to the key windows of H atoms, key
+    window k covering half-windows 2k - h/2 + 1 .. 2k + h/2 (h = H / (W/2)),
+    with half-windows outside the sequence left out (zero keys)."""
+    assert w % 2 == 0 and h % (w // 2) == 0
+    hh = h // (w // 2)
+    assert hh % 2 == 0
+    ar = torch.arange(2 * k_windows, device=device)
+    index = ((ar.unsqueeze(0) - ar.unsqueeze(1)) + hh // 2).clamp(min=0, max=hh + 1)
+    index = index.view(k_windows, 2, 2 * k_windows)[:, 0, :]
+    onehot = F.one_hot(index, num_classes=hh + 2)[..., 1:-1].transpose(1, 0)
+    return onehot.reshape(2 * k_windows, hh * k_windows).float()
+
+
+def single_to_keys(single, indexing_matrix, w, h):
+    """Upstream ``encodersv2.single_to_keys``: [B, N, D] atom rows to
+    [B, N / W, H, D] key windows through the indexing matrix."""
+    b, n, d = single.shape
+    k_windows = n // w
+    single = single.view(b, 2 * k_windows, w // 2, d)
+    return torch.einsum("bjid,jk->bkid", single, indexing_matrix.to(single.dtype)).reshape(b, k_windows, h, d)
+
+
+class AtomTransformer(nn.Module):
+    """Upstream ``transformersv2.AtomTransformer`` (windowed, eval): atoms in
+    windows of ``attn_window_queries`` (32) attend to the ``attn_window_keys``
+    (128) atoms ``to_keys`` gathers around them.  The per-window pair bias
+    ``[B, N / W, W, H, depth * heads]`` is repeated per sample
+    (``multiplicity``) and the stack runs with multiplicity 1 on
+    ``[B * mult * N / W, W, D]``.  The reference walks these layers at
+    ``atom_conditioning.py:27-35``."""
+
+    def __init__(self, attn_window_queries=32, attn_window_keys=128, depth=3, heads=4, dim=128,
+                 dim_single_cond=None):
+        super().__init__()
+        self.attn_window_queries = attn_window_queries
+        self.attn_window_keys = attn_window_keys
+        self.diffusion_transformer = DiffusionTransformer(depth, heads, dim, dim_single_cond)
+
+    def forward(self, q, c, bias, to_keys, mask, multiplicity=1):
+        w, h = self.attn_window_queries, self.attn_window_keys
+        b, n, d = q.shape
+        nw = n // w
+        q = q.view(b * nw, w, -1)
+        c = c.view(b * nw, w, -1)
+        mask = mask.view(b * nw, w)
+        bias = bias.repeat_interleave(multiplicity, 0)
+        bias = bias.view(bias.shape[0] * nw, w, h, -1)
+
+        def window_keys(x):
+            return to_keys(x.view(b, nw * w, -1)).view(b * nw, h, -1)
+
+        q = self.diffusion_transformer(a=q, s=c, bias=bias, mask=mask.float(), multiplicity=1, to_keys=window_keys)
+        return q.view(b, nw * w, d)
+
+
+class DiffusionStacks(nn.Module):
+    """The three transformer stacks of Boltz-2's score model at their module
+    paths (``atom_attention_encoder.atom_encoder``, ``token_transformer``,
+    ``atom_attention_decoder.atom_decoder``: atom
+    encoder / decoder 3 blocks x 4 heads at 128 channels with 32 / 128
+    windows, token transformer 24 blocks x 16 heads at 768).  One denoiser
+    step here embeds the noisy coordinates r (EDM input scaling
+    1 / sqrt(sigma^2 + sigma_data^2), sigma_data 16, then a 3 -> 128 linear
+    added to the atom queries), runs the atom encoder on the atom queries,
+    the token transformer on the token activations and the atom decoder on
+    the encoder's output, and maps the decoder's atoms to a coordinate
+    update (LayerNorm + 128 -> 3 linear).  Those two small linears stand in
+    for upstream's coordinate embedding and update head; the atom <-> token
+    aggregation linears between the stacks are outside the hot path and
+    left out."""
+
+    def __init__(self, token_depth=24, token_heads=16, token_dim=768, atom_depth=3, atom_heads=4, atom_dim=128,
+                 window_queries=32, window_keys=128):
+        super().__init__()
+        self.atom_attention_encoder = nn.Module()
+        self.atom_attention_encoder.atom_encoder = AtomTransformer(window_queries, window_keys, atom_depth,
+                                                                   atom_heads, atom_dim, atom_dim)
+        self.token_transformer = DiffusionTransformer(token_depth, token_heads, token_dim, token_dim)
+        self.atom_attention_decoder = nn.Module()
+        self.atom_attention_decoder.atom_decoder = AtomTransformer(window_queries, window_keys, atom_depth,
+                                                                   atom_heads, atom_dim, atom_dim)
+        self.r_to_q = nn.Linear(3, atom_dim, bias=False)
+        self.pos_update = nn.Sequential(nn.LayerNorm(atom_dim), nn.Linear(atom_dim, 3, bias=False))
+
+    def forward(self, r, q, c, atom_mask, enc_bias, dec_bias, to_keys, a, s, token_bias, token_mask,
+                multiplicity=1, sigma=160.0, sigma_data=16.0):
+        q = q + self.r_to_q(r / math.sqrt(sigma ** 2 + sigma_data ** 2))
+        q = self.atom_attention_encoder.atom_encoder(q, c, enc_bias, to_keys, atom_mask, multiplicity)
+        a = self.token_transformer(a, s, token_bias, token_mask, multiplicity=multiplicity)
+        q = self.atom_attention_decoder.atom_decoder(q, c, dec_bias, to_keys, atom_mask, multiplicity)
+        return self.pos_update(q), q, a

@@ -126,3 +126,15 @@ def test_conditioning_cache_computes_once(gpu):
     for gw, ww in zip(got, want):
         for g_, w_ in zip(gw, ww):
             assert torch.equal(g_, w_)
+
+
+def test_diffusion_widths_off_the_kernels_fall_back(gpu):
+    """The fused epilogues take widths that are multiples of 4: a block of
+    another width runs its class forward, bit for bit, instead of raising."""
+    from boltz_lumi_amd.diffusion import adaln_forward, transition_forward
+
+    ctb = R.randomize(R.ConditionedTransitionBlock(6, 8), generator=torch.Generator().manual_seed(3)).to(gpu).eval()
+    a, s = torch.randn(2, 5, 6, device=gpu), torch.randn(2, 5, 8, device=gpu)
+    with torch.inference_mode():
+        assert torch.equal(transition_forward(ctb, a, s), type(ctb).forward(ctb, a, s))
+        assert torch.equal(adaln_forward(ctb.adaln, a, s), type(ctb.adaln).forward(ctb.adaln, a, s))

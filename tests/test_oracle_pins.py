@@ -631,3 +631,83 @@ def test_diffusion_layer_default_gate_init():
     layer = R.DiffusionTransformerLayer(2, 8, 6)
     for lin in (layer.output_projection_linear, layer.transition.output_projection[0]):
         assert not lin.weight.any() and torch.all(lin.bias == -2.0)
+
+
+# ------------------------------------------------ diffusion transformer stacks
+
+
+def _window_keys_by_formula(x, w, h):
+    """Key t of window k is atom W k - (H - W) / 2 + t, zero outside the
+    sequence (upstream's centred windows written out directly)."""
+    b, n, d = x.shape
+    out = torch.zeros(b, n // w, h, d, dtype=x.dtype)
+    for k in range(n // w):
+        for t in range(h):
+            atom = w * k - (h - w) // 2 + t
+            if 0 <= atom < n:
+                out[:, k, t] = x[:, atom]
+    return out
+
+
+@pytest.mark.parametrize("n,w,h", [(128, 32, 128), (96, 8, 32), (64, 16, 64)])
+def test_single_to_keys_is_the_centred_window(n, w, h):
+    x = torch.randn(2, n, 3, generator=_gen(40), dtype=torch.float64)
+    got = R.single_to_keys(x, R.get_indexing_matrix(n // w, w, h), w, h)
+    assert torch.equal(got, _window_keys_by_formula(x, w, h))
+
+
+def test_diffusion_transformer_slices_the_bias_per_layer():
+    """Layer i of the stack sees bias channels i*H .. i*H+H-1, in dense and in
+    head-major (prepacked) storage alike."""
+    torch.manual_seed(41)
+    stack = R.randomize(R.DiffusionTransformer(3, 2, 8, 6), generator=_gen(42)).double()
+    a, s, _, mask = _dtl_inputs(43)
+    bias = torch.randn(2, 5, 5, 6, generator=_gen(44), dtype=torch.float64)
+    packed = bias.permute(0, 3, 1, 2).contiguous().permute(0, 2, 3, 1)  # upstream-layout, head-major storage
+    with torch.no_grad():
+        got = stack(a, s, bias, mask)
+        got_packed = stack(a, s, packed, mask)
+        want = a
+        for i, layer in enumerate(stack.layers):
+            want = layer(want, s, bias[..., 2 * i:2 * i + 2].contiguous(), mask)
+    assert torch.equal(got, want) and torch.equal(got_packed, want)
+
+
+@pytest.mark.parametrize("multiplicity", [1, 2])
+def test_atom_transformer_windows_and_multiplicity(multiplicity):
+    """The windowed stack equals its layers applied window by window, with
+    keys and key mask gathered by the centred-window formula, zero keys
+    masked, and sample j of a structure using that structure's window bias."""
+    w, h, n, heads, depth = 8, 16, 32, 2, 2
+    nw = n // w
+    tr = R.randomize(R.AtomTransformer(w, h, depth, heads, 8, 6), generator=_gen(45)).double()
+    g = _gen(46)
+    batch = 2 * multiplicity  # 2 structures x multiplicity samples
+    q = torch.randn(batch, n, 8, generator=g, dtype=torch.float64)
+    c = torch.randn(batch, n, 6, generator=g, dtype=torch.float64)
+    mask = (torch.rand(batch, n, generator=g) > 0.2).double()
+    bias = torch.randn(2, nw, w, h, depth * heads, generator=g, dtype=torch.float64)
+    index = R.get_indexing_matrix(nw, w, h)
+
+    def to_keys(x):
+        return R.single_to_keys(x, index, w, h)
+
+    with torch.no_grad():
+        got = tr(q, c, bias, to_keys, mask, multiplicity)
+        want = torch.empty_like(q)
+        for bi in range(batch):
+            x, cond = q[bi], c[bi]  # this sample's atoms, all windows
+            kmask = _window_keys_by_formula(mask[bi].view(1, n, 1), w, h)[0, :, :, 0]  # [nw, h]
+            for i, layer in enumerate(tr.diffusion_transformer.layers):
+                ad = layer.adaln(x[None], cond[None])[0]
+                keys = _window_keys_by_formula(ad[None], w, h)[0]  # [nw, h, D]
+                nxt = torch.empty_like(x)
+                for k in range(nw):
+                    rows = slice(w * k, w * (k + 1))
+                    sl = bias[bi // multiplicity, k, :, :, heads * i:heads * (i + 1)][None]
+                    att = layer.pair_bias_attn(s=ad[None, rows], z=sl, mask=kmask[k][None], k_in=keys[k][None])
+                    y = x[None, rows] + layer.output_projection(cond[None, rows]) * att
+                    nxt[rows] = (y + layer.transition(y, cond[None, rows]))[0]
+                x = nxt
+            want[bi] = x
+    assert _rel(got, want) < 1e-12
