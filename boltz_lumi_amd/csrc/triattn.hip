@@ -47,6 +47,10 @@ struct Layout {
   bf16 *q, *k, *vt, *o;
   tb_t* tb;
   float* mb;
+  // Per row i and 64-key tile: the first masked key of the tile (n if none)
+  // and the last open key (-1 if none), keys < n only; written by the
+  // projection, read by the attention core to pick its path per block.
+  int2* keyspan;
 };
 
 __host__ __device__ inline int64_t qkv_elems(int np) { return (int64_t)np * kH * np * kD; }
@@ -171,7 +175,16 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
     if (t < kP1) {
       // mask bias mb[i][j] = log2(e) * inf * (mask'[i][j] - 1); 0 outside n x n
       const int j = j0 + t;
-      L.mb[(int64_t)i * np + j] = (i < n && j < n) ? inf * (mpre - 1.f) * kLog2e : 0.f;
+      const bool valid = i < n && j < n;
+      const float mbv = valid ? inf * (mpre - 1.f) * kLog2e : 0.f;
+      L.mb[(int64_t)i * np + j] = mbv;
+      int fm = valid && mbv != 0.f ? j : n, lo = valid && mbv == 0.f ? j : -1;
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) {
+        fm = min(fm, __shfl_xor(fm, d, kWave));
+        lo = max(lo, __shfl_xor(lo, d, kWave));
+      }
+      if (t == 0) L.keyspan[(int64_t)i * (np / kP1) + j0 / kP1] = make_int2(fm, lo);
     }
     if (prev >= 0) store_stage(prev);
     __syncthreads();  // xt written; the stage has been read
@@ -295,15 +308,24 @@ __device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf
 // end of the pass checks (every row sum in [2^-60, 2^100], every output
 // finite); otherwise nothing is written and false is returned, and the caller
 // redoes the block with per-row tracked maxima.
-template <bool MASKED, bool SPEC>
-__device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0, char* lds) {
+//
+// KEYMASK (speculative pass for key-padded rows): every row of the block has
+// at least one unmasked key and its masked keys form a suffix of the key
+// range (token padding gives exactly this: pair (i, k) is masked for the
+// padded tokens k).  Stages from `mask_k0` on add the rows' mask bias to the
+// C operand as the masked path does, so masked keys contribute exp2 of about
+// -1.4e9, i.e. exactly 0; keys from `kend` on are masked for every row and
+// are skipped.  The result is the masked path's up to the offset.
+template <bool MASKED, bool SPEC, bool KEYMASK = false>
+__device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0, char* lds, int kend, int mask_k0) {
   static_assert(!(MASKED && SPEC), "speculation is for unmasked rows");
+  static_assert(!KEYMASK || SPEC, "key-padded rows use the speculative pass");
   constexpr int G = kRows;
   const int n = L.n, np = L.np;
   // w is wave-uniform: read into an SGPR so that the DMA job set-up and the
   // LDS (M0) addresses below stay scalar.
   const int l = lane_id(), g = l >> 4, lq = l & 15, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nk = (n + kKT - 1) / kKT * kKT;
+  const int nk = kend;  // a multiple of kKT, at most round_up(n, kKT)
   const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
   const bf16* kb[G];
   const bf16* vb[G];
@@ -344,7 +366,7 @@ __device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0
   const bf16* tb_src = L.tb + tb_offset(np, h, q0, 0) + 8 * l;  // + 256 per 16-key block
   const int i_mb = min(i0 + (l >> 4), n - 1);
   const float* mb_src = L.mb + (int64_t)i_mb * np + 4 * lq;
-  auto dma_stage = [&](int buf) {
+  auto dma_stage = [&](int buf, int stage_k0) {
     const unsigned base = lds0 + buf * kStageBytes;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -356,7 +378,8 @@ __device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0
       lds_dma16(tb_src + 16 * 32 * hb,
                 __builtin_amdgcn_readfirstlane(base + kOffBias + w * kBiasWaveBytes + 1024 * hb));
     tb_src += 16 * kKT;
-    if (MASKED && w == 0 && l < 32) lds_dma16(mb_src, __builtin_amdgcn_readfirstlane(base + kOffMb));
+    if ((MASKED || (KEYMASK && stage_k0 >= mask_k0)) && w == 0 && l < 32)
+      lds_dma16(mb_src, __builtin_amdgcn_readfirstlane(base + kOffMb));
     mb_src += kKT;
   };
 
@@ -384,13 +407,13 @@ __device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0
   const int k_rd = kOffK + (4 * lq + (g ^ ((lq >> 2) & 3))) * 16;  // + 1024 j (16 keys) + r tile
   const int b_rd = kOffBias + w * kBiasWaveBytes + 16 * (l & 31);   // + 512 j
 
-  dma_stage(0);
+  dma_stage(0, 0);
   wait_vm0();
   __syncthreads();
   for (int k0 = 0; k0 < nk; k0 += kKT) {
     const int cur = (k0 / kKT) & 1;
     const bool more = k0 + kKT < nk;
-    if (more) dma_stage(cur ^ 1);
+    if (more) dma_stage(cur ^ 1, k0 + kKT);
     const char* sb = lds + cur * kStageBytes;
     // S^T for all rows first, so the scheduler can overlap one row's MFMAs
     // with another row's max / exp work inside one basic block.
@@ -400,12 +423,16 @@ __device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0
     // of their query; groups 2 and 3 read the same bytes, which ident
     // multiplies by zero (the bias is finite).
     if constexpr (SPEC) {
+      const bool mstage = KEYMASK && k0 >= mask_k0;  // wave-uniform
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f32x4 bc = mfma16(ident, *(const bf16x8*)(sb + b_rd + 512 * j), mneg[0]);
 #pragma unroll
-        for (int r = 0; r < G; ++r)
-          s[r][j] = mfma16(*(const bf16x8*)(sb + k_rd + r * kTileBytes + 1024 * j), qf[r], bc);
+        for (int r = 0; r < G; ++r) {
+          f32x4 c = bc;
+          if (mstage) c += *(const f32x4*)(sb + kOffMb + r * kKT * 4 + (16 * j + 4 * g) * 4);
+          s[r][j] = mfma16(*(const bf16x8*)(sb + k_rd + r * kTileBytes + 1024 * j), qf[r], c);
+        }
       }
     }
 #pragma unroll
@@ -525,6 +552,35 @@ __device__ __forceinline__ bool core_rows(const Layout& L, int i0, int h, int q0
   return true;
 }
 
+// Rows with every key masked: the mask bias (-1e9 log2 e) swamps every
+// score, so upstream's softmax is uniform over the n keys and each query's
+// output is the mean of v over them (the masked path gives the same: every
+// score rounds to the mask bias, p = 1).  Keys past n hold v = 0.  Each wave
+// writes its 16 queries; lane (d = l % 32, half = l / 32) sums dim d over
+// half of the keys.
+__device__ __forceinline__ void uniform_rows(const Layout& L, int i0, int h, int q0) {
+  const int n = L.n, np = L.np, l = lane_id(), d = l & 31, half = l >> 5;
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const int i = i0 + r;
+    if (i >= n) break;
+    const bf16* vrow = L.vt + (((int64_t)i * kH + h) * kD + d) * np;
+    float acc = 0.f;
+    for (int k = 8 * half; k < np; k += 16) {
+      const bf16x8 v = gload8(vrow + k);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)v[e];
+    }
+    acc += __shfl_xor(acc, 32, kWave);
+    const bf16 mean = (bf16)(acc * (1.f / n));
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int q = q0 + 8 * half + u;
+      if (q < n) L.o[((int64_t)i * n + q) * kC + h * kD + d] = mean;
+    }
+  }
+}
+
 // Two 8-wave blocks per CU need <= 128 VGPRs; one register more would leave a
 // single block per CU, which measured 1.5-2.3x slower, so the budget is pinned.
 __global__ __launch_bounds__(kCoreThreads) __attribute__((amdgpu_waves_per_eu(4))) void triattn_core_kernel(Layout L) {
@@ -541,17 +597,44 @@ __global__ __launch_bounds__(kCoreThreads) __attribute__((amdgpu_waves_per_eu(4)
   const int i0 = ig * kRows;
   const int q0 = qt * kCoreQ + 16 * w;  // this wave's 16 queries (< np: np is a multiple of kCoreQ)
 
-  bool masked = false;
-  for (int r = 0; r < kRows && i0 + r < n; ++r) {
-    const float* mbrow = L.mb + (int64_t)(i0 + r) * np;
-    for (int k = t; k < n; k += kCoreThreads) masked |= mbrow[k] != 0.f;
+  // Row classes from the projection's per-tile key spans: per row, the first
+  // masked key and the last open one.  Every wave reduces the same entries
+  // (shuffles, no barrier).
+  bool any_mask = false, suffix = true, all_closed = true;
+  int kend = 0, mask_from = n;
+  {
+    const int l = t & (kWave - 1), tiles = np / kP1;
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const int2* span = L.keyspan + (int64_t)min(i0 + r, n - 1) * tiles;  // rows past n repeat row n-1
+      int fm = n, lo = -1;
+      for (int e = l; e < tiles; e += kWave) {
+        const int2 v = span[e];
+        fm = min(fm, v.x);
+        lo = max(lo, v.y);
+      }
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) {
+        fm = min(fm, __shfl_xor(fm, d, kWave));
+        lo = max(lo, __shfl_xor(lo, d, kWave));
+      }
+      any_mask |= fm < n;
+      all_closed &= lo < 0;          // no open key at all
+      suffix &= lo >= 0 && lo < fm;  // some open key, and every open key before every masked one
+      kend = max(kend, fm);          // keys from here on are masked in every row (or past n)
+      mask_from = min(mask_from, fm);
+    }
   }
-  masked = __syncthreads_or(masked);
-  if (masked) {
-    core_rows<true, false>(L, i0, h, q0, stage_lds);
-  } else if (!core_rows<false, true>(L, i0, h, q0, stage_lds)) {
-    // a score rose far above the first stage's max: redo the block with the tracked max
-    core_rows<false, false>(L, i0, h, q0, stage_lds);
+  const int nk = (n + kKT - 1) / kKT * kKT;
+  if (all_closed) {
+    uniform_rows(L, i0, h, q0);
+  } else if (!any_mask) {
+    if (!core_rows<false, true>(L, i0, h, q0, stage_lds, nk, nk))
+      // a score rose far above the first stage's max: redo the block with the tracked max
+      core_rows<false, false>(L, i0, h, q0, stage_lds, nk, nk);
+  } else if (!suffix || !core_rows<false, true, true>(L, i0, h, q0, stage_lds, (kend + kKT - 1) / kKT * kKT,
+                                                      mask_from / kKT * kKT)) {
+    core_rows<true, false>(L, i0, h, q0, stage_lds, nk, nk);
   }
 }
 
@@ -692,6 +775,8 @@ Layout make_layout(void* ws, int n) {
   L.tb = (tb_t*)p;
   p += (int64_t)kH * L.np * L.np * sizeof(tb_t);
   L.mb = (float*)p;
+  p += (int64_t)L.np * L.np * 4;
+  L.keyspan = (int2*)p;
   return L;
 }
 
@@ -728,7 +813,7 @@ size_t bmx_triattn_workspace_bytes(int64_t n) {
   if (n <= 0) return 0;
   int64_t np = round_up(n, kPad);
   return (size_t)(3 * qkv_elems((int)np) * 2 + round_up(n * n * kC * 2, 256) + (int64_t)kH * np * np * (int64_t)sizeof(tb_t) +
-                  np * np * 4);
+                  np * np * 4 + np * (np / kP1) * (int64_t)sizeof(int2));
 }
 
 int bmx_triattn_fwd(const void* x, int x_dtype, const float* mask, int64_t n, int starting, float inf,

@@ -98,3 +98,43 @@ def test_core_rows_far_below_their_block_partner(gpu, gap):
     for rows in (slice(0, n, 2), slice(1, n, 2)):
         err = ((got[rows] - want[rows]).abs().max() / want[rows].abs().max()).item()
         assert err < 2e-2, err
+
+
+@pytest.mark.parametrize("n,masked,boost", [(200, "last31", 1.0), (200, "last140", 1.0), (256, "last51", 1.0),
+                                            (200, "last31", 3000.0), (200, "random10", 1.0)])
+def test_core_token_padding(gpu, n, masked, boost):
+    """Token masks (pair mask m_i m_k).  Rows of unmasked tokens have their
+    masked keys as a suffix when the padding is at the end: those blocks run
+    the speculative pass with the mask bias added from the first stage that
+    holds a padded key and skip the stages past the last open key (last31:
+    the mask starts inside a stage; last140: every row has fewer than 64 open
+    keys, so one stage).  Rows of padded tokens have no open key and take the
+    masked path (uniform weights), as do rows whose masked keys are not a
+    suffix (random10).  boost 3000 makes the speculative pass overflow after
+    its first stage, so those blocks are redone on the masked path."""
+    torch.manual_seed(7)
+    m = layers.TriangleAttention().to(gpu).eval()
+    x = torch.randn(1, n, n, 128, device=gpu)
+    tok = torch.ones(n, device=gpu)
+    if masked.startswith("last"):
+        tok[n - int(masked[4:]):] = 0
+    else:
+        tok[torch.randperm(n, generator=torch.Generator().manual_seed(8))[:int(masked[6:]) * n // 100].to(gpu)] = 0
+    mask = (tok[:, None] * tok[None, :]).contiguous()
+    ws = ops.new_workspace(n, gpu)
+    with torch.inference_mode():
+        ops.triattn(m, x[0], mask, True, ops.OUT_BF16, None, ws, stages=1)
+        npad, q, k, vt, o, tb, mb = _views(ws, n)
+        if boost != 1.0:
+            k[:, :, 64:n] = (k[:, :, 64:n].float() * boost).bfloat16()
+        ops.triattn(m, x[0], mask, True, ops.OUT_BF16, None, ws, stages=2)
+        want = _reference(n, npad, q, k, vt, tb, mb)
+        got = o.float()
+    assert torch.isfinite(got).all()
+    # open rows, and the padded rows (uniform weights; with boosted keys their
+    # scores no longer vanish next to the 1e9 mask bias in fp32, so only the
+    # open rows are compared there)
+    for rows in (tok.bool(), ~tok.bool()) if boost == 1.0 else (tok.bool(),):
+        if rows.any():
+            err = ((got[rows] - want[rows]).abs().max() / want[rows].abs().max()).item()
+            assert err < 2e-2, err
