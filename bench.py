@@ -471,10 +471,19 @@ def isolated_module(args, kind):
                 kfn = lambda m=m, nm=name: ops.triattn(m, x, mb, nm == "start", ops.OUT_BF16, None, ws, stages=2)
             kfn()
             kernel_ms[name], _ = timed_loop(kfn, steps, 1)
+    fp32_ms = {}
+    if kind == "triattn":  # fp32 mode (autocast off): fp32 LN and GEMMs, fused fp32-MFMA attention
+        with torch.inference_mode():
+            for name, m in mods.items():
+                fp32_ms[name], _ = timed_loop(lambda m=m, nm=name: ops.triattn_fp32(m, zd[0], pmd[0], nm == "start"),
+                                              max(3, steps // 4), 1)
     f, b = tri_module_cost(kind, n)
     ts = t_star_ms(f, b)
     modules = {f"{kind}_{k}": {"ms": round(v, 4), "t_star_ms": round(ts, 4), "frac": round(ts / v, 4)}
                for k, v in times.items()}
+    for k, v in fp32_ms.items():
+        modules[f"{kind}_{k}_fp32_mode"] = {"ms": round(v, 4), "t_star_ms": round(ts, 4), "frac": round(ts / v, 4),
+                                            "note": "fp32 mode, against the bf16 MFMA T*"}
     kf, kb = kernel_table(n)[core]
     kms = statistics.mean(kernel_ms.values())
     roofline = {"kernel": core, **roofline_of(kf, kb, kms), "traffic": measured_traffic(core, n),

@@ -431,6 +431,45 @@ def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=No
     return out
 
 
+def triattn_fp32(module, x, mask, starting):
+    """TriangleAttention (starting or ending node) in fp32 for x [N, N, 128]
+    fp32, the fp32 mode of the module (autocast off; reference
+    triangle.py:38-52 accelerates it too).  LayerNorm runs on the fp32 LN128
+    kernel; the q | k | v | g projection and the triangle bias are fp32 GEMMs;
+    the attention, mask bias, softmax, PV product and gate run fused in
+    ``bmx_seq_attention_batched_fwd`` on fp32 MFMA (every row i is one batch
+    element attending over its N keys, all rows sharing the [4, N, N]
+    triangle bias), so the [N, 4, N, N] scores never reach HBM; ``linear_o``
+    is an fp32 GEMM.  Returns fp32 [N, N, 128]."""
+    _cuda(x)
+    _check(x.dim() == 3 and x.size(0) == x.size(1) and x.size(2) == C and x.dtype == torch.float32,
+           "expected fp32 x of shape [N, N, 128]")
+    n = x.size(0)
+    mha, heads, d = module.mha, module.no_heads, module.c_hidden
+    _check(heads * d == C, "expected heads x head dim = 128")
+    if not starting:
+        x = x.transpose(0, 1)
+        mask = None if mask is None else mask.transpose(0, 1)
+    x = x.contiguous()
+    ln = module.layer_norm
+    xn = norm(x.view(-1, C), _f32(ln.weight), _f32(ln.bias), ln.eps, bf16_output=False)
+    w = cached_weight(module, "qkvg_f32", (mha.linear_q.weight, mha.linear_k.weight, mha.linear_v.weight,
+                                           mha.linear_g.weight), lambda *ws: torch.cat(ws, 0).float())
+    b = cached_weight(module, "qkvg_bias_f32", (mha.linear_g.bias,),
+                      lambda bg: torch.cat([bg.new_zeros(3 * C), bg]).float())
+    proj = torch.nn.functional.linear(xn, w, b).view(n, n, 4 * C)
+    tri_bias = torch.nn.functional.linear(xn, module.linear.weight.float()).view(n, n, heads)
+    tri_bias = tri_bias.permute(2, 0, 1).contiguous()  # [H, q, k], shared by every row
+    m = x.new_ones(n, n) if mask is None else mask.to(torch.float32).contiguous()
+    q, k, v, g = proj.split(C, dim=-1)
+    o = torch.empty((n, n, C), device=x.device, dtype=torch.float32)
+    N.call("bmx_seq_attention_batched_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), tri_bias.data_ptr(),
+           m.data_ptr(), g.data_ptr(), n, n, n, 4 * C, 4 * C, n * 4 * C, n * 4 * C, 0, n, n, heads, d,
+           float(module.inf), o.data_ptr(), _stream(x))
+    out = torch.nn.functional.linear(o, mha.linear_o.weight.float(), mha.linear_o.bias.float())
+    return out if starting else out.transpose(0, 1)
+
+
 def pair_transition(module, x, out_mode=OUT_BF16, out=None, pair_bias=None):
     """Fused Transition(128, 512) over the rows of x [..., 128].
 

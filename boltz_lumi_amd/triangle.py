@@ -14,7 +14,7 @@ from __future__ import annotations
 import torch
 
 from . import ops
-from ._guards import bf16_autocast, fp32_contiguous_on, gfx950_tensor, inference
+from ._guards import autocast_off, bf16_autocast, fp32_contiguous_on, gfx950_tensor, inference
 
 
 def _native_shape_ok(module, x) -> bool:
@@ -32,21 +32,24 @@ def _native_shape_ok(module, x) -> bool:
 def triangle_attention_forward(self, x, mask=None, chunk_size=None, use_kernels=False):
     """Drop-in for ``TriangleAttention{,EndingNode}.forward(x, mask, chunk_size, use_kernels)``.
 
-    Native under bf16 autocast (or for bf16 x) in inference; returns bf16 like
-    the upstream autocast path.  fp32 mode (autocast off, fp32 x) keeps the
-    upstream fp32 math so its 1e-4 tolerance holds."""
-    supported = (
+    Native in inference under bf16 autocast (or for bf16 x), with a bf16
+    result like the upstream autocast path; and in fp32 mode (autocast off,
+    fp32 x; reference triangle.py:38-52), with an fp32 result from fp32
+    LayerNorm, fp32 GEMMs and the fused fp32-MFMA attention (``ops.triattn_fp32``)."""
+    base = (
         not use_kernels
         and inference(self)
         and gfx950_tensor(x)
         and _native_shape_ok(self, x)
-        and (bf16_autocast() or x.dtype == torch.bfloat16)
-        and x.dtype in (torch.float32, torch.bfloat16)
         and (mask is None or tuple(mask.shape) == tuple(x.shape[:-1]))
     )
+    starting = getattr(self, "starting", True)
+    if base and autocast_off() and x.dtype == torch.float32 and self.layer_norm.weight.dtype == torch.float32:
+        outs = [ops.triattn_fp32(self, x[b], None if mask is None else mask[b], starting) for b in range(x.shape[0])]
+        return torch.stack(outs)
+    supported = base and (bf16_autocast() or x.dtype == torch.bfloat16) and x.dtype in (torch.float32, torch.bfloat16)
     if not supported:
         return type(self).forward(self, x, mask, chunk_size=chunk_size, use_kernels=use_kernels)
-    starting = getattr(self, "starting", True)
     out = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
     ws = ops.new_workspace(x.shape[1], x.device)
     for b in range(x.shape[0]):
