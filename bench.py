@@ -158,6 +158,25 @@ def exp_co_bound(n, core_ms):
             "issue_floor_frac": round((exp_ms + mfma_ms) / core_ms, 4)}
 
 
+class no_gc:
+    """Run the cyclic garbage collector, then pause it for the block (a full
+    collection stalls the launching thread for 50-60 ms, measured)."""
+
+    def __enter__(self):
+        import gc
+
+        gc.collect()
+        self.was_enabled = gc.isenabled()
+        gc.disable()
+
+    def __exit__(self, *exc):
+        import gc
+
+        if self.was_enabled:
+            gc.enable()
+        return False
+
+
 def event_timer():
     import torch
 
@@ -187,7 +206,10 @@ def timed_loop(fn, steps, warmup, warm_s=0.25):
     """ms per call of ``fn`` over ``steps`` calls after ``warmup`` untimed ones
     (continued until ``warm_s`` seconds have passed, so that the GPU has left
     its idle clocks on the measured work itself), between device
-    synchronisations, by HIP events on the current stream."""
+    synchronisations, by HIP events on the current stream.  Python's cyclic
+    garbage collector is run before and paused during the timed calls: a full
+    collection stalls the launching thread for 50-60 ms (measured), which
+    would leave the GPU idle for ten layers' worth of work."""
     import torch
 
     t0 = time.perf_counter()
@@ -198,14 +220,16 @@ def timed_loop(fn, steps, warmup, warm_s=0.25):
         if done >= warmup:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    wall0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps):
-        fn()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps, time.perf_counter() - wall0
+    with no_gc():
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        wall0 = time.perf_counter()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+    return e0.elapsed_time(e1) / steps, wall
 
 
 def line(metric, value, unit, args, steps, dtype, data, config, higher_is_better=False, **extra):
@@ -367,12 +391,13 @@ def per_kernel_times(layer, s, z, mask, pair_mask, z_out, ws, reps):
                                                                 pair_bias=pb)))
     plan.append(("sequence_stack", lambda: layer.sequence_stack(s, z_out, mask, pair_bias=bias)))
     timer = event_timer()
-    for _ in range(reps):
-        for name, fn in plan:
-            timer.run(name, fn)
-        for name, fn in modules:
-            timer.run("module:" + name, fn)
-    avg, cnt = timer.averages()
+    with no_gc():
+        for _ in range(reps):
+            for name, fn in plan:
+                timer.run(name, fn)
+            for name, fn in modules:
+                timer.run("module:" + name, fn)
+        avg, cnt = timer.averages()
     kernels = {k: (v, cnt[k] // reps) for k, v in avg.items() if not k.startswith("module:")}
     mods = {k[len("module:"):]: v for k, v in avg.items() if k.startswith("module:")}
     return kernels, mods

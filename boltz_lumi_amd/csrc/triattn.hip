@@ -47,9 +47,10 @@ struct Layout {
   bf16 *q, *k, *vt, *o;
   tb_t* tb;
   float* mb;
-  // Per row i and 64-key tile: the first masked key of the tile (n if none)
-  // and the last open key (-1 if none), keys < n only; written by the
-  // projection, read by the attention core to pick its path per block.
+  // Per row i and 64-key tile: the first masked key of the tile (n if none;
+  // -2 if some key's mask is neither 0 nor 1) and the last open key (-1 if
+  // none), keys < n only; written by the projection, read by the attention
+  // core to pick its path per block.
   int2* keyspan;
 };
 
@@ -178,7 +179,8 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
       const bool valid = i < n && j < n;
       const float mbv = valid ? inf * (mpre - 1.f) * kLog2e : 0.f;
       L.mb[(int64_t)i * np + j] = mbv;
-      int fm = valid && mbv != 0.f ? j : n, lo = valid && mbv == 0.f ? j : -1;
+      // masked keys: closed (mask 0) by index, fractional ones as -2 (they pin the block to the masked path)
+      int fm = valid && mbv != 0.f ? (mpre == 0.f ? j : -2) : n, lo = valid && mbv == 0.f ? j : -1;
 #pragma unroll
       for (int d = 32; d >= 1; d >>= 1) {
         fm = min(fm, __shfl_xor(fm, d, kWave));
@@ -619,7 +621,7 @@ __global__ __launch_bounds__(kCoreThreads) __attribute__((amdgpu_waves_per_eu(4)
         lo = max(lo, __shfl_xor(lo, d, kWave));
       }
       any_mask |= fm < n;
-      all_closed &= lo < 0;          // no open key at all
+      all_closed &= lo < 0 && fm >= 0;  // no open key, and every key closed by a 0 mask (no fractional one)
       suffix &= lo >= 0 && lo < fm;  // some open key, and every open key before every masked one
       kend = max(kend, fm);          // keys from here on are masked in every row (or past n)
       mask_from = min(mask_from, fm);

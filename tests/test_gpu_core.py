@@ -138,3 +138,29 @@ def test_core_token_padding(gpu, n, masked, boost):
         if rows.any():
             err = ((got[rows] - want[rows]).abs().max() / want[rows].abs().max()).item()
             assert err < 2e-2, err
+
+
+def test_core_fractional_mask_rows(gpu):
+    """Masks that are neither 0 nor 1 (mask bias between 0 and -1e9 log2 e):
+    rows whose every key is fractional have no open key but are not uniform,
+    so they must take the masked path, not the closed-row mean; rows mixing
+    open, closed and fractional keys likewise."""
+    torch.manual_seed(9)
+    n = 160
+    m = layers.TriangleAttention().to(gpu).eval()
+    x = torch.randn(1, n, n, 128, device=gpu)
+    g = torch.Generator().manual_seed(10)
+    mask = torch.ones(n, n)
+    mask[:64] = 1.0 - (torch.rand(64, n, generator=g) * 9e-7 + 2e-7)  # fractional everywhere, just below 1
+    mask[64:96, 100:] = 0.0                                   # open keys then a closed suffix
+    mask[64:96, 120:130] = 0.9999999                         # ... with fractional keys inside it
+    mask = mask.to(gpu)
+    ws = ops.new_workspace(n, gpu)
+    with torch.inference_mode():
+        ops.triattn(m, x[0], mask, True, ops.OUT_BF16, None, ws, stages=3)
+        npad, q, k, vt, o, tb, mb = _views(ws, n)
+        want = _reference(n, npad, q, k, vt, tb, mb)
+        got = o.float()
+    assert torch.isfinite(got).all()
+    err = ((got - want).abs().max() / want.abs().max()).item()
+    assert err < 2e-2, err
