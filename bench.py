@@ -645,6 +645,52 @@ def diffusion_step(args):
     print(json.dumps(out), flush=True)
 
 
+def elementwise_kernel_rates(m, d, di, g, dev, reps_min=10):
+    """The fused diffusion elementwise kernels at M rows: bmx_adaln (width D),
+    bmx_diffusion_epilogue GATED_SWIGLU (width Di) and GATE (width D), each
+    launched through the C ABI on preallocated outputs, cycling through input
+    sets larger than the 256 MB Infinity Cache, and timed by HIP events.  The
+    Python wrappers allocate the output and check the arguments on every call
+    (host time longer than these 10-20 us kernels), so they are not in the
+    loop.  Bytes per launch: AdaLN 16 M D, GATED_SWIGLU 16 M Di, GATE 12 M D."""
+    import torch
+    from boltz_lumi_amd import _native as N, ops
+
+    sets = 1 + (768 << 20) // (16 * m * d)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def rnd(*shape):
+        return torch.randn(*shape, generator=g).to(dev)
+
+    bufs = [{"a": rnd(m, d), "scale": rnd(m, d), "shift": rnd(m, d), "u": rnd(m, 2 * di), "b": rnd(m, di),
+             "g": rnd(m, d), "y": rnd(m, d), "out": torch.empty(m, d, device=dev),
+             "out_i": torch.empty(m, di, device=dev)} for _ in range(sets)]
+    reps = sets * max(1, reps_min // sets + 1)
+    # entry point, per-set argument tuples (pointers taken once), bytes per launch
+    launches = {
+        "adaln": ("bmx_adaln", [(t["a"].data_ptr(), t["scale"].data_ptr(), t["shift"].data_ptr(),
+                                 t["out"].data_ptr(), 0, m, d, 1e-5, st) for t in bufs], 16 * m * d),
+        "gated_swiglu": ("bmx_diffusion_epilogue", [(ops.GATED_SWIGLU, t["u"].data_ptr(), t["b"].data_ptr(), None,
+                                                     t["out_i"].data_ptr(), 0, m, di, st) for t in bufs],
+                         16 * m * di),
+        "gate": ("bmx_diffusion_epilogue", [(ops.GATE, t["g"].data_ptr(), t["y"].data_ptr(), None,
+                                             t["out"].data_ptr(), 0, m, d, st) for t in bufs], 12 * m * d)}
+    out = {}
+    for name, (entry, arg_sets, nbytes) in launches.items():
+        fn = getattr(N.lib(), entry)
+        turn = [0]
+
+        def step(fn=fn, arg_sets=arg_sets, entry=entry):
+            if fn(*arg_sets[turn[0]]) != 0:
+                raise RuntimeError(f"{entry} failed: {N.last_error()}")
+            turn[0] = (turn[0] + 1) % sets
+
+        ms, _ = timed_loop(step, reps, sets)
+        out[name] = {"ms": round(ms, 4), "bytes": nbytes, "input_sets": sets,
+                     **roofline_of(0, nbytes, ms, PEAK_BF16_TFLOPS)}
+    return out
+
+
 def diffusion_kernel_times(stacks, t, packed, samples, tokens):
     """Each fused kernel of one step at the step's shapes, timed alone:
     the token attention (fp32 MFMA, 16 x 48), the windowed atom attention
@@ -677,13 +723,10 @@ def diffusion_kernel_times(stacks, t, packed, samples, tokens):
     rate("seq_attention (atom windows, 4 x 32)",
          lambda: ops.seq_attention_batched(aq[..., :128], ak[..., :128], ak[..., 128:], ab, am, aq[..., 128:], 1e6),
          4.0 * 4 * 32 * 32 * 128 * samples * nw, samples * nw * (32 * 512 + 128 * 1024 + 4 * 32 * 128 * 4), 6)
-    x = [torch.randn(m, d, generator=g).to(dev) for _ in range(3)]
-    rate("adaln (token)", lambda: ops.adaln_modulate(x[0], x[1], x[2], 1e-5), 0, 16 * m * d, 48, PEAK_BF16_TFLOPS)
-    u = torch.randn(m, 4 * d, generator=g).to(dev)
-    b = torch.randn(m, 2 * d, generator=g).to(dev)
-    rate("gated_swiglu (token)", lambda: ops.epilogue(u, b, None, ops.GATED_SWIGLU), 0, 16 * m * 2 * d, 24,
-         PEAK_BF16_TFLOPS)
-    rate("gate (token)", lambda: ops.epilogue(x[0], x[1], None, ops.GATE), 0, 12 * m * d, 24, PEAK_BF16_TFLOPS)
+    per_step = {"adaln": 48, "gated_swiglu": 24, "gate": 24}
+    for name, rec in elementwise_kernel_rates(m, d, 2 * d, g, dev).items():
+        out[f"{name} (token)"] = {"ms": rec["ms"], "launches_per_step": per_step[name],
+                                  **{k: rec[k] for k in ("bound", "achieved", "peak", "unit", "frac")}}
     return out
 
 
@@ -835,29 +878,9 @@ def diffusion(args):
 
             blocks[name], _ = timed_loop(layer, steps, args.warmup)
             blocks[name + "_attention"], _ = timed_loop(lambda: prepared_forward(apb, qs, z, kmask, ks, mult), steps, 1)
-            sets = 1 + (768 << 20) // (16 * m * d)
-            bufs = [{"a": torch.randn(m, d, generator=g).to(dev), "scale": torch.randn(m, d, generator=g).to(dev),
-                     "shift": torch.randn(m, d, generator=g).to(dev), "u": torch.randn(m, 2 * di, generator=g).to(dev),
-                     "b": torch.randn(m, di, generator=g).to(dev), "g": torch.randn(m, d, generator=g).to(dev),
-                     "y": torch.randn(m, d, generator=g).to(dev)} for _ in range(sets)]
-            reps = sets * max(1, max(steps, 10) // sets)
-            turn = [0]
-
-            def nxt():
-                turn[0] = (turn[0] + 1) % sets
-                return bufs[turn[0]]
-
-            for kname, fn, nbytes in (
-                    ("adaln", lambda: (lambda t: ops.adaln_modulate(t["a"], t["scale"], t["shift"], 1e-5))(nxt()),
-                     16 * m * d),
-                    ("gated_swiglu", lambda: (lambda t: ops.epilogue(t["u"], t["b"], None, ops.GATED_SWIGLU))(nxt()),
-                     16 * m * di),
-                    ("gate", lambda: (lambda t: ops.epilogue(t["g"], t["y"], None, ops.GATE))(nxt()), 12 * m * d)):
-                ms, _ = timed_loop(fn, reps, 1)
-                gbs = nbytes / (ms * 1e-3) / 1e9
-                kernels[f"{kname}_{name}"] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(gbs, 1),
-                                              "frac": round(gbs / PEAK_HBM_GBS, 4), "input_sets": sets}
-            del bufs
+            for kname, rec in elementwise_kernel_rates(m, d, di, g, dev, max(steps, 10)).items():
+                kernels[f"{kname}_{name}"] = {"ms": rec["ms"], "bytes": rec["bytes"], "gbs": rec["achieved"],
+                                              "frac": rec["frac"], "input_sets": rec["input_sets"]}
     ms = blocks["token"] + blocks["atom"]
     dom = kernels["gated_swiglu_token"]
     out_line = line("diffusion score-model modules (AdaLN + AttentionPairBias + ConditionedTransitionBlock) ms per "

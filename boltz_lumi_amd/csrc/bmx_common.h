@@ -133,6 +133,14 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
   return v;
 }
+// Sum over a whole wave whose 64 lanes are all active: the DPP half-wave
+// sum, then the two halves' totals read into scalars (no LDS round trip).
+// The result is the same in every lane.
+__device__ __forceinline__ float wave_sum_full(float v) {
+  v = half_sum(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));

@@ -158,8 +158,14 @@ __global__ __launch_bounds__(256) void epilogue_kernel(const T* __restrict__ a, 
   const int64_t q = cols >> 2;
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= rows * q) return;
-  int64_t row = i / q, col = (i - row * q) * 4;
-  int64_t o = row * cols + col;
+  // Rows are contiguous (cols % 4 == 0): element 4 i of the flat arrays; only
+  // the gated SwiGLU, whose a operand is twice as wide, needs the row.
+  int64_t row = 0, col = 0, o = 4 * i;
+  if (KIND == kGatedSwiGLU) {
+    row = i / q;
+    col = (i - row * q) * 4;
+    o = row * cols + col;
+  }
   f32x4 r;
   if (KIND == kModulation) {
     f32x4 av = load4(a + o), bv = load4(b + o), cv = load4(c + o);

@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const T* __restrict__ x, c
     v[u] = ch < chunks ? load4(x + row * d + 4 * ch) : f32x4{0.f, 0.f, 0.f, 0.f};
     s += v[u][0] + v[u][1] + v[u][2] + v[u][3];
   }
-  const float mean = wave_sum(s) / d;
+  const float mean = wave_sum_full(s) / d;
   float q = 0.f;
 #pragma unroll
   for (int u = 0; u < kMaxChunks; ++u) {
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const T* __restrict__ x, c
       q += dv[0] * dv[0] + dv[1] * dv[1] + dv[2] * dv[2] + dv[3] * dv[3];
     }
   }
-  const float inv = rsqrtf(wave_sum(q) / d + eps);
+  const float inv = rsqrtf(wave_sum_full(q) / d + eps);
 #pragma unroll
   for (int u = 0; u < kMaxChunks; ++u) {
     int ch = l + 64 * u;
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256) void adaln_kernel(const T* __restrict__ a, con
     sc[u] = load4(scale + base + 4 * ch);
     sh[u] = load4(shift + base + 4 * ch);
   }
-  auto reduce = [](float x) { return LANES == 64 ? wave_sum(x) : half_sum(x); };
+  auto reduce = [](float x) { return LANES == 64 ? wave_sum_full(x) : half_sum(x); };
   float s = 0.f;
 #pragma unroll
   for (int u = 0; u < kPer; ++u)
