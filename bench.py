@@ -693,7 +693,7 @@ def elementwise_kernel_rates(m, d, di, g, dev, reps_min=10):
 
 def diffusion_kernel_times(stacks, t, packed, samples, tokens):
     """Each fused kernel of one step at the step's shapes, timed alone:
-    the token attention (fp32 MFMA, 16 x 48), the windowed atom attention
+    the token attention (split-bf16 MFMA, 16 x 48), the windowed atom attention
     (4 x 32), AdaLN and the conditioned-transition epilogues at the token
     shape; launches per step count every layer."""
     import torch
@@ -712,9 +712,12 @@ def diffusion_kernel_times(stacks, t, packed, samples, tokens):
     qq, kk, vv, gg = q.split(d, dim=-1)
     bias = packed[..., :16].movedim(-1, 1)
     mask = torch.ones(samples, tokens, device=dev)
-    rate("seq_attention (token, 16 x 48)",
+    # split-bf16 by default (the K / V split pre-pass included): 3 bf16 MFMA
+    # products per fp32 product, so the executed flops against the bf16 peak
+    rate("seq_attention (token, 16 x 48, split-bf16)",
          lambda: ops.seq_attention_batched(qq, kk, vv, bias, mask, gg, 1e6, bias_div=samples),
-         4.0 * 16 * 48 * tokens * tokens * samples, samples * tokens * d * 16 + 16 * tokens * tokens * 4, 24)
+         3 * 4.0 * 16 * 48 * tokens * tokens * samples, samples * tokens * d * 16 + 16 * tokens * tokens * 4, 24,
+         PEAK_BF16_TFLOPS)
     nw = 8192 // 32
     aq = torch.randn(samples * nw, 32, 2 * 128, generator=g).to(dev)
     ak = torch.randn(samples * nw, 128, 2 * 128, generator=g).to(dev)

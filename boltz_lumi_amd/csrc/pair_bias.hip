@@ -245,6 +245,297 @@ int launch_seq_attention(const char* name, const float* q, const float* k, const
   return check_launch(name);
 }
 
+// ------------------------------------------------------------------
+// The same attention on bf16 MFMA with both products split into bf16 high
+// and low parts (x y ~ xh yh + xh yl + xl yh, about 2^-16 relative per
+// product, the form the fp32 linears of the diffusion blocks use), for long
+// key rows (the token transformer's).
+//
+// A pre-pass writes K as bf16 hi / lo [b][h][key][d] and V^T as hi / lo
+// [b][h][d][key'], keys padded with zeros to a multiple of the 64-key stage
+// and, in V^T, permuted inside each 32-key block into the order in which a
+// lane holds P: slot 8 gi + e of a block holds key 4 gi + e (e < 4) or
+// 16 + 4 gi + e - 4.  A block serves 64 queries of one head (16 per wave) and
+// walks the keys in 64-key stages that LDS DMA copies into a double-buffered
+// LDS stage shared by the four waves (K tiles dense, V^T rows of 64 slots with
+// their 16-byte chunks XOR-swizzled by d & 7), so each K / V element is read
+// from L2 once per 64 queries.  v_mfma_f32_16x16x32_bf16 (lane l, gi = l / 16:
+// A holds A[l%16][8 gi .. 8 gi + 7], B holds B[8 gi .. 8 gi + 7][l%16], D
+// register r holds D[4 gi + r][l%16]); per stage and wave:
+//   S^T[key][q] = K Q^T         four 16-key tiles, ceil(D / 32) k steps of 32
+//                               dims (dims past D are zero), 3 terms;
+//   O^T[d][q] += V^T P^T        two 32-key k steps per 16-dim tile, 3 terms,
+//                               P^T from the lane's probabilities.
+constexpr int kX3Stage = 64;  // keys per LDS stage
+constexpr int kX3Q = 64;      // queries per block
+
+__host__ __device__ inline int64_t x3_nkp(int64_t nk) { return (nk + kX3Stage - 1) / kX3Stage * kX3Stage; }
+
+__device__ __forceinline__ int x3_slot(int key_in_block) {
+  return ((key_in_block & 15) >> 2) * 8 + (key_in_block >> 4) * 4 + (key_in_block & 3);
+}
+
+// Thread (channel c, 32-key block kb, element b) splits K[b][kb*32 + e][c] and
+// V[b][kb*32 + e][c] for the block's 32 keys (zeros past nk).
+__global__ __launch_bounds__(256) void seq_attn_split_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                             int nk, int64_t ldk, int64_t sk, int heads, int d,
+                                                             bf16* __restrict__ kh, bf16* __restrict__ kl,
+                                                             bf16* __restrict__ vth, bf16* __restrict__ vtl) {
+  const int hd = heads * d;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= hd) return;
+  const int kb = blockIdx.y, hh = c / d, dd = c % d;
+  const int64_t b = blockIdx.z, nkp = x3_nkp(nk);
+  const float* kb_src = k + b * sk + c;
+  const float* vb_src = v + b * sk + c;
+  bf16* kh_dst = kh + ((b * heads + hh) * nkp) * d + dd;
+  bf16* kl_dst = kl + ((b * heads + hh) * nkp) * d + dd;
+  bf16x8 vh[4], vlo[4];
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const int key = kb * 32 + e;
+    float kv = 0.f, vv = 0.f;
+    if (key < nk) {
+      kv = kb_src[(int64_t)key * ldk];
+      vv = vb_src[(int64_t)key * ldk];
+    }
+    const bf16 khi = (bf16)kv;
+    kh_dst[(int64_t)key * d] = khi;
+    kl_dst[(int64_t)key * d] = (bf16)(kv - (float)khi);
+    const int slot = x3_slot(e);
+    const bf16 vhi = (bf16)vv;
+    vh[slot >> 3][slot & 7] = vhi;
+    vlo[slot >> 3][slot & 7] = (bf16)(vv - (float)vhi);
+  }
+  const int64_t row = ((b * heads + hh) * d + dd) * nkp + kb * 32;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    *(bf16x8*)(vth + row + 8 * u) = vh[u];
+    *(bf16x8*)(vtl + row + 8 * u) = vlo[u];
+  }
+}
+
+__device__ __forceinline__ f32x4 mfma16bf(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// One LDS DMA: 64 lanes x 16 bytes from per-lane global addresses to
+// lds_addr + 16 * lane; waited for explicitly (s_waitcnt vmcnt(0)) before the
+// barrier that publishes the stage.
+__device__ __forceinline__ void lds_dma16(const void* src, unsigned lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
+}
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+template <int D>
+__global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __restrict__ q,
+                                                               const bf16* __restrict__ kh, const bf16* __restrict__ kl,
+                                                               const bf16* __restrict__ vth,
+                                                               const bf16* __restrict__ vtl,
+                                                               const float* __restrict__ bias,
+                                                               const float* __restrict__ mask,
+                                                               const float* __restrict__ g, SeqAttnShape sh, int heads,
+                                                               float inf, float rscale, bool vec,
+                                                               float* __restrict__ out) {
+  constexpr int DK = (D + 31) / 32;              // QK^T k steps
+  constexpr int DT = (D + 15) / 16;              // O^T d tiles
+  constexpr int kTile = kX3Stage * D * 2;        // bytes of one K (or V^T) tile, hi or lo
+  constexpr int kStage = 4 * kTile;              // K hi, K lo, V^T hi, V^T lo
+  constexpr int kDmaPerWave = kStage / 1024 / kAttnWaves;
+  static_assert(D % 8 == 0 && kTile % 1024 == 0 && kDmaPerWave * kAttnWaves * 1024 == kStage, "stage layout");
+  __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
+  const int HD = heads * D;
+  const int nq = sh.nq, nk = sh.nk;
+  const int64_t ldq = sh.ldq, nkp = x3_nkp(nk);
+  const int64_t b = blockIdx.z;
+  const int h = blockIdx.y;
+  q += b * sh.sq;
+  g += b * sh.sq;
+  bias += (b / sh.bdiv) * sh.sbias;
+  mask += b * sh.smask;
+  out += b * nq * HD;
+  const bf16* k_src[2] = {kh + (b * heads + h) * nkp * D, kl + (b * heads + h) * nkp * D};
+  const bf16* v_src[2] = {vth + (b * heads + h) * D * nkp, vtl + (b * heads + h) * D * nkp};
+  const int l = lane_id(), gi = l >> 4, c = l & 15, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qw = blockIdx.x * kX3Q + 16 * w;     // this wave's 16 queries
+  const int qc = min(qw + c, nq - 1);            // rows past the end re-read the last one and are not stored
+  const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
+
+  // DMA job u of this wave copies stage bytes [1024 j, 1024 j + 1024), j = w + 4 u:
+  // region j / (kTile / 1024) is K hi, K lo, V^T hi or V^T lo.  K tiles are
+  // the dense rows of 64 keys; a V^T row is 64 slots (128 bytes) whose chunk
+  // at position p holds the global chunk p ^ (d & 7).
+  const bf16* dma_src[kDmaPerWave];
+  int dma_step[kDmaPerWave];
+#pragma unroll
+  for (int u = 0; u < kDmaPerWave; ++u) {
+    const int j = w + kAttnWaves * u, region = j / (kTile / 1024);
+    const int off = (j - region * (kTile / 1024)) * 1024 + 16 * l;  // byte offset inside the tile
+    if (region < 2) {
+      dma_src[u] = k_src[region] + off / 2;
+      dma_step[u] = kX3Stage * D;
+    } else {
+      const int d = off / 128, p = (off % 128) / 16;
+      dma_src[u] = v_src[region - 2] + (int64_t)d * nkp + 8 * (p ^ (d & 7));
+      dma_step[u] = kX3Stage;
+    }
+  }
+  auto dma_stage = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < kDmaPerWave; ++u) {
+      const int j = w + kAttnWaves * u;
+      lds_dma16(dma_src[u], __builtin_amdgcn_readfirstlane(lds0 + buf * kStage + 1024 * j));
+      dma_src[u] += dma_step[u];
+    }
+  };
+
+  // Q^T (B operand): dims 32 ks + 8 gi .. + 7 of query qc, split; dims past D are zero.
+  bf16x8 qh[DK], ql[DK];
+#pragma unroll
+  for (int ks = 0; ks < DK; ++ks) {
+    const int d0 = 32 * ks + 8 * gi;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = d0 < D ? q[(int64_t)qc * ldq + h * D + d0 + e] : 0.f;
+      qh[ks][e] = (bf16)x;
+      ql[ks][e] = (bf16)(x - (float)qh[ks][e]);
+    }
+  }
+  const float* brow = bias + ((int64_t)h * nq + qc) * nk;
+  const bf16x8 zero8 = {};
+  f32x4 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -3.4e38f, lsum = 0.f;
+  const int nst = (int)(nkp / kX3Stage);
+  // the q loads must land before the first DMA: a wait the compiler places for
+  // them inside the loop would be vmcnt(0), which also waits for a DMA in flight
+  wait_vm0();
+  dma_stage(0);
+  wait_vm0();
+  __syncthreads();
+  for (int st = 0; st < nst; ++st) {
+    if (st + 1 < nst) dma_stage((st + 1) & 1);
+    const char* sb = lds + (st & 1) * kStage;
+    const int key0 = st * kX3Stage;
+    const bool full = vec && key0 + kX3Stage <= nk;
+    f32x4 sc[4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < DK; ++ks) {
+        const int d0 = 32 * ks + 8 * gi;
+        const int off = ((16 * t + c) * D + d0) * 2;
+        const bf16x8 ah = d0 < D ? *(const bf16x8*)(sb + off) : zero8;
+        const bf16x8 al = d0 < D ? *(const bf16x8*)(sb + kTile + off) : zero8;
+        acc = mfma16bf(ah, qh[ks], acc);
+        acc = mfma16bf(ah, ql[ks], acc);
+        acc = mfma16bf(al, qh[ks], acc);
+      }
+      const int kb = key0 + 16 * t + 4 * gi;  // this lane's keys kb .. kb + 3
+      f32x4 b4, m4;
+      if (full) {
+        b4 = *(const f32x4*)(brow + kb);
+        m4 = *(const f32x4*)(mask + kb);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          b4[r] = brow[min(kb + r, nk - 1)];
+          m4[r] = mask[min(kb + r, nk - 1)];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = (acc[r] * rscale + b4[r]) + (1.f - m4[r]) * -inf;
+        sc[t][r] = kb + r < nk ? x : -INFINITY;
+        tmax = fmaxf(tmax, sc[t][r]);
+      }
+    }
+    const float mn = fmaxf(m, col_max(tmax));
+    const float alpha = __builtin_amdgcn_exp2f((m - mn) * kLog2e);
+    m = mn;
+    lsum *= alpha;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] *= alpha;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      // P^T of keys key0 + 32 s2 + (slots): slot 4 t' + r <-> key 16 t' + 4 gi + r of the 32-key block
+      bf16x8 ph, pl;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pr = __builtin_amdgcn_exp2f((sc[2 * s2 + t][r] - mn) * kLog2e);
+          lsum += pr;
+          ph[4 * t + r] = (bf16)pr;
+          pl[4 * t + r] = (bf16)(pr - (float)ph[4 * t + r]);
+        }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = 16 * dt + c, chunk = 4 * s2 + gi;
+        const int off = d * (kX3Stage * 2) + ((chunk ^ (d & 7)) * 16);
+        const bf16x8 vh = d < D ? *(const bf16x8*)(sb + 2 * kTile + off) : zero8;
+        const bf16x8 vl = d < D ? *(const bf16x8*)(sb + 3 * kTile + off) : zero8;
+        o[dt] = mfma16bf(vh, ph, o[dt]);
+        o[dt] = mfma16bf(vh, pl, o[dt]);
+        o[dt] = mfma16bf(vl, ph, o[dt]);
+      }
+    }
+    wait_vm0();  // this wave's DMAs of the next stage
+    __syncthreads();
+  }
+  // This wave holds every key of its 16 queries: O^T rows 16 dt + 4 gi + r of query qw + c.
+  lsum = col_sum(lsum);
+  const int i = qw + c;
+  if (i < nq) {
+    const float inv = 1.f / lsum;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d0 = 16 * dt + 4 * gi;
+      if (d0 < D) {
+        const f32x4 gv = load4(g + (int64_t)i * ldq + h * D + d0);
+        f32x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = sigmoid_f(gv[e]) * (o[dt][e] * inv);
+        store4(out + (int64_t)i * HD + h * D + d0, r);
+      }
+    }
+  }
+}
+
+size_t x3_workspace_bytes(int64_t batch, int64_t nk, int heads, int head_dim) {
+  const size_t tile = (size_t)(batch * heads * head_dim * x3_nkp(nk)) * sizeof(bf16);  // K and V^T alike
+  return 4 * ((tile + 255) / 256 * 256);
+}
+
+int launch_seq_attention_x3(const char* name, const float* q, const float* k, const float* v, const float* bias,
+                            const float* mask, const float* g, int64_t batch, const SeqAttnShape& sh, int heads,
+                            int head_dim, float inf, float* out, void* ws, hipStream_t stream) {
+  const int64_t hd = (int64_t)heads * head_dim, nkp = x3_nkp(sh.nk);
+  const size_t tile = ((size_t)(batch * hd * nkp) * sizeof(bf16) + 255) / 256 * 256;
+  bf16* kh = (bf16*)ws;
+  bf16* kl = (bf16*)((char*)ws + tile);
+  bf16* vth = (bf16*)((char*)ws + 2 * tile);
+  bf16* vtl = (bf16*)((char*)ws + 3 * tile);
+  const dim3 sgrid((unsigned)((hd + 255) / 256), (unsigned)(nkp / 32), (unsigned)batch);
+  seq_attn_split_kernel<<<sgrid, 256, 0, stream>>>(k, v, sh.nk, sh.ldk, sh.sk, heads, head_dim, kh, kl, vth, vtl);
+  if (int rc = check_launch(name)) return rc;
+  const bool vec = sh.nk % 4 == 0 && sh.sbias % 4 == 0 && sh.smask % 4 == 0 && (uintptr_t)bias % 16 == 0 &&
+                   (uintptr_t)mask % 16 == 0;
+  const dim3 grid((unsigned)((sh.nq + kX3Q - 1) / kX3Q), (unsigned)heads, (unsigned)batch);
+  const float rscale = 1.f / sqrtf((float)head_dim);
+#define SEQ_ATTN_X3(DIM)                                                                                          \
+  seq_attention_x3_kernel<DIM><<<grid, 256, 0, stream>>>(q, kh, kl, vth, vtl, bias, mask, g, sh, heads, inf, rscale, \
+                                                         vec, out)
+  if (head_dim == 24) SEQ_ATTN_X3(24);
+  else if (head_dim == 32) SEQ_ATTN_X3(32);
+  else SEQ_ATTN_X3(48);
+#undef SEQ_ATTN_X3
+  return check_launch(name);
+}
+
 }  // namespace
 
 extern "C" {
@@ -303,6 +594,42 @@ int bmx_seq_attention_batched_fwd(const float* q, const float* k, const float* v
   const SeqAttnShape sh{(int)nq, (int)nk, (int)bias_div, ldq, ldk, sq, sk, sbias, smask};
   return launch_seq_attention("bmx_seq_attention_batched_fwd", q, k, v, bias, mask, g, batch, sh, heads, head_dim,
                               inf, out, stream);
+}
+
+size_t bmx_seq_attention_x3_workspace_bytes(int64_t batch, int64_t nk, int heads, int head_dim) {
+  if (batch <= 0 || nk <= 0 || heads <= 0 || head_dim <= 0) return 0;
+  return x3_workspace_bytes(batch, nk, heads, head_dim);
+}
+
+int bmx_seq_attention_x3_batched_fwd(const float* q, const float* k, const float* v, const float* bias,
+                                     const float* mask, const float* g, int64_t batch, int64_t nq, int64_t nk,
+                                     int64_t ldq, int64_t ldk, int64_t sq, int64_t sk, int64_t sbias, int64_t smask,
+                                     int64_t bias_div, int heads, int head_dim, float inf, float* out,
+                                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  BMX_REQUIRE(batch >= 0 && batch <= 65535, "bmx_seq_attention_x3_batched_fwd: batch must be in [0, 65535]");
+  BMX_REQUIRE(nq >= 0 && nq <= (1 << 20) && nk >= 1 && nk <= (1 << 20),
+              "bmx_seq_attention_x3_batched_fwd: need 0 <= nq <= 2^20 and 1 <= nk <= 2^20");
+  BMX_REQUIRE(head_dim == 24 || head_dim == 32 || head_dim == 48,
+              "bmx_seq_attention_x3_batched_fwd: head_dim must be 24, 32 or 48 (got %d)", head_dim);
+  BMX_REQUIRE(heads >= 1 && heads <= 64, "bmx_seq_attention_x3_batched_fwd: heads must be in [1, 64] (got %d)",
+              heads);
+  BMX_REQUIRE(ldq >= (int64_t)heads * head_dim && ldk >= (int64_t)heads * head_dim,
+              "bmx_seq_attention_x3_batched_fwd: row strides must be >= heads * head_dim");
+  BMX_REQUIRE(sq >= 0 && sk >= 0 && sbias >= 0 && smask >= 0 && bias_div >= 1,
+              "bmx_seq_attention_x3_batched_fwd: strides must be >= 0 and bias_div >= 1");
+  BMX_REQUIRE(inf > 0.f, "bmx_seq_attention_x3_batched_fwd: inf must be positive");
+  if (batch == 0 || nq == 0) return BMX_OK;
+  BMX_REQUIRE(q && k && v && bias && mask && g && out && workspace,
+              "bmx_seq_attention_x3_batched_fwd: null pointer");
+  BMX_REQUIRE(ldq % 4 == 0 && sq % 4 == 0 && (uintptr_t)g % 16 == 0 && (uintptr_t)out % 16 == 0,
+              "bmx_seq_attention_x3_batched_fwd: g and out must be 16-byte aligned, ldq and sq multiples of 4");
+  const size_t need = x3_workspace_bytes(batch, nk, heads, head_dim);
+  BMX_REQUIRE(workspace_bytes >= need && (uintptr_t)workspace % 256 == 0,
+              "bmx_seq_attention_x3_batched_fwd: workspace must be 256-byte aligned and hold %zu bytes (got %zu)",
+              need, workspace_bytes);
+  const SeqAttnShape sh{(int)nq, (int)nk, (int)bias_div, ldq, ldk, sq, sk, sbias, smask};
+  return launch_seq_attention_x3("bmx_seq_attention_x3_batched_fwd", q, k, v, bias, mask, g, batch, sh, heads,
+                                 head_dim, inf, out, workspace, stream);
 }
 
 }  // extern "C"

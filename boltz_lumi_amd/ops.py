@@ -569,13 +569,23 @@ def seq_attention(q, k, v, bias, mask, g, inf, out=None):
     return out
 
 
-def seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=1, out=None):
+# The token transformer's attention (H * D = 768 >= X3_MIN_K, 1024 keys) runs
+# its two products as split-bf16 MFMA (bmx_seq_attention_x3_batched_fwd) like
+# its linears, unless exact fp32 is switched on; short key rows (the atom
+# windows' 128) and the Pairformer sequence stack (H * D = 384) keep the fp32
+# MFMA kernel, where the split pre-pass would cost more than it saves.
+X3_ATTN_MIN_KEYS = 256
+
+
+def seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=1, out=None, split=None):
     """``seq_attention`` for a batch in one launch (``bmx_seq_attention_batched_fwd``):
     q, g [B, NQ, H * D] and k, v [B, NK, H * D] (D = 24, 32 or 48; unit column
     stride; q and g share their strides, k and v theirs), bias
     [B / bias_div, H, NQ, NK] with dense elements (element b uses bias
     b // bias_div), mask [B or 1, NK] with unit stride.  Returns (or writes into
-    ``out``) a contiguous fp32 [B, NQ, H * D]."""
+    ``out``) a contiguous fp32 [B, NQ, H * D].  ``split``: True for the
+    split-bf16 kernel (``bmx_seq_attention_x3_batched_fwd``, about 2^-16
+    relative per product), False for fp32 MFMA, None to choose as above."""
     _cuda(q, k, v, bias, mask, g)
     _check(q.dim() == 3 and k.dim() == 3 and bias.dim() == 4 and mask.dim() == 2, "expected 3-d q/k, 4-d bias, 2-d mask")
     b, nq, width = q.shape
@@ -593,11 +603,20 @@ def seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=1, out=None):
         out = torch.empty((b, nq, width), device=q.device, dtype=torch.float32)
     _check(out.shape == (b, nq, width) and out.dtype == torch.float32 and out.is_contiguous(),
            "out must be a contiguous fp32 [B, NQ, H * D]")
+    if split is None:
+        split = (not _EXACT_FP32[0] and width >= X3_MIN_K and nk >= X3_ATTN_MIN_KEYS and g.data_ptr() % 16 == 0
+                 and q.stride(1) % 4 == 0 and q.stride(0) % 4 == 0)
     if b and nq:
-        N.call("bmx_seq_attention_batched_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(),
-               mask.data_ptr(), g.data_ptr(), b, nq, nk, q.stride(1), k.stride(1), q.stride(0), k.stride(0),
-               bias.stride(0), mask.stride(0) if mask.shape[0] > 1 else 0, bias_div, heads, width // heads,
-               float(inf), out.data_ptr(), _stream(q))
+        args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), mask.data_ptr(), g.data_ptr(), b, nq, nk,
+                q.stride(1), k.stride(1), q.stride(0), k.stride(0), bias.stride(0),
+                mask.stride(0) if mask.shape[0] > 1 else 0, bias_div, heads, width // heads, float(inf),
+                out.data_ptr())
+        if split:
+            nbytes = N.lib().bmx_seq_attention_x3_workspace_bytes(b, nk, heads, width // heads)
+            ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+            N.call("bmx_seq_attention_x3_batched_fwd", *args, ws.data_ptr(), nbytes, _stream(q))
+        else:
+            N.call("bmx_seq_attention_batched_fwd", *args, _stream(q))
     return out
 
 

@@ -215,6 +215,20 @@ int bmx_seq_attention_batched_fwd(const float* q, const float* k, const float* v
                                   int64_t sq, int64_t sk, int64_t sbias, int64_t smask, int64_t bias_div, int heads,
                                   int head_dim, float inf, float* out, bmx_stream_t stream);
 
+/* bmx_seq_attention_batched_fwd with both products on bf16 MFMA, each operand split into bf16 high
+ * and low parts (x y ~ xh yh + xh yl + xl yh: about 2^-16 relative per product, the same form as the
+ * split-bf16 fp32 linears of the diffusion blocks) instead of fp32 MFMA; same arguments and result,
+ * within 1e-4 of the fp32 reference.  A pre-pass writes the split K and the split, transposed V into
+ * `workspace` (256-byte aligned, bmx_seq_attention_x3_workspace_bytes bytes).  Replaces the same
+ * part of AttentionPairBias.forward (math as src/boltz_lumi/pair_bias.py:21-36); the reference runs
+ * these products as fp32 matmuls. */
+size_t bmx_seq_attention_x3_workspace_bytes(int64_t batch, int64_t nk, int heads, int head_dim);
+int bmx_seq_attention_x3_batched_fwd(const float* q, const float* k, const float* v, const float* bias,
+                                     const float* mask, const float* g, int64_t batch, int64_t nq, int64_t nk,
+                                     int64_t ldq, int64_t ldk, int64_t sq, int64_t sk, int64_t sbias, int64_t smask,
+                                     int64_t bias_div, int heads, int head_dim, float inf, float* out,
+                                     void* workspace, size_t workspace_bytes, bmx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,10 @@ def test_workspace_queries(lib):
     assert lib.bmx_trimul_workspace_bytes(100) == 3 * 128 * 256 * 256 * 2  # planes padded to 256
     assert lib.bmx_triattn_workspace_bytes(1024) > 3 * 1024 * 1024 * 128 * 2
     assert lib.bmx_triattn_proj_rows() == 3 * 128 + 32
+    # split K (hi, lo) and split V^T (hi, lo), keys padded to the 64-key stage: 5 x 1024 x 768 -> 4 x 7.5 MiB
+    assert lib.bmx_seq_attention_x3_workspace_bytes(5, 1024, 16, 48) == 4 * 5 * 1024 * 768 * 2
+    assert lib.bmx_seq_attention_x3_workspace_bytes(1, 17, 4, 32) == 4 * 64 * 128 * 2
+    assert lib.bmx_seq_attention_x3_workspace_bytes(0, 17, 4, 32) == 0
 
 
 def test_argument_validation_needs_no_gpu(lib):
@@ -77,6 +81,14 @@ def test_argument_validation_needs_no_gpu(lib):
     rc = lib.bmx_seq_attention_fwd(None, None, None, None, None, None, 8, 100, 16, 24, 1e6, None, None)
     assert rc == N.BMX_EINVAL and b"row stride" in lib.bmx_last_error()
     assert lib.bmx_pair_bias_fold_bytes() == 2 * 4 * 64 * 8 * 2 + 16 * 4
+    # the split attention checks its workspace before anything is launched
+    fake = ctypes.c_void_p(256)
+    args = [fake] * 6 + [1, 16, 1024, 768, 768, 0, 0, 0, 0, 1, 16, 48, 1e6, fake]
+    rc = lib.bmx_seq_attention_x3_batched_fwd(*args, fake, 1024, None)
+    assert rc == N.BMX_EINVAL and b"workspace" in lib.bmx_last_error()
+    rc = lib.bmx_seq_attention_x3_batched_fwd(*args[:17], 40, 1e6, fake, fake, 1 << 30, None)
+    assert rc == N.BMX_EINVAL and b"head_dim" in lib.bmx_last_error()
+    assert lib.bmx_seq_attention_x3_batched_fwd(*args[:6], 0, *args[7:], None, 0, None) == N.BMX_OK
 
 
 def test_call_raises_with_message(lib):
