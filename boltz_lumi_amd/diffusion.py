@@ -66,12 +66,57 @@ def adaln_forward(self, a, s):
     return ops.adaln_modulate(a, _linear(self.s_scale, sn), _linear(self.s_bias, sn), self.a_norm.eps)
 
 
+def _transition_ok(block, a, s) -> bool:
+    return eligible(block, a, s) and a.shape[-1] % 4 == 0 and block.a_to_b.weight.shape[0] % 4 == 0
+
+
+def _transition_inner(block, a, s):
+    """b_to_a(b) and the output-gate logits of a ConditionedTransitionBlock."""
+    x = block.adaln(a, s)
+    b = ops.epilogue(_linear(block.swish_gate[0], x), _linear(block.a_to_b, x), None, ops.GATED_SWIGLU)
+    return _linear(block.b_to_a, b), _linear(block.output_projection[0], s)
+
+
 def transition_forward(self, a, s):
     """Drop-in for ``ConditionedTransitionBlock.forward(a, s)``.  The fused
     epilogues take widths that are multiples of 4 (every Boltz-2 width is);
     other widths run the class forward."""
-    if not eligible(self, a, s) or a.shape[-1] % 4 or self.a_to_b.weight.shape[0] % 4:
+    if not _transition_ok(self, a, s):
         return type(self).forward(self, a, s)
-    a = self.adaln(a, s)
-    b = ops.epilogue(_linear(self.swish_gate[0], a), _linear(self.a_to_b, a), None, ops.GATED_SWIGLU)
-    return ops.epilogue(_linear(self.output_projection[0], s), _linear(self.b_to_a, b), None, ops.GATE)
+    y, gate = _transition_inner(self, a, s)
+    return ops.epilogue(gate, y, None, ops.GATE)
+
+
+def _plain(module) -> bool:
+    """No forward hooks on ``module``, so a fused path may skip its call."""
+    return not (module._forward_hooks or module._forward_pre_hooks)
+
+
+def layer_forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity=1):
+    """Drop-in for ``DiffusionTransformerLayer.forward``: the attention's output
+    gate and residual add (``a + sigmoid(output_projection_linear(s)) * b``)
+    and the transition's (``a + sigmoid(gate(s)) * b_to_a(b)``) each run as one
+    MODULATION epilogue instead of separate sigmoid, multiply and add passes;
+    the product and the sum round as the eager expression does.  The
+    transition is fused only while its forward is ``transition_forward`` with
+    no hooks; otherwise ``a + transition(a, s)`` is called as is."""
+    if not (eligible(self, a, s) and a.shape == s.shape and a.shape[-1] % 4 == 0 and _plain(self.output_projection)):
+        return type(self).forward(self, a, s, bias, mask, to_keys, multiplicity)
+    b = self.adaln(a, s)
+    k_in = b
+    if to_keys is not None:
+        k_in = to_keys(b)
+        mask = to_keys(mask.unsqueeze(-1)).squeeze(-1)
+    b = self.pair_bias_attn(s=b, z=bias, mask=mask, multiplicity=multiplicity, k_in=k_in)
+    if b.shape == a.shape and b.dtype == torch.float32:
+        a = ops.epilogue(b.contiguous(), _linear(self.output_projection_linear, s), a, ops.MODULATION)
+    else:
+        a = a + self.output_projection(s) * b
+    block = self.transition
+    fwd = vars(block).get("forward")
+    if getattr(fwd, "__func__", None) is transition_forward and _plain(block) and _transition_ok(block, a, s):
+        y, gate = _transition_inner(block, a, s)
+        a = ops.epilogue(y, gate, a, ops.MODULATION)
+    else:
+        a = a + block(a, s)
+    return self.post_lnorm(a)

@@ -57,16 +57,18 @@ def test_install_patches_by_class_and_path_and_is_idempotent():
     model = Boltz2()
     n = adapters.install(model, require_device=False)
     # tri_mul_out, tri_mul_in, tri_att_start, tri_att_end, transition_z; score model: block (CTB) and its
-    # AdaLN, token-transformer layer's AdaLN, AttentionPairBias, CTB and its AdaLN; structure_module.sample
-    assert n == 12
+    # AdaLN, the token-transformer layer itself, its AdaLN, AttentionPairBias, CTB and its AdaLN;
+    # structure_module.sample
+    assert n == 13
     layer = model.pairformer_module.layers[0]
     assert "forward" in vars(layer.tri_att_start) and "forward" in vars(layer.tri_att_start.layer_norm)
     assert "forward" in vars(layer.transition_z) and "forward" not in vars(layer.transition_s)
     assert "forward" not in vars(layer.attention)  # the trunk's AttentionPairBias stays upstream
     token_layer = model.structure_module.score_model.token_transformer.layers[0]
     assert "forward" in vars(token_layer.pair_bias_attn) and "sample" in vars(model.structure_module)
+    assert "forward" in vars(token_layer)
     assert adapters.install(model, require_device=False) == 0
-    assert adapters.uninstall(model) >= 12
+    assert adapters.uninstall(model) >= 13
     assert "forward" not in vars(layer.tri_att_start) and "sample" not in vars(model.structure_module)
 
 

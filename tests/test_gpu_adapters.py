@@ -143,3 +143,50 @@ def test_diffusion_widths_off_the_kernels_fall_back(gpu):
     with torch.inference_mode():
         assert torch.equal(transition_forward(ctb, a, s), type(ctb).forward(ctb, a, s))
         assert torch.equal(adaln_forward(ctb.adaln, a, s), type(ctb.adaln).forward(ctb.adaln, a, s))
+
+
+@pytest.mark.parametrize("width,heads,n,windows", [(768, 16, 300, False), (128, 4, 256, True)])
+def test_diffusion_layer_fused_gates_match_upstream(gpu, width, heads, n, windows):
+    """An installed DiffusionTransformerLayer (token shape, and atom shape
+    with 32-query windows over 128 to_keys rows) fuses both output gates with
+    their residual adds and matches the fp32 upstream layer within 1e-4; with a
+    forward hook on its transition the layer calls ``a + transition(a, s)``
+    instead, with the same result."""
+    torch.manual_seed(41 + width)
+    ref = R.randomize(R.DiffusionTransformerLayer(heads, width, width), std=0.05).to(gpu).eval()
+    host = nn.Module()
+    host.structure_module = nn.Module()
+    host.structure_module.score_model = nn.Module()
+    host.structure_module.score_model.layer = R.DiffusionTransformerLayer(heads, width, width).to(gpu).eval()
+    layer = host.structure_module.score_model.layer
+    layer.load_state_dict(ref.state_dict())
+    assert adapters.install(host, require_boltz2=False) >= 5  # the layer, its AdaLNs, attention, transition
+    assert "forward" in vars(layer)
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(2, n, width, generator=g).to(gpu)
+    s = torch.randn(2, n, width, generator=g).to(gpu)
+    mask = torch.ones(2, n, device=gpu)
+    mask[:, -7:] = 0
+    if windows:  # as the atom transformer calls its layers: [B * N / W, W, D] windows over to_keys rows
+        nw, w, h = n // 32, 32, 128
+        index = R.get_indexing_matrix(nw, w, h, device=gpu)
+
+        def to_keys(x):
+            return R.single_to_keys(x.view(2, nw * w, -1), index, w, h).view(2 * nw, h, -1)
+
+        a, s, mask = a.view(2 * nw, w, width), s.view(2 * nw, w, width), mask.view(2 * nw, w)
+        bias = torch.randn(2 * nw, w, h, heads, generator=g).to(gpu)
+    else:
+        to_keys = None
+        bias = torch.randn(2, n, n, heads, generator=g).to(gpu)
+    with torch.inference_mode():
+        want = ref(a, s, bias, mask, to_keys)
+        got = layer(a, s, bias, mask, to_keys)
+        handle = layer.transition.register_forward_hook(lambda *args: None)
+        try:
+            hooked = layer(a, s, bias, mask, to_keys)
+        finally:
+            handle.remove()
+    assert max_rel(got, want) < 1e-4
+    assert max_rel(hooked, want) < 1e-4
+    adapters.uninstall(host)
