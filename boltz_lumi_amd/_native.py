@@ -34,6 +34,11 @@ SIGNATURES = {
     "bmx_trimul_pack": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int, c_int, _P]),
     "bmx_silu_mul": (c_int, [_P, _P, _P, c_int64, _P]),
     "bmx_split3_bf16": (c_int, [_P, c_int64, c_int64, c_int64, _P, _P]),
+    "bmx_layernorm_split3_bf16": (c_int, [_P, c_int64, c_int, c_int64, c_float, _P, _P]),
+    "bmx_adaln_split3_bf16": (c_int, [_P, _P, _P, c_int64, c_int64, c_int, c_float, _P, _P]),
+    "bmx_swiglu_split3_bf16": (c_int, [_P, c_int64, c_int64, c_int64, _P, _P]),
+    "bmx_adaln_strided": (c_int, [_P, _P, _P, c_int64, _P, c_int, c_int64, c_int, c_float, _P]),
+    "bmx_gated_residual": (c_int, [_P, _P, c_int64, _P, _P, c_int64, c_int64, _P]),
     "bmx_diffusion_epilogue": (c_int, [c_int, _P, _P, _P, _P, c_int, c_int64, c_int64, _P]),
     "bmx_bias_softmax": (c_int, [_P, _P, _P, _P, c_int, _I64P, _I64P, _I64P, _I64P, _P]),
     "bmx_trimul_workspace_bytes": (c_size_t, [c_int64]),

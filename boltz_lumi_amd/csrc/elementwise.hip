@@ -6,10 +6,8 @@
 //  bmx_trimul_pack     gate + mask -> channel-major GEMM operands (multiplication_gate_hip.cu:27-60)
 //  bmx_silu_mul        out = bf16(bf16(silu(a)) * b)              (pair_hip.cu:12-40)
 //  bmx_diffusion_epilogue  MODULATION / GATE / GATED_SWIGLU       (diffusion_hip.cu:14-66)
+//  bmx_gated_residual  MODULATION with a strided gate operand
 //  bmx_bias_softmax    softmax(round(round(s + mask) + bias))     (triangle_softmax.py:35-114)
-//  bmx_split3_bf16     x -> [bf16(x) | bf16(x) | bf16(x - bf16(x))], the activation
-//                      operand of the near-fp32 linears (no reference counterpart:
-//                      the reference runs these fp32 linears on hipBLASLt)
 #include "bmx_common.h"
 
 using namespace bmx;
@@ -121,31 +119,6 @@ __global__ __launch_bounds__(256) void silu_scalar_kernel(const bf16* __restrict
   if (i < n) out[i] = (bf16)silu_product((float)a[i], (float)b[i]);
 }
 
-// Split-bf16 operand of a near-fp32 GEMM on bf16 MFMA: row r of x (k fp32
-// values) becomes [hi | hi | lo] (3k bf16) with hi = bf16(x), lo = bf16(x - hi),
-// so that one bf16 GEMM against the weight rows [Wh | Wl | Wh] (fp32
-// accumulation) sums xh Wh + xh Wl + xl Wh: x W up to the dropped xl Wl term and
-// the residues below lo, about 2^-16 relative per product.  One thread per 4
-// columns.
-__global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ x, int64_t ldx, bf16* __restrict__ out,
-                                                     int64_t rows, int64_t k) {
-  const int64_t q = k >> 2;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= rows * q) return;
-  const int64_t row = i / q, col = (i - row * q) * 4;
-  const f32x4 v = *(const f32x4*)(x + row * ldx + col);
-  bf16x4 hi, lo;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    hi[e] = (bf16)v[e];
-    lo[e] = (bf16)(v[e] - (float)hi[e]);
-  }
-  bf16* o = out + row * 3 * k + col;
-  *(bf16x4*)o = hi;
-  *(bf16x4*)(o + k) = hi;
-  *(bf16x4*)(o + 2 * k) = lo;
-}
-
 enum Epilogue { kModulation = 0, kGate = 1, kGatedSwiGLU = 3 };
 
 // fp32/bf16 epilogues; products and sums round separately as in the eager
@@ -190,6 +163,29 @@ __global__ __launch_bounds__(256) void epilogue_kernel(const T* __restrict__ a, 
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) out[o + e] = (T)r[e];
+}
+
+// out = c + sigmoid(g) * a, the MODULATION epilogue with the gate rows at
+// stride ldg (a column slice of a wider projection); one wave per row.  out
+// may alias c (each element is read and written by the same lane).
+__global__ __launch_bounds__(256) void gated_residual_kernel(const float* __restrict__ a, const float* __restrict__ g,
+                                                             int64_t ldg, const float* c, float* out, int64_t rows,
+                                                             int64_t cols) {
+#pragma clang fp contract(off)
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  for (int64_t col = 4 * lane; col < cols; col += 4 * kWave) {
+    const int64_t o = row * cols + col;
+    const f32x4 av = load4(a + o), gv = load4(g + row * ldg + col), cv = load4(c + o);
+    f32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float prod = sigmoid_f(gv[e]) * av[e];
+      r[e] = prod + cv[e];
+    }
+    store4(out + o, r);
+  }
 }
 
 // One block (256 threads) per score row; up to 16 keys cached per thread.
@@ -303,17 +299,6 @@ int bmx_silu_mul(const void* a, const void* b, void* out, int64_t n, hipStream_t
   return check_launch("bmx_silu_mul");
 }
 
-int bmx_split3_bf16(const float* x, int64_t rows, int64_t k, int64_t ldx, void* out, hipStream_t stream) {
-  BMX_REQUIRE(rows >= 0 && k > 0 && k % 4 == 0 && ldx >= k && ldx % 4 == 0,
-              "bmx_split3_bf16: need k > 0, k %% 4 == 0, ldx >= k, ldx %% 4 == 0");
-  if (rows == 0) return BMX_OK;
-  BMX_REQUIRE(x && out, "bmx_split3_bf16: null pointer");
-  BMX_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)out % 8 == 0,
-              "bmx_split3_bf16: x must be 16-byte and out 8-byte aligned");
-  split3_kernel<<<blocks_for(rows * (k / 4), 256), 256, 0, stream>>>(x, ldx, (bf16*)out, rows, k);
-  return check_launch("bmx_split3_bf16");
-}
-
 int bmx_diffusion_epilogue(int kind, const void* a, const void* b, const void* c, void* out, int dtype,
                            int64_t rows, int64_t cols, hipStream_t stream) {
   BMX_REQUIRE(kind == kModulation || kind == kGate || kind == kGatedSwiGLU,
@@ -340,6 +325,19 @@ int bmx_diffusion_epilogue(int kind, const void* a, const void* b, const void* c
   }
 #undef EPI
   return check_launch("bmx_diffusion_epilogue");
+}
+
+int bmx_gated_residual(const float* a, const float* gate, int64_t ld_gate, const float* c, float* out, int64_t rows,
+                       int64_t cols, hipStream_t stream) {
+  BMX_REQUIRE(rows >= 0 && cols > 0 && cols % 4 == 0 && ld_gate >= cols && ld_gate % 4 == 0,
+              "bmx_gated_residual: need cols > 0, cols %% 4 == 0, ld_gate >= cols, ld_gate %% 4 == 0");
+  BMX_REQUIRE(rows < (int64_t)1 << 33, "bmx_gated_residual: too many rows");
+  if (rows == 0) return BMX_OK;
+  BMX_REQUIRE(a && gate && c && out, "bmx_gated_residual: null pointer");
+  BMX_REQUIRE(((uintptr_t)a | (uintptr_t)gate | (uintptr_t)c | (uintptr_t)out) % 16 == 0,
+              "bmx_gated_residual: operands must be 16-byte aligned");
+  gated_residual_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, stream>>>(a, gate, ld_gate, c, out, rows, cols);
+  return check_launch("bmx_gated_residual");
 }
 
 // shape = {B, I, H, Q, K}; s_strides / b_strides / m_strides are element

@@ -7,6 +7,7 @@
 //  bmx_layernorm      LN over D <= 1024 channels with optional weight / bias
 //                     (AdaLN's a_norm without affine and s_norm without bias).
 //  bmx_adaln          sigmoid(scale) * LN_noaffine(a) + shift in one pass
+//  bmx_adaln_strided  the same with scale / shift rows at a stride
 //                     (AdaLN.forward after the s_scale / s_bias GEMMs,
 //                     reference diffusion.py:52-57 + diffusion_hip.cu:14-18).
 #include "bmx_common.h"
@@ -105,9 +106,10 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const T* __restrict__ x, c
 // d <= 128 (two rows per wave, so no lane idles at the atom transformer's
 // width).  a, scale and shift are all requested before the row reductions,
 // with indices clamped into the row so that every load is unconditional.
+// scale and shift rows sit at stride ldm (d when they are dense).
 template <typename T, int LANES>
 __global__ __launch_bounds__(256) void adaln_kernel(const T* __restrict__ a, const T* __restrict__ scale,
-                                                    const T* __restrict__ shift, T* __restrict__ out,
+                                                    const T* __restrict__ shift, int64_t ldm, T* __restrict__ out,
                                                     int64_t rows, int d, float eps) {
 #pragma clang fp contract(off)
   constexpr int kPer = LANES == 64 ? kMaxChunks : 1;  // float4 chunks per lane: d <= 4 * LANES * kPer
@@ -121,8 +123,8 @@ __global__ __launch_bounds__(256) void adaln_kernel(const T* __restrict__ a, con
   for (int u = 0; u < kPer; ++u) {
     const int ch = min(l + LANES * u, chunks - 1);
     v[u] = load4(a + base + 4 * ch);
-    sc[u] = load4(scale + base + 4 * ch);
-    sh[u] = load4(shift + base + 4 * ch);
+    sc[u] = load4(scale + row * ldm + 4 * ch);
+    sh[u] = load4(shift + row * ldm + 4 * ch);
   }
   auto reduce = [](float x) { return LANES == 64 ? wave_sum_full(x) : half_sum(x); };
   float s = 0.f;
@@ -207,10 +209,11 @@ int bmx_layernorm(const void* x, const float* weight, const float* bias, float e
   return check_launch("bmx_layernorm");
 }
 
-int bmx_adaln(const void* a, const void* scale, const void* shift, void* out, int dtype, int64_t rows, int dim,
-              float eps, hipStream_t stream) {
+int bmx_adaln_strided(const void* a, const void* scale, const void* shift, int64_t ld_mod, void* out, int dtype,
+                      int64_t rows, int dim, float eps, hipStream_t stream) {
   BMX_REQUIRE(rows >= 0 && dim > 0 && dim % 4 == 0 && dim <= 1024,
               "bmx_adaln: need 0 < dim <= 1024 and dim %% 4 == 0 (got %d)", dim);
+  BMX_REQUIRE(ld_mod >= dim && ld_mod % 4 == 0, "bmx_adaln: need ld_mod >= dim and ld_mod %% 4 == 0");
   BMX_REQUIRE(dtype == kF32 || dtype == kBF16, "bmx_adaln: dtype must be fp32 or bf16");
   BMX_REQUIRE(eps > 0.f, "bmx_adaln: eps must be positive");
   if (rows == 0) return BMX_OK;
@@ -220,7 +223,7 @@ int bmx_adaln(const void* a, const void* scale, const void* shift, void* out, in
               "bmx_adaln: operands must be %d-byte aligned", align);
 #define ADALN(T, LANES)                                                                             \
   adaln_kernel<T, LANES><<<dim3((unsigned)((rows + 256 / LANES - 1) / (256 / LANES))), 256, 0, stream>>>( \
-      (const T*)a, (const T*)scale, (const T*)shift, (T*)out, rows, dim, eps)
+      (const T*)a, (const T*)scale, (const T*)shift, ld_mod, (T*)out, rows, dim, eps)
   if (dtype == kF32) {
     if (dim <= 128) ADALN(float, 32);
     else ADALN(float, 64);
@@ -230,6 +233,11 @@ int bmx_adaln(const void* a, const void* scale, const void* shift, void* out, in
   }
 #undef ADALN
   return check_launch("bmx_adaln");
+}
+
+int bmx_adaln(const void* a, const void* scale, const void* shift, void* out, int dtype, int64_t rows, int dim,
+              float eps, hipStream_t stream) {
+  return bmx_adaln_strided(a, scale, shift, dim, out, dtype, rows, dim, eps, stream);
 }
 
 }  // extern "C"

@@ -207,39 +207,166 @@ def silu_mul(a, b):
     return out
 
 
+SPLIT_TAIL = 64  # operand columns past 3 k: two ones that meet the split bias, then zeros
+
+
+def split_width(k: int) -> int:
+    """Columns of a split-bf16 operand row for ``k`` input channels."""
+    return 3 * k + SPLIT_TAIL
+
+
+def _row_stride(t) -> int:
+    """Element stride between consecutive rows of ``t`` (last axis dense, the
+    leading axes collapsing to one row index), e.g. a column slice of a wider
+    projection; raises otherwise."""
+    _check(t.dim() >= 1 and (t.shape[-1] <= 1 or t.stride(-1) == 1), "the last axis must be dense")
+    lead = [(t.shape[i], t.stride(i)) for i in range(t.dim() - 1) if t.shape[i] != 1]
+    if not lead:
+        return max(t.shape[-1], 1)
+    for (_, outer), (n, inner) in zip(lead, lead[1:]):
+        _check(outer == inner * n, "the leading axes must collapse to one row index")
+    return lead[-1][1]
+
+
+def _split_out(x, k):
+    return torch.empty(x.shape[:-1] + (split_width(k),), device=x.device, dtype=torch.bfloat16)
+
+
 def split3(x):
-    """[bf16(x) | bf16(x) | bf16(x - bf16(x))] along the last axis (``bmx_split3_bf16``), bf16 [..., 3 k]."""
+    """Split-bf16 operand of fp32 ``x`` (``bmx_split3_bf16``): bf16 [..., 3 k + 64],
+    rows [bf16(x) | bf16(x) | bf16(x - bf16(x)) | 1 1 0 ... 0].  ``x`` may be a
+    column slice (rows at a stride)."""
     _cuda(x)
-    _check(x.dtype == torch.float32 and x.is_contiguous() and x.shape[-1] % 4 == 0,
-           "expected contiguous fp32 x with a multiple of 4 columns")
+    _check(x.dtype == torch.float32 and x.shape[-1] % 4 == 0 and x.shape[-1] > 0,
+           "expected fp32 x with a positive multiple of 4 columns")
     k = x.shape[-1]
-    out = torch.empty(x.shape[:-1] + (3 * k,), device=x.device, dtype=torch.bfloat16)
-    rows = x.numel() // k if k else 0
+    out = _split_out(x, k)
+    rows = x.numel() // k
     if rows:
-        N.call("bmx_split3_bf16", x.data_ptr(), rows, k, k, out.data_ptr(), _stream(x))
+        N.call("bmx_split3_bf16", x.data_ptr(), rows, k, _row_stride(x), out.data_ptr(), _stream(x))
     return out
 
 
-def _x3_weight(w):
-    """[bf16(W) | bf16(W - bf16(W)) | bf16(W)]^T, contiguous [3 K, N] bf16, for W [N, K] fp32."""
+def layernorm_split3(x, eps):
+    """Split-bf16 operand of LayerNorm-without-affine(x) (``bmx_layernorm_split3_bf16``)."""
+    _cuda(x)
+    _check(x.dtype == torch.float32 and 0 < x.shape[-1] <= 1024 and x.shape[-1] % 4 == 0,
+           "expected fp32 x with a multiple of 4 columns, at most 1024")
+    k = x.shape[-1]
+    out = _split_out(x, k)
+    rows = x.numel() // k
+    if rows:
+        N.call("bmx_layernorm_split3_bf16", x.data_ptr(), rows, k, _row_stride(x), float(eps), out.data_ptr(),
+               _stream(x))
+    return out
+
+
+def _same_rows(a, *mods):
+    """Row stride shared by ``mods`` (column slices of one projection, or dense
+    tensors of a's shape)."""
+    _check(all(m.shape == a.shape and m.dtype == a.dtype and m.device == a.device for m in mods),
+           "shape/dtype mismatch")
+    lds = {_row_stride(m) for m in mods}
+    _check(len(lds) == 1, "the modulation operands must share one row stride")
+    return lds.pop()
+
+
+def adaln_split3(a, scale, shift, eps):
+    """Split-bf16 operand of ``sigmoid(scale) * LN_noaffine(a) + shift``
+    (``bmx_adaln_split3_bf16``); scale and shift may be column slices of one
+    wider fp32 projection (rows at one stride)."""
+    _cuda(a, scale, shift)
+    _check(a.dtype == torch.float32 and a.is_contiguous(), "expected contiguous fp32 a")
+    d = a.shape[-1]
+    _check(0 < d <= 1024 and d % 4 == 0, "expected a multiple of 4 channels, at most 1024")
+    ld = _same_rows(a, scale, shift)
+    out = _split_out(a, d)
+    rows = a.numel() // d
+    if rows:
+        N.call("bmx_adaln_split3_bf16", a.data_ptr(), scale.data_ptr(), shift.data_ptr(), ld, rows, d, float(eps),
+               out.data_ptr(), _stream(a))
+    return out
+
+
+def swiglu_split3(u, cols):
+    """Split-bf16 operand of ``silu(g) * x * b`` for rows [x | g | b | ...] of
+    fp32 ``u`` (``cols`` values each; ``bmx_swiglu_split3_bf16``)."""
+    _cuda(u)
+    _check(u.dtype == torch.float32 and cols > 0 and cols % 4 == 0 and u.shape[-1] >= 3 * cols,
+           "expected fp32 u with at least 3 cols columns, cols a multiple of 4")
+    out = torch.empty(u.shape[:-1] + (split_width(cols),), device=u.device, dtype=torch.bfloat16)
+    rows = u.numel() // u.shape[-1]
+    if rows:
+        N.call("bmx_swiglu_split3_bf16", u.data_ptr(), _row_stride(u), rows, cols, out.data_ptr(), _stream(u))
+    return out
+
+
+def gated_residual(a, gate, c, out=None):
+    """``c + sigmoid(gate) * a`` (fp32, ``bmx_gated_residual``; the MODULATION
+    epilogue) with ``gate`` possibly a column slice of a wider projection;
+    ``out`` may be ``c``."""
+    _cuda(a, gate, c)
+    _check(a.dtype == gate.dtype == c.dtype == torch.float32, "expected fp32 operands")
+    _check(a.is_contiguous() and c.is_contiguous() and a.shape == c.shape == gate.shape, "shape mismatch")
+    if out is None:
+        out = torch.empty_like(a)
+    _check(out.shape == a.shape and out.is_contiguous() and out.dtype == torch.float32, "bad out")
+    cols = a.shape[-1]
+    rows = a.numel() // cols if cols else 0
+    if rows:
+        N.call("bmx_gated_residual", a.data_ptr(), gate.data_ptr(), _row_stride(gate), c.data_ptr(), out.data_ptr(),
+               rows, cols, _stream(a))
+    return out
+
+
+def _x3_weight(w, b=None):
+    """Weight rows [Wh | Wl | Wh | bh bl 0 ... 0] (Wh = bf16(W), Wl = bf16(W - Wh),
+    likewise for the bias), bf16 [N, 3 K + 64], for W [N, K] and bias b [N] or None."""
     w = w.detach().float()
     hi = w.to(torch.bfloat16)
     lo = (w - hi.float()).to(torch.bfloat16)
-    return torch.cat([hi, lo, hi], dim=1).t().contiguous()
+    tail = torch.zeros(w.shape[0], SPLIT_TAIL, device=w.device, dtype=torch.bfloat16)
+    if b is not None:
+        b = b.detach().float()
+        bh = b.to(torch.bfloat16)
+        tail[:, 0] = bh
+        tail[:, 1] = (b - bh.float()).to(torch.bfloat16)
+    return torch.cat([hi, lo, hi, tail], dim=1)
 
 
-def x3_weight(module, name, *weights):
-    """Split weight of ``mm_x3`` for the row concatenation of ``weights``
-    ([N_i, K] each), cached on ``module`` under ``name``."""
-    return cached_weight(module, name, weights, lambda *ws: _x3_weight(torch.cat(ws, 0)))
+def x3_weight(module, name, weights, biases=None):
+    """Split weight of ``mm_split`` for the row concatenation of ``weights``
+    ([N_i, K] each) with the biases ``biases`` (one per weight, None for none),
+    cached on ``module`` under ``name``."""
+    weights = tuple(weights)
+    biases = tuple(biases) if biases is not None else (None,) * len(weights)
+    _check(len(biases) == len(weights), "one bias (or None) per weight")
+    present = tuple(b for b in biases if b is not None)
+
+    def build(*srcs):
+        ws = srcs[:len(weights)]
+        b = None
+        if present:
+            it = iter(srcs[len(weights):])
+            b = torch.cat([next(it).detach().float() if bb is not None else w.new_zeros(w.shape[0], dtype=torch.float32)
+                           for bb, w in zip(biases, ws)])
+        return _x3_weight(torch.cat(ws, 0), b)
+
+    return cached_weight(module, name, weights + present, build)
+
+
+def mm_split(op, w3):
+    """``x @ W^T + b`` from the split operand ``op`` of x ([M, 3 K + 64] bf16)
+    and ``w3 = x3_weight(..W.., ..b..)``: one hipBLASLt bf16 GEMM with fp32
+    accumulation (x W + b up to about 2^-16 relative per product); fp32 [M, N]."""
+    _check(op.dim() == 2 and op.shape[1] == w3.shape[1], "operand does not match the split weight")
+    return torch.mm(op, w3.t(), out_dtype=torch.float32)
 
 
 def mm_x3(x, w3):
-    """``x @ W^T`` for fp32 x [M, K] and ``w3 = x3_weight(..W..)``: one hipBLASLt
-    bf16 GEMM with fp32 accumulation of ``split3(x)`` against the split weight
-    (x W ~ xh Wh + xh Wl + xl Wh, about 2^-16 relative per product); fp32 [M, N]."""
-    _check(x.dim() == 2 and w3.shape[0] == 3 * x.shape[1], "x does not match the split weight")
-    return torch.mm(split3(x.float().contiguous()), w3, out_dtype=torch.float32)
+    """``mm_split(split3(x), w3)`` for fp32 x [M, K]."""
+    _check(x.dim() == 2 and w3.shape[1] == split_width(x.shape[1]), "x does not match the split weight")
+    return mm_split(split3(x.float()), w3)
 
 
 # Narrower fp32 linears (the atom transformer's 128 / 256) measured faster on
@@ -273,15 +400,13 @@ def linear_fp32(x, linear):
 
 
 def linear_x3(x, linear):
-    """``linear(x)`` for fp32 x through ``mm_x3``; the bias, if any, is added in fp32."""
+    """``linear(x)`` for fp32 x through ``mm_x3``, the bias folded into the GEMM."""
     _cuda(x)
     k = x.shape[-1]
     _check(linear.weight.shape[1] == k, "x does not match the linear's input width")
-    w = x3_weight(linear, "x3", linear.weight)
+    w = x3_weight(linear, "x3", (linear.weight,), (linear.bias,))
     y = mm_x3(x.reshape(-1, k), w)
-    if linear.bias is not None:
-        y += linear.bias.float()
-    return y.view(x.shape[:-1] + (w.shape[1],))
+    return y.view(x.shape[:-1] + (w.shape[0],))
 
 
 MODULATION, GATE, GATED_SWIGLU = 0, 1, 3
@@ -621,14 +746,16 @@ def seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=1, out=None, spl
 
 
 def adaln_modulate(a, scale, shift, eps):
-    """``sigmoid(scale) * LN_noaffine(a) + shift`` in one pass."""
+    """``sigmoid(scale) * LN_noaffine(a) + shift`` in one pass; scale and shift
+    may be column slices of one wider projection (rows at one stride,
+    ``bmx_adaln_strided``)."""
     _cuda(a, scale, shift)
-    _check(a.shape == scale.shape == shift.shape and a.dtype == scale.dtype == shift.dtype, "shape/dtype mismatch")
-    _check(a.is_contiguous() and scale.is_contiguous() and shift.is_contiguous(), "expected contiguous inputs")
+    _check(a.is_contiguous(), "expected contiguous a")
+    ld = _same_rows(a, scale, shift)
     d = a.shape[-1]
     out = torch.empty_like(a)
     rows = a.numel() // d if d else 0
     if rows:
-        N.call("bmx_adaln", a.data_ptr(), scale.data_ptr(), shift.data_ptr(), out.data_ptr(), _code(a.dtype), rows,
-               d, float(eps), _stream(a))
+        N.call("bmx_adaln_strided", a.data_ptr(), scale.data_ptr(), shift.data_ptr(), ld, out.data_ptr(),
+               _code(a.dtype), rows, d, float(eps), _stream(a))
     return out

@@ -42,17 +42,15 @@ def _joint_projection(module, name, x, linears):
     autocast, else fp32 (split-bf16 from ``ops.X3_MIN_K`` input channels up)."""
     weights = tuple(lin.weight for lin in linears)
     biases = [lin.bias for lin in linears]
+    if not torch.is_autocast_enabled() and x.shape[-1] >= ops.X3_MIN_K and x.shape[-1] % 4 == 0:
+        y = ops.mm_x3(x.reshape(-1, x.shape[-1]), ops.x3_weight(module, name + "_x3", weights, biases))
+        return y.view(x.shape[:-1] + (y.shape[-1],))
     bias = None
     if any(b is not None for b in biases):
         srcs = tuple(b for b in biases if b is not None)
         bias = ops.cached_weight(module, name + "_bias", srcs, lambda *bs: torch.cat(
             [b.float() if b is not None else lin.weight.new_zeros(lin.out_features, dtype=torch.float32)
              for b, lin in zip(biases, linears)]))
-    if not torch.is_autocast_enabled() and x.shape[-1] >= ops.X3_MIN_K and x.shape[-1] % 4 == 0:
-        y = ops.mm_x3(x.reshape(-1, x.shape[-1]), ops.x3_weight(module, name + "_x3", *weights))
-        if bias is not None:
-            y += bias
-        return y.view(x.shape[:-1] + (y.shape[-1],))
     w = ops.cached_weight(module, name, weights, lambda *ws: torch.cat(ws, 0).float())
     return F.linear(x if torch.is_autocast_enabled() else x.float(), w, bias).float()
 
@@ -78,13 +76,14 @@ def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
     batch, nq, nk = s.shape[0], s.shape[1], k_in.shape[1]
     if k_in is s:
         weights = (module.proj_q.weight, module.proj_k.weight, module.proj_v.weight, module.proj_g.weight)
-        bq = ops.cached_weight(module, "qkvg_bias", (module.proj_q.bias,),
-                               lambda b: torch.cat([b.float(), b.new_zeros(3 * width)]))
         if not torch.is_autocast_enabled() and width >= ops.X3_MIN_K and width % 4 == 0:
             # fp32 at the token transformer's width: one split-bf16 GEMM with fp32 accumulation
-            proj = ops.mm_x3(s.reshape(-1, width), ops.x3_weight(module, "qkvg_x3", *weights)).add_(bq)
+            biases = (module.proj_q.bias, module.proj_k.bias, module.proj_v.bias, module.proj_g.bias)
+            proj = ops.mm_x3(s.reshape(-1, width), ops.x3_weight(module, "qkvg_x3", weights, biases))
             proj = proj.view(s.shape[:-1] + (4 * width,))
         else:
+            bq = ops.cached_weight(module, "qkvg_bias", (module.proj_q.bias,),
+                                   lambda b: torch.cat([b.float(), b.new_zeros(3 * width)]))
             w = ops.cached_weight(module, "qkvg", weights, lambda *ws: torch.cat(ws, 0).float())
             proj = F.linear(s if torch.is_autocast_enabled() else s.float(), w, bq).float()
         q, k, v, g = proj.split(width, dim=-1)

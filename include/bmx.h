@@ -52,6 +52,11 @@ int bmx_layernorm(const void* x, const float* weight, const float* bias, float e
 int bmx_adaln(const void* a, const void* scale, const void* shift, void* out, int dtype, int64_t rows, int dim,
               float eps, bmx_stream_t stream);
 
+/* bmx_adaln with the scale / shift rows at stride ld_mod (ld_mod >= dim, multiple of 4): column
+ * slices of one conditioning projection shared by the layers of a diffusion transformer. */
+int bmx_adaln_strided(const void* a, const void* scale, const void* shift, int64_t ld_mod, void* out, int dtype,
+                      int64_t rows, int dim, float eps, bmx_stream_t stream);
+
 /* ---- Elementwise operators (reference's unfused operator set) ---------- */
 
 /* out = bf16(x * bf16(sigmoid(g))), bf16.
@@ -78,13 +83,40 @@ int bmx_silu_mul(const void* a, const void* b, void* out, int64_t n, bmx_stream_
 int bmx_diffusion_epilogue(int kind, const void* a, const void* b, const void* c, void* out, int dtype, int64_t rows,
                            int64_t cols, bmx_stream_t stream);
 
-/* out[r] = [bf16(x[r]) | bf16(x[r]) | bf16(x[r] - bf16(x[r]))] (3k bf16 per row) for rows of k fp32
- * values at row stride ldx (k and ldx multiples of 4; x 16-byte, out 8-byte aligned).  The activation
- * operand of the near-fp32 linears: one bf16 GEMM of this against the weight rows
- * [bf16(W) | bf16(W - bf16(W)) | bf16(W)] with fp32 accumulation gives x W up to about 2^-16 relative
- * per product.  No reference counterpart: it serves fp32 linears that the reference leaves to
- * hipBLASLt (the conditioned transition's a-path projections, diffusion.py:60-68). */
+/* out = c + sigmoid(gate) * a (the MODULATION epilogue, fp32) with the gate rows at stride
+ * ld_gate; out may alias c.  The output gate and residual add of a diffusion transformer
+ * layer, a + sigmoid(output_projection_linear(s)) * b (transformersv2; diffusion.py:60-68). */
+int bmx_gated_residual(const float* a, const float* gate, int64_t ld_gate, const float* c, float* out, int64_t rows,
+                       int64_t cols, bmx_stream_t stream);
+
+/* ---- Split-bf16 operands of the near-fp32 linears ---------------------
+ * The diffusion blocks' fp32 linears (the reference leaves them to hipBLASLt in fp32:
+ * diffusion.py:52-68, pair_bias.py:15-36; no reference counterpart) run as one bf16 GEMM
+ * with fp32 accumulation of an operand row of kp = 3k + 64 bf16,
+ *     [bf16(x) | bf16(x) | bf16(x - bf16(x)) | 1 1 0 ... 0],
+ * against the weight row [Wh | Wl | Wh | bh bl 0 ... 0] (Wh = bf16(W), Wl = bf16(W - Wh),
+ * likewise for the bias): x W + b up to about 2^-16 relative per product.  Operands are
+ * written dense at row stride kp; inputs are fp32, 16-byte aligned; out 8-byte aligned. */
+
+/* Operand rows of x (rows of k values at row stride ldx; k, ldx multiples of 4). */
 int bmx_split3_bf16(const float* x, int64_t rows, int64_t k, int64_t ldx, void* out, bmx_stream_t stream);
+
+/* Operand rows of LayerNorm-without-affine(x) (dim <= 1024, dim % 4 == 0): the s_norm input of
+ * every AdaLN of a diffusion transformer, whose LayerNorm weight the caller folds into the
+ * s_scale / s_bias weights (AdaLN.forward, transformersv2; diffusion.py:52-57). */
+int bmx_layernorm_split3_bf16(const float* x, int64_t rows, int dim, int64_t ldx, float eps, void* out,
+                              bmx_stream_t stream);
+
+/* Operand rows of sigmoid(scale) * LN_noaffine(a) + shift (rounded as bmx_adaln), a dense
+ * [rows][dim], scale / shift rows at stride ld_mod: the AdaLN output that feeds the
+ * attention's q|k|v|g and the transition's swish_gate|a_to_b projections (diffusion.py:52-68). */
+int bmx_adaln_split3_bf16(const float* a, const float* scale, const float* shift, int64_t ld_mod, int64_t rows,
+                          int dim, float eps, void* out, bmx_stream_t stream);
+
+/* Operand rows of silu(g) * x * b (rounded as the GATED_SWIGLU epilogue) where row r of u
+ * holds [x | g | b] of cols values each at stride ldu: the conditioned transition's b from
+ * one swish_gate|a_to_b projection, the input of b_to_a (diffusion.py:60-68). */
+int bmx_swiglu_split3_bf16(const float* u, int64_t ldu, int64_t rows, int64_t cols, void* out, bmx_stream_t stream);
 
 /* P = softmax(round(round(S + mask) + bias)) over the last axis, rounding to dtype.
  * shape = {B, I, H, Q, K}; element strides of scores [B,I,H,Q,K], bias [B,1,H,Q,K], mask [B,I,1,1,K].

@@ -89,6 +89,22 @@ def test_argument_validation_needs_no_gpu(lib):
     rc = lib.bmx_seq_attention_x3_batched_fwd(*args[:17], 40, 1e6, fake, fake, 1 << 30, None)
     assert rc == N.BMX_EINVAL and b"head_dim" in lib.bmx_last_error()
     assert lib.bmx_seq_attention_x3_batched_fwd(*args[:6], 0, *args[7:], None, 0, None) == N.BMX_OK
+    # split-bf16 operand writers and the strided modulation kernels
+    assert lib.bmx_split3_bf16(None, 0, 768, 768, None, None) == N.BMX_OK
+    rc = lib.bmx_split3_bf16(fake, 4, 768, 700, fake, None)
+    assert rc == N.BMX_EINVAL and b"ldx >= k" in lib.bmx_last_error()
+    rc = lib.bmx_layernorm_split3_bf16(fake, 4, 1028, 1028, ctypes.c_float(1e-5), fake, None)
+    assert rc == N.BMX_EINVAL and b"dim <= 1024" in lib.bmx_last_error()
+    rc = lib.bmx_adaln_split3_bf16(fake, fake, fake, 512, 4, 768, ctypes.c_float(1e-5), fake, None)
+    assert rc == N.BMX_EINVAL and b"ld_mod >= dim" in lib.bmx_last_error()
+    rc = lib.bmx_adaln_split3_bf16(fake, ctypes.c_void_p(260), fake, 768, 4, 768, ctypes.c_float(1e-5), fake, None)
+    assert rc == N.BMX_EINVAL and b"aligned" in lib.bmx_last_error()
+    rc = lib.bmx_swiglu_split3_bf16(fake, 2000, 4, 768, fake, None)
+    assert rc == N.BMX_EINVAL and b"ldu >= 3 cols" in lib.bmx_last_error()
+    rc = lib.bmx_adaln_strided(fake, fake, fake, 100, fake, 0, 4, 128, ctypes.c_float(1e-5), None)
+    assert rc == N.BMX_EINVAL and b"ld_mod" in lib.bmx_last_error()
+    rc = lib.bmx_gated_residual(fake, fake, 768, None, fake, 4, 768, None)
+    assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
 
 
 def test_call_raises_with_message(lib):

@@ -215,5 +215,8 @@ def test_linear_x3_is_near_fp32(gpu, m, k, n, bias):
     assert got.dtype == torch.float32 and got.shape == want.shape
     assert errors(got, want)["max_rel"] < 2e-5
     hi = x[0].bfloat16()
-    assert torch.equal(split[:, :k].cpu(), hi) and torch.equal(split[:, k:2 * k].cpu(), hi)
-    assert torch.equal(split[:, 2 * k:].cpu(), (x[0] - hi.float()).bfloat16())
+    split = split.cpu()
+    assert split.shape == (m, 3 * k + 64)
+    assert torch.equal(split[:, :k], hi) and torch.equal(split[:, k:2 * k], hi)
+    assert torch.equal(split[:, 2 * k:3 * k], (x[0] - hi.float()).bfloat16())
+    assert (split[:, 3 * k:3 * k + 2] == 1).all() and (split[:, 3 * k + 2:] == 0).all()
