@@ -19,8 +19,12 @@ Patched (class name, path rule -> replacement):
       (the reference patches the token transformer's only, adapters.py:39-42;
       the atom transformer's windowed ones run on the same fused kernel here)
   DiffusionTransformerLayer under
-      "structure_module.score_model."              -> diffusion.layer_forward (output gates and
-      residual adds fused; beyond the reference, which leaves the layer upstream)
+      "structure_module.score_model."              -> diffusion.layer_forward (conditioning
+      projections as two GEMMs, output gates and residual adds fused; beyond the
+      reference, which leaves the layer upstream)
+  DiffusionTransformer under
+      "structure_module.score_model."              -> diffusion.stack_forward (operands of s
+      built once per stack call; beyond the reference)
   structure_module.sample                          -> diffusion.optimized_sample
 """
 
@@ -56,7 +60,7 @@ def install(model, *, require_boltz2: bool = True, require_device: bool = True):
     from . import _native
 
     _native.lib()  # fail loudly here, not inside the first forward
-    from .diffusion import adaln_forward, layer_forward, optimized_sample, transition_forward
+    from .diffusion import adaln_forward, layer_forward, optimized_sample, stack_forward, transition_forward
     from .multiplication import normalized_forward
     from .pair_bias import prepared_forward
     from .pair_transition import transition_forward as pair_transition_forward
@@ -88,6 +92,9 @@ def install(model, *, require_boltz2: bool = True, require_device: bool = True):
             patched += 1
         elif name.startswith(SCORE_MODEL) and cls == "DiffusionTransformerLayer":
             module.forward = MethodType(layer_forward, module)
+            patched += 1
+        elif name.startswith(SCORE_MODEL) and cls == "DiffusionTransformer":
+            module.forward = MethodType(stack_forward, module)
             patched += 1
     structure = getattr(model, "structure_module", None)
     if structure is not None and hasattr(type(structure), "sample"):

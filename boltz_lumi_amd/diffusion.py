@@ -92,16 +92,157 @@ def _plain(module) -> bool:
     return not (module._forward_hooks or module._forward_pre_hooks)
 
 
-def layer_forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity=1):
-    """Drop-in for ``DiffusionTransformerLayer.forward``: the attention's output
-    gate and residual add (``a + sigmoid(output_projection_linear(s)) * b``)
-    and the transition's (``a + sigmoid(gate(s)) * b_to_a(b)``) each run as one
-    MODULATION epilogue instead of separate sigmoid, multiply and add passes;
-    the product and the sum round as the eager expression does.  The
-    transition is fused only while its forward is ``transition_forward`` with
-    no hooks; otherwise ``a + transition(a, s)`` is called as is."""
-    if not (eligible(self, a, s) and a.shape == s.shape and a.shape[-1] % 4 == 0 and _plain(self.output_projection)):
-        return type(self).forward(self, a, s, bias, mask, to_keys, multiplicity)
+def _untouched(module) -> bool:
+    """No hooks and no instance-level forward (such as the memo of
+    ``atom_conditioning_cache``), so its math may be folded elsewhere."""
+    return _plain(module) and "forward" not in vars(module)
+
+
+def _patched_with(module, func) -> bool:
+    return getattr(vars(module).get("forward"), "__func__", None) is func
+
+
+def _adaln_foldable(adaln, c) -> bool:
+    """AdaLN whose s-side (s_norm, s_scale, s_bias) may run as one projection
+    of LayerNorm-without-affine(s) with the s_norm affine folded into the
+    weights: an a_norm without affine, an s_norm over the c channels, nothing
+    hooked or memoised."""
+    fwd = vars(adaln).get("forward")
+    an, sn = adaln.a_norm, adaln.s_norm
+    return (_plain(adaln) and (fwd is None or getattr(fwd, "__func__", None) is adaln_forward)
+            and isinstance(an, torch.nn.LayerNorm) and an.weight is None and an.bias is None
+            and isinstance(sn, torch.nn.LayerNorm) and tuple(sn.normalized_shape) == (c,)
+            and all(_untouched(m) for m in (sn, adaln.s_scale, adaln.s_bias)))
+
+
+def _side_ok(layer, a, s) -> bool:
+    """The whole layer may run with its conditioning projections as two GEMMs
+    on operands of s shared by the stack (``_Side``)."""
+    c = s.shape[-1]
+    tr = layer.transition
+    return (a.shape[-1] <= 1024 and _adaln_foldable(layer.adaln, c) and _adaln_foldable(tr.adaln, c)
+            and _untouched(layer.output_projection_linear) and _plain(layer.output_projection)
+            and _patched_with(tr, transition_forward) and _plain(tr) and _plain(tr.output_projection)
+            and _untouched(tr.output_projection[0]) and _transition_ok(tr, a, s))
+
+
+class _Side:
+    """Operands of the conditioning projections built from ``s`` once per
+    stack call: LayerNorm-without-affine(s) (every AdaLN's s_norm, whose
+    affine is folded into the projection weights; one per eps) and s itself.
+    Split-bf16 operands where the linears run split (``ops.use_split``), else
+    fp32 rows."""
+
+    def __init__(self, s):
+        self.s = s.reshape(-1, s.shape[-1])
+        self.split = ops.use_split(s.shape[-1])
+        self._norm = {}
+        self._raw = None
+
+    def norm(self, eps):
+        if eps not in self._norm:
+            self._norm[eps] = (ops.layernorm_split3(self.s, eps) if self.split
+                               else ops.layer_norm(self.s, None, None, eps))
+        return self._norm[eps]
+
+    def raw(self):
+        if self._raw is None:
+            self._raw = ops.split3(self.s) if self.split else self.s
+        return self._raw
+
+
+def _folded(adaln):
+    """[s_scale; s_bias] (weight [2 d, c], bias [2 d]) acting on
+    LayerNorm-without-affine(s): s_scale(LN(s) w + b) = LN(s) (W diag(w)) + W b + bias."""
+    lins = (adaln.s_scale, adaln.s_bias)
+    w = torch.cat([lin.weight.detach().float() for lin in lins])
+    b = torch.cat([lin.bias.detach().float() if lin.bias is not None
+                   else w.new_zeros(lin.out_features) for lin in lins])
+    sn = adaln.s_norm
+    if sn.bias is not None:
+        b = b + w @ sn.bias.detach().float()
+    if sn.weight is not None:
+        w = w * sn.weight.detach().float()
+    return w, b
+
+
+def _mods_sources(layer):
+    out = []
+    for adaln in (layer.adaln, layer.transition.adaln):
+        for m in (adaln.s_norm, adaln.s_scale, adaln.s_bias):
+            out += [p for p in (m.weight, m.bias) if p is not None]
+    return tuple(out)
+
+
+def _gate_linears(layer):
+    return (layer.output_projection_linear, layer.transition.output_projection[0])
+
+
+def _conditioning(layer, side, eps):
+    """(mods [M, 4 d], gates [M, 2 d]) of one layer: the attention AdaLN's
+    scale | shift and the transition AdaLN's scale | shift from LN(s), and the
+    two output-gate logits from s, as two GEMMs (split-bf16 or fp32, the
+    biases and s_norm affines folded in)."""
+    gl = _gate_linears(layer)
+    gw = tuple(lin.weight for lin in gl)
+    gb = tuple(lin.bias for lin in gl)
+    if side.split:
+        wm = ops.cached_weight(layer, "cond_mods_x3", _mods_sources(layer), lambda *_: ops._x3_weight(
+            *(torch.cat(t) for t in zip(_folded(layer.adaln), _folded(layer.transition.adaln)))))
+        mods = ops.mm_split(side.norm(eps), wm)
+        gates = ops.mm_split(side.raw(), ops.x3_weight(layer, "cond_gates_x3", gw, gb))
+        return mods, gates
+    wm = ops.cached_weight(layer, "cond_mods_w", _mods_sources(layer), lambda *_: torch.cat(
+        [_folded(layer.adaln)[0], _folded(layer.transition.adaln)[0]]))
+    bm = ops.cached_weight(layer, "cond_mods_b", _mods_sources(layer), lambda *_: torch.cat(
+        [_folded(layer.adaln)[1], _folded(layer.transition.adaln)[1]]))
+    wg = ops.cached_weight(layer, "cond_gates_w", gw, lambda *ws: torch.cat(ws).float())
+    bg = ops.cached_weight(layer, "cond_gates_b", tuple(b for b in gb if b is not None), lambda *_: torch.cat(
+        [lin.bias.detach().float() if lin.bias is not None else lin.weight.new_zeros(lin.out_features,
+                                                                                        dtype=torch.float32)
+         for lin in gl]))
+    return (torch.nn.functional.linear(side.norm(eps), wm, bm),
+            torch.nn.functional.linear(side.raw(), wg, bg))
+
+
+def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity):
+    d = a.shape[-1]
+    tr = self.transition
+    eps = self.adaln.s_norm.eps
+    if tr.adaln.s_norm.eps != eps:
+        return _layer_per_linear(self, a, s, bias, mask, to_keys, multiplicity)
+    mods, gates = _conditioning(self, side, eps)
+    scale_a, shift_a, scale_t, shift_t = mods.split(d, dim=-1)
+    gate_a, gate_t = gates.split(d, dim=-1)
+    rows = a.reshape(-1, d)
+    b = ops.adaln_modulate(rows, scale_a, shift_a, self.adaln.a_norm.eps).view(a.shape)
+    k_in = b
+    if to_keys is not None:
+        k_in = to_keys(b)
+        mask = to_keys(mask.unsqueeze(-1)).squeeze(-1)
+    b = self.pair_bias_attn(s=b, z=bias, mask=mask, multiplicity=multiplicity, k_in=k_in)
+    if b.shape == a.shape and b.dtype == torch.float32:
+        rows = ops.gated_residual(b.reshape(-1, d).contiguous(), gate_a, rows)
+    else:
+        rows = (a + torch.sigmoid(gate_a).reshape(a.shape) * b).reshape(-1, d)
+    t_eps = tr.adaln.a_norm.eps
+    if side.split:
+        u = ops.mm_split(ops.adaln_split3(rows, scale_t, shift_t, t_eps), ops.x3_weight(
+            tr, "swish_a2b_x3", (tr.swish_gate[0].weight, tr.a_to_b.weight), (tr.swish_gate[0].bias, tr.a_to_b.bias)))
+        b2a = tr.b_to_a
+        y = ops.mm_split(ops.swiglu_split3(u, tr.a_to_b.out_features),
+                         ops.x3_weight(b2a, "x3", (b2a.weight,), (b2a.bias,)))
+    else:
+        x = ops.adaln_modulate(rows, scale_t, shift_t, t_eps)
+        y = _linear(tr.b_to_a, ops.epilogue(_linear(tr.swish_gate[0], x), _linear(tr.a_to_b, x), None,
+                                            ops.GATED_SWIGLU))
+    rows = ops.gated_residual(y.reshape(rows.shape), gate_t, rows, out=rows)
+    return self.post_lnorm(rows.view(a.shape))
+
+
+def _layer_per_linear(self, a, s, bias, mask, to_keys, multiplicity):
+    """The layer with each conditioning projection called on its own (memoised
+    or hooked projections keep their behaviour); output gates fused."""
     b = self.adaln(a, s)
     k_in = b
     if to_keys is not None:
@@ -113,10 +254,55 @@ def layer_forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity=1
     else:
         a = a + self.output_projection(s) * b
     block = self.transition
-    fwd = vars(block).get("forward")
-    if getattr(fwd, "__func__", None) is transition_forward and _plain(block) and _transition_ok(block, a, s):
+    if _patched_with(block, transition_forward) and _plain(block) and _transition_ok(block, a, s):
         y, gate = _transition_inner(block, a, s)
         a = ops.epilogue(y, gate, a, ops.MODULATION)
     else:
         a = a + block(a, s)
     return self.post_lnorm(a)
+
+
+def _layer(self, a, s, bias, mask, to_keys, multiplicity, side):
+    if not (eligible(self, a, s) and a.shape == s.shape and a.shape[-1] % 4 == 0 and _plain(self.output_projection)):
+        return type(self).forward(self, a, s, bias, mask, to_keys, multiplicity)
+    if _side_ok(self, a, s):
+        return _layer_with_side(self, a, s, side if side is not None else _Side(s), bias, mask, to_keys,
+                                multiplicity)
+    return _layer_per_linear(self, a, s, bias, mask, to_keys, multiplicity)
+
+
+def layer_forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity=1):
+    """Drop-in for ``DiffusionTransformerLayer.forward``.
+
+    With nothing hooked or memoised on the conditioning path, the layer's six
+    conditioning projections (both AdaLNs' s_scale / s_bias after s_norm, both
+    output gates) run as two GEMMs, one on LayerNorm-without-affine(s) with the
+    s_norm affines folded into the weights and one on s; the AdaLN
+    modulations, the transition's swish_gate | a_to_b projection and SwiGLU,
+    and both output gates with their residual adds
+    (``a + sigmoid(gate) * b``) read column slices of those projections.  In
+    split-bf16 mode the AdaLN and SwiGLU passes write the split operands of
+    the next GEMM directly.  Otherwise (memoised or hooked projections, a
+    transition forward other than ``transition_forward``) each projection is
+    called on its own and only the gates are fused; off the kernels' domain the
+    class forward runs."""
+    return _layer(self, a, s, bias, mask, to_keys, multiplicity, None)
+
+
+def stack_forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity=1):
+    """Drop-in for ``DiffusionTransformer.forward`` (upstream transformersv2):
+    the same per-layer loop, with the layers' operands of s built once per
+    call and shared (``_Side``).  Upstream runs when a layer is not patched
+    with ``layer_forward`` or is hooked, in training and under grad."""
+    layers = list(self.layers)
+    if not (inference(self) and layers and all(_patched_with(l, layer_forward) and _plain(l) for l in layers)
+            and eligible(self, a, s)):
+        return type(self).forward(self, a, s, bias, mask, to_keys, multiplicity)
+    if getattr(self, "pair_bias_attn", True):
+        n_b, n, m, d = bias.shape
+        bias = bias.view(n_b, n, m, len(layers), d // len(layers))
+    side = _Side(s)
+    for i, layer in enumerate(layers):
+        bias_l = bias[:, :, :, i] if getattr(self, "pair_bias_attn", True) else None
+        a = _layer(layer, a, s, bias_l, mask, to_keys, multiplicity, side)
+    return a

@@ -389,12 +389,16 @@ def exact_fp32_linears(enabled: bool = True) -> bool:
     return before
 
 
+def use_split(k: int) -> bool:
+    """Whether fp32 linears of ``k`` input channels run as split-bf16 GEMMs."""
+    return not _EXACT_FP32[0] and k >= X3_MIN_K and k % 4 == 0
+
+
 def linear_fp32(x, linear):
     """``linear(x)`` for fp32 x: ``linear_x3`` for input widths >= X3_MIN_K
     (multiples of 4) unless exact fp32 linears are switched on, else the fp32
     GEMM."""
-    k = x.shape[-1]
-    if not _EXACT_FP32[0] and k >= X3_MIN_K and k % 4 == 0:
+    if use_split(x.shape[-1]):
         return linear_x3(x, linear)
     return torch.nn.functional.linear(x, linear.weight, linear.bias)
 

@@ -6,13 +6,14 @@ the other pair modules fall back to the upstream forward bit for bit, as does
 grad mode; the diffusion blocks run natively in fp32 within 1e-4; the
 conditioning cache computes each projection once."""
 
+import copy
 from types import SimpleNamespace
 
 import pytest
 import torch
 from torch import nn
 
-from boltz_lumi_amd import adapters
+from boltz_lumi_amd import adapters, ops
 from boltz_lumi_amd.atom_conditioning import atom_conditioning_cache
 from oracle import boltz_ref as R
 
@@ -189,4 +190,69 @@ def test_diffusion_layer_fused_gates_match_upstream(gpu, width, heads, n, window
             handle.remove()
     assert max_rel(got, want) < 1e-4
     assert max_rel(hooked, want) < 1e-4
+    adapters.uninstall(host)
+
+
+@pytest.mark.parametrize("width,heads,n,windows", [(768, 16, 300, False), (128, 4, 256, True)])
+def test_diffusion_stack_shared_conditioning_matches_upstream(gpu, width, heads, n, windows):
+    """An installed DiffusionTransformer (3 layers; token shape, and atom shape
+    with windows over to_keys rows) builds the operands of s once and runs each
+    layer's six conditioning projections as two GEMMs with the s_norm affine
+    folded into the weights; it matches the fp32 upstream stack within 1e-4.
+    Covered on the way: an s_norm with a bias (folded as W b), a layer whose
+    s_scale has an instance forward (a memo: that layer calls its projections
+    one by one), and exact fp32 linears at the token width."""
+    torch.manual_seed(43 + width)
+    depth = 3
+    ref = R.DiffusionTransformer(depth, heads, width, width)
+    ref.layers[1].adaln.s_norm = nn.LayerNorm(width)  # affine with a bias
+    ref = R.randomize(ref, std=0.05).to(gpu).eval()
+    host = nn.Module()
+    host.structure_module = nn.Module()
+    host.structure_module.score_model = nn.Module()
+    host.structure_module.score_model.stack = copy.deepcopy(ref)
+    stack = host.structure_module.score_model.stack
+    assert adapters.install(host, require_boltz2=False) == 5 * depth + 1
+    assert "forward" in vars(stack)
+    g = torch.Generator().manual_seed(9)
+    a = torch.randn(2, n, width, generator=g).to(gpu)
+    s = torch.randn(2, n, width, generator=g).to(gpu)
+    mask = torch.ones(2, n, device=gpu)
+    mask[:, -5:] = 0
+    if windows:
+        nw, w, h = n // 32, 32, 128
+        index = R.get_indexing_matrix(nw, w, h, device=gpu)
+
+        def to_keys(x):
+            return R.single_to_keys(x.view(2, nw * w, -1), index, w, h).view(2 * nw, h, -1)
+
+        a, s, mask = a.view(2 * nw, w, width), s.view(2 * nw, w, width), mask.view(2 * nw, w)
+        bias = torch.randn(2 * nw, w, h, depth * heads, generator=g).to(gpu)
+    else:
+        to_keys = None
+        bias = torch.randn(2, n, n, depth * heads, generator=g).to(gpu)
+    calls = []
+    real = ops.layernorm_split3 if width >= ops.X3_MIN_K else ops.layer_norm
+    name = "layernorm_split3" if width >= ops.X3_MIN_K else "layer_norm"
+    with torch.inference_mode():
+        want = ref(a, s, bias, mask, to_keys)
+        with pytest.MonkeyPatch.context() as mp:
+            mp.setattr(ops, name, lambda *args: calls.append(1) or real(*args))
+            got = stack(a, s, bias, mask, to_keys)
+        lin = stack.layers[2].adaln.s_scale
+        lin.forward = lambda x, f=type(lin).forward, m=lin: f(m, x)  # an instance forward, as a memo installs
+        try:
+            memo = stack(a, s, bias, mask, to_keys)
+        finally:
+            del lin.forward
+        if width >= ops.X3_MIN_K:
+            before = ops.exact_fp32_linears(True)
+            try:
+                exact = stack(a, s, bias, mask, to_keys)
+            finally:
+                ops.exact_fp32_linears(before)
+            assert max_rel(exact, want) < 1e-5
+    assert len(calls) == 1  # LayerNorm(s) once for the three layers
+    assert max_rel(got, want) < 1e-4
+    assert max_rel(memo, want) < 1e-4
     adapters.uninstall(host)

@@ -82,7 +82,8 @@ def test_configs4_stacks_match_fp32_oracle(gpu, monkeypatch):
     host.structure_module.score_model = copy.deepcopy(ref).to(gpu)
     patched = adapters.install(host, require_boltz2=False)
     layers = 24 + 3 + 3
-    assert patched == 5 * layers  # per layer: the layer, AdaLN, the transition's AdaLN, the transition, the attention
+    # per layer: the layer, AdaLN, the transition's AdaLN, the transition, the attention; and the three stacks
+    assert patched == 5 * layers + 3
     launches = []
     original = ops.seq_attention_batched
     monkeypatch.setattr(ops, "seq_attention_batched", lambda *a, **k: launches.append(1) or original(*a, **k))
