@@ -25,6 +25,9 @@ Patched (class name, path rule -> replacement):
   DiffusionTransformer under
       "structure_module.score_model."              -> diffusion.stack_forward (operands of s
       built once per stack call; beyond the reference)
+  AtomTransformer under
+      "structure_module.score_model."              -> diffusion.atom_transformer_forward (key
+      windows read by address instead of gathered; beyond the reference)
   structure_module.sample                          -> diffusion.optimized_sample
 """
 
@@ -60,7 +63,8 @@ def install(model, *, require_boltz2: bool = True, require_device: bool = True):
     from . import _native
 
     _native.lib()  # fail loudly here, not inside the first forward
-    from .diffusion import adaln_forward, layer_forward, optimized_sample, stack_forward, transition_forward
+    from .diffusion import (adaln_forward, atom_transformer_forward, layer_forward, optimized_sample, stack_forward,
+                            transition_forward)
     from .multiplication import normalized_forward
     from .pair_bias import prepared_forward
     from .pair_transition import transition_forward as pair_transition_forward
@@ -95,6 +99,9 @@ def install(model, *, require_boltz2: bool = True, require_device: bool = True):
             patched += 1
         elif name.startswith(SCORE_MODEL) and cls == "DiffusionTransformer":
             module.forward = MethodType(stack_forward, module)
+            patched += 1
+        elif name.startswith(SCORE_MODEL) and cls == "AtomTransformer":
+            module.forward = MethodType(atom_transformer_forward, module)
             patched += 1
     structure = getattr(model, "structure_module", None)
     if structure is not None and hasattr(type(structure), "sample"):

@@ -97,9 +97,21 @@ constexpr float kLog2e = 1.4426950408889634f;
 // bias element b / bdiv ([heads][nq][nk], element stride sbias; upstream
 // repeat_interleave(multiplicity)) and mask element b (stride smask, 0 to
 // broadcast one mask); out element b is [nq][heads * D] at stride nq * heads * D.
+//
+// The fp32 kernel also takes (defaults give the form above):
+//  * bias element (b / bdiv) * bwin + b % bwin, at head / query / key strides
+//    sbh, sbq, sbk (sbq == 0: dense [heads][nq][nk]);
+//  * windowed keys (nw > 0; the atom transformer's to_keys gather): element b
+//    is window b % nw of its sample, and its key j is row koff + j of its k / v
+//    / mask block (sk = wq * ldk, smask = wq), present only while
+//    0 <= (b % nw) * wq + koff + j < nw * wq; an absent key is a zero key and
+//    value row with mask 0, as upstream's zero rows of single_to_keys.
 struct SeqAttnShape {
   int nq, nk, bdiv;
   int64_t ldq, ldk, sq, sk, sbias, smask;
+  int bwin = 1;
+  int64_t sbh = 0, sbq = 0, sbk = 1;
+  int nw = 0, wq = 0, koff = 0;
 };
 
 // TILES 16-key tiles per wave and step: 4 (64 keys), or 2 for short key rows
@@ -118,15 +130,24 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
   const int HD = heads * D;
   const int nq = sh.nq, nk = sh.nk;
   const int64_t ldq = sh.ldq, ldk = sh.ldk;
+  int klo = 0, khi = nk;  // keys present: klo <= j < khi
   {
     const int64_t b = blockIdx.z;
     q += b * sh.sq;
     g += b * sh.sq;
     k += b * sh.sk;
     v += b * sh.sk;
-    bias += (b / sh.bdiv) * sh.sbias;
+    bias += ((b / sh.bdiv) * sh.bwin + b % sh.bwin) * sh.sbias;
     mask += b * sh.smask;
     out += b * nq * HD;
+    if (sh.nw > 0) {
+      const int t0 = (int)(b % sh.nw) * sh.wq + sh.koff;
+      klo = max(0, -t0);
+      khi = min(nk, sh.nw * sh.wq - t0);
+      k += (int64_t)sh.koff * ldk;
+      v += (int64_t)sh.koff * ldk;
+      mask += sh.koff;
+    }
   }
   __shared__ float part_o[kAttnWaves][16 * DT][kAttnQ];
   __shared__ float part_m[kAttnWaves][kAttnQ], part_l[kAttnWaves][kAttnQ];
@@ -136,7 +157,7 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
   float qf[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) qf[s] = q[(int64_t)qc * ldq + h * D + KS * gi + s];
-  const float* brow = bias + ((int64_t)h * nq + qc) * nk;
+  const float* brow = bias + h * sh.sbh + qc * sh.sbq;
   f32x4 o[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -148,11 +169,12 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
     float tmax = -INFINITY;
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
-      const int kr = min(key0 + 16 * t + c, nk - 1);
-      const float* krow = k + (int64_t)kr * ldk + h * D + KS * gi;
+      const int kj = key0 + 16 * t + c;
+      const bool kin = kj >= klo && kj < khi;
+      const float* krow = k + (int64_t)min(max(kj, klo), khi - 1) * ldk + h * D + KS * gi;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < KS; ++s) acc = mfma16f32(krow[s], qf[s], acc);
+      for (int s = 0; s < KS; ++s) acc = mfma16f32(kin ? krow[s] : 0.f, qf[s], acc);
       const int kb = key0 + 16 * t + 4 * gi;  // this lane's keys kb .. kb + 3
       f32x4 b4, m4;
       if (full) {
@@ -161,8 +183,9 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          b4[r] = brow[min(kb + r, nk - 1)];
-          m4[r] = mask[min(kb + r, nk - 1)];
+          const int j = kb + r;
+          b4[r] = brow[(int64_t)min(j, nk - 1) * sh.sbk];
+          m4[r] = j >= klo && j < khi ? mask[j] : 0.f;
         }
       }
 #pragma unroll
@@ -184,13 +207,14 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
       for (int s = 0; s < 4; ++s) {
         const float p = __builtin_amdgcn_exp2f((st[t][s] - mn) * kLog2e);
         lsum += p;
-        const int kr = min(key0 + 16 * t + 4 * gi + s, nk - 1);
-        const float* vrow = v + (int64_t)kr * ldk + h * D;
+        const int kj = key0 + 16 * t + 4 * gi + s;
+        const bool kin = kj >= klo && kj < khi;
+        const float* vrow = v + (int64_t)min(max(kj, klo), khi - 1) * ldk + h * D;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const int d = 16 * dt + c;
-          const float a = vrow[d < D ? d : D - 1];  // clamped load, zero row past D
-          o[dt] = mfma16f32(d < D ? a : 0.f, p, o[dt]);
+          const float a = vrow[d < D ? d : D - 1];  // clamped load; zero past D and for absent keys
+          o[dt] = mfma16f32(d < D && kin ? a : 0.f, p, o[dt]);
         }
       }
     }
@@ -227,11 +251,17 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
 }
 
 int launch_seq_attention(const char* name, const float* q, const float* k, const float* v, const float* bias,
-                         const float* mask, const float* g, int64_t batch, const SeqAttnShape& sh, int heads,
+                         const float* mask, const float* g, int64_t batch, SeqAttnShape sh, int heads,
                          int head_dim, float inf, float* out, hipStream_t stream) {
-  // 16-byte bias / mask loads where every row start is aligned; scalar loads otherwise
-  const bool vec = sh.nk % 4 == 0 && sh.sbias % 4 == 0 && sh.smask % 4 == 0 && (uintptr_t)bias % 16 == 0 &&
-                   (uintptr_t)mask % 16 == 0;
+  if (sh.sbq == 0) {  // dense [heads][nq][nk] bias elements
+    sh.sbh = (int64_t)sh.nq * sh.nk;
+    sh.sbq = sh.nk;
+    sh.sbk = 1;
+  }
+  // 16-byte bias / mask loads where every row start is aligned and keys are
+  // plain rows; scalar loads otherwise
+  const bool vec = sh.nw == 0 && sh.sbk == 1 && sh.nk % 4 == 0 && sh.sbias % 4 == 0 && sh.sbh % 4 == 0 &&
+                   sh.sbq % 4 == 0 && sh.smask % 4 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)mask % 16 == 0;
   const dim3 grid((unsigned)((sh.nq + kAttnQ - 1) / kAttnQ), (unsigned)heads, (unsigned)batch);
   const float rscale = 1.f / sqrtf((float)head_dim);
 #define SEQ_ATTN(DIM, TILES) \
@@ -593,6 +623,45 @@ int bmx_seq_attention_batched_fwd(const float* q, const float* k, const float* v
   BMX_REQUIRE(q && k && v && bias && mask && g && out, "bmx_seq_attention_batched_fwd: null pointer");
   const SeqAttnShape sh{(int)nq, (int)nk, (int)bias_div, ldq, ldk, sq, sk, sbias, smask};
   return launch_seq_attention("bmx_seq_attention_batched_fwd", q, k, v, bias, mask, g, batch, sh, heads, head_dim,
+                              inf, out, stream);
+}
+
+int bmx_seq_attention_windowed_fwd(const float* q, const float* k, const float* v, const float* bias,
+                                   const float* mask, const float* g, int64_t batch, int64_t nq, int64_t nk,
+                                   int64_t ldq, int64_t ldk, int64_t windows, int64_t key_offset,
+                                   int64_t bias_group, int64_t sbias, int64_t sbias_h, int64_t sbias_q,
+                                   int64_t sbias_k, int heads, int head_dim, float inf, float* out,
+                                   hipStream_t stream) {
+  BMX_REQUIRE(batch >= 0 && batch <= 65535, "bmx_seq_attention_windowed_fwd: batch must be in [0, 65535]");
+  BMX_REQUIRE(nq >= 1 && nq <= 4096 && nk >= 1 && nk <= 4096,
+              "bmx_seq_attention_windowed_fwd: need 1 <= nq, nk <= 4096");
+  BMX_REQUIRE(head_dim == 24 || head_dim == 32 || head_dim == 48,
+              "bmx_seq_attention_windowed_fwd: head_dim must be 24, 32 or 48 (got %d)", head_dim);
+  BMX_REQUIRE(heads >= 1 && heads <= 64, "bmx_seq_attention_windowed_fwd: heads must be in [1, 64] (got %d)",
+              heads);
+  BMX_REQUIRE(ldq >= (int64_t)heads * head_dim && ldk >= (int64_t)heads * head_dim,
+              "bmx_seq_attention_windowed_fwd: row strides must be >= heads * head_dim");
+  BMX_REQUIRE(windows >= 1 && windows * nq <= (1 << 24) && batch % windows == 0,
+              "bmx_seq_attention_windowed_fwd: need windows >= 1 dividing batch, windows * nq <= 2^24");
+  BMX_REQUIRE(key_offset <= 0 && key_offset + nk >= nq,
+              "bmx_seq_attention_windowed_fwd: need key_offset <= 0 and key_offset + nk >= nq (every window "
+              "sees its own queries)");
+  BMX_REQUIRE(bias_group >= 1 && bias_group % windows == 0,
+              "bmx_seq_attention_windowed_fwd: bias_group must be a positive multiple of windows");
+  BMX_REQUIRE(sbias >= 0 && sbias_h >= 0 && sbias_q >= 1 && sbias_k >= 0 && bias_group <= (1 << 30),
+              "bmx_seq_attention_windowed_fwd: bias strides must be >= 0 (the query stride >= 1)");
+  BMX_REQUIRE(inf > 0.f, "bmx_seq_attention_windowed_fwd: inf must be positive");
+  if (batch == 0) return BMX_OK;
+  BMX_REQUIRE(q && k && v && bias && mask && g && out, "bmx_seq_attention_windowed_fwd: null pointer");
+  SeqAttnShape sh{(int)nq, (int)nk, (int)bias_group, ldq, ldk, nq * ldq, nq * ldk, sbias, nq};
+  sh.bwin = (int)windows;
+  sh.sbh = sbias_h;
+  sh.sbq = sbias_q;
+  sh.sbk = sbias_k;
+  sh.nw = (int)windows;
+  sh.wq = (int)nq;
+  sh.koff = (int)key_offset;
+  return launch_seq_attention("bmx_seq_attention_windowed_fwd", q, k, v, bias, mask, g, batch, sh, heads, head_dim,
                               inf, out, stream);
 }
 

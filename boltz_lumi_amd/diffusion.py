@@ -16,6 +16,7 @@ the class forward.
 
 from __future__ import annotations
 
+import weakref
 from contextlib import nullcontext
 
 import torch
@@ -23,7 +24,7 @@ import torch
 from . import ops
 from ._guards import autocast_off, gfx950_tensor, inference
 from .atom_conditioning import atom_conditioning_cache
-from .pair_bias import prepare_token_bias
+from .pair_bias import prepare_token_bias, windowed_attention, windowed_ok
 
 
 def optimized_sample(self, *args, **kwargs):
@@ -205,22 +206,28 @@ def _conditioning(layer, side, eps):
             torch.nn.functional.linear(side.raw(), wg, bg))
 
 
-def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity):
+def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity, keys=None):
+    """The layer with its conditioning projections on the shared operands of s
+    (``side``); with ``keys`` (a ``_WindowKeys``) the attention reads its key
+    windows by address (``windowed_attention``) instead of ``to_keys``."""
     d = a.shape[-1]
     tr = self.transition
     eps = self.adaln.s_norm.eps
-    if tr.adaln.s_norm.eps != eps:
-        return _layer_per_linear(self, a, s, bias, mask, to_keys, multiplicity)
     mods, gates = _conditioning(self, side, eps)
     scale_a, shift_a, scale_t, shift_t = mods.split(d, dim=-1)
     gate_a, gate_t = gates.split(d, dim=-1)
     rows = a.reshape(-1, d)
     b = ops.adaln_modulate(rows, scale_a, shift_a, self.adaln.a_norm.eps).view(a.shape)
-    k_in = b
-    if to_keys is not None:
-        k_in = to_keys(b)
-        mask = to_keys(mask.unsqueeze(-1)).squeeze(-1)
-    b = self.pair_bias_attn(s=b, z=bias, mask=mask, multiplicity=multiplicity, k_in=k_in)
+    if keys is not None:
+        att = self.pair_bias_attn
+        o = windowed_attention(att, b, bias, keys)
+        b = att.proj_o(o) if "forward" in vars(att.proj_o) else ops.linear_fp32(o, att.proj_o)
+    else:
+        k_in = b
+        if to_keys is not None:
+            k_in = to_keys(b)
+            mask = to_keys(mask.unsqueeze(-1)).squeeze(-1)
+        b = self.pair_bias_attn(s=b, z=bias, mask=mask, multiplicity=multiplicity, k_in=k_in)
     if b.shape == a.shape and b.dtype == torch.float32:
         rows = ops.gated_residual(b.reshape(-1, d).contiguous(), gate_a, rows)
     else:
@@ -265,7 +272,7 @@ def _layer_per_linear(self, a, s, bias, mask, to_keys, multiplicity):
 def _layer(self, a, s, bias, mask, to_keys, multiplicity, side):
     if not (eligible(self, a, s) and a.shape == s.shape and a.shape[-1] % 4 == 0 and _plain(self.output_projection)):
         return type(self).forward(self, a, s, bias, mask, to_keys, multiplicity)
-    if _side_ok(self, a, s):
+    if _side_ok(self, a, s) and self.transition.adaln.s_norm.eps == self.adaln.s_norm.eps:
         return _layer_with_side(self, a, s, side if side is not None else _Side(s), bias, mask, to_keys,
                                 multiplicity)
     return _layer_per_linear(self, a, s, bias, mask, to_keys, multiplicity)
@@ -306,3 +313,89 @@ def stack_forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity=1
         bias_l = bias[:, :, :, i] if getattr(self, "pair_bias_attn", True) else None
         a = _layer(layer, a, s, bias_l, mask, to_keys, multiplicity, side)
     return a
+
+
+# ---------------------------------------------------------------- atom windows
+
+_WINDOW_PROBES = weakref.WeakKeyDictionary()  # to_keys -> {(n, w, h, device): key offset or None}
+
+
+def window_key_offset(to_keys, n, w, h, device):
+    """The key offset koff if ``to_keys`` maps [1, n, 1] atom rows to [1, n / w,
+    h, 1] key windows as the window gather (key j of window k is atom
+    k w + koff + j, zero outside 0 .. n - 1; koff = (w - h) / 2, the map of
+    upstream single_to_keys through get_indexing_matrix), else None.  Checked
+    once per to_keys object and shape on a probe of atom numbers (upstream's
+    to_keys is one 0/1 matrix product per channel, so the probe's image fixes
+    it); the check synchronises with the device once."""
+    key = (n, w, h, str(device))
+    try:
+        seen = _WINDOW_PROBES.setdefault(to_keys, {})
+    except TypeError:  # not weak-referenceable: probe every time
+        seen = {}
+    if key not in seen:
+        koff = (w - h) // 2
+        ok = n % w == 0 and (w - h) % 2 == 0
+        if ok:
+            probe = torch.arange(1, n + 1, device=device, dtype=torch.float32).view(1, n, 1)
+            t = torch.arange(n // w, device=device)[:, None] * w + koff + torch.arange(h, device=device)[None, :]
+            want = torch.where((t >= 0) & (t < n), t + 1, torch.zeros_like(t)).float()
+            got = to_keys(probe)
+            ok = isinstance(got, torch.Tensor) and got.numel() == want.numel() and torch.equal(
+                got.reshape(want.shape).float(), want)
+        seen[key] = koff if ok else None
+    return seen[key]
+
+
+class _WindowKeys:
+    """The atom transformer's to_keys as addressing for ``windowed_attention``:
+    ``windows`` per sample, keys from atom ``offset`` relative to each window,
+    ``bias_group`` windows (the samples of one structure) sharing bias
+    elements, and the flat atom ``mask``."""
+
+    def __init__(self, windows, offset, bias_group, mask):
+        self.windows, self.offset, self.bias_group, self.mask = windows, offset, bias_group, mask
+
+
+def _windowed_layer_ok(layer, a, s) -> bool:
+    return (_patched_with(layer, layer_forward) and _plain(layer) and eligible(layer, a, s) and a.shape == s.shape
+            and a.shape[-1] % 4 == 0 and _plain(layer.output_projection) and _side_ok(layer, a, s)
+            and layer.transition.adaln.s_norm.eps == layer.adaln.s_norm.eps and windowed_ok(layer.pair_bias_attn))
+
+
+def atom_transformer_forward(self, q, c, bias, to_keys, mask, multiplicity=1, *args, **kwargs):
+    """Drop-in for ``AtomTransformer.forward`` (upstream transformersv2).
+
+    Upstream windows q and c into [B * N / W, W, D], repeats the per-structure
+    bias [B, N / W, W, H, layers * heads] over the samples and runs its
+    DiffusionTransformer with ``to_keys`` gathering each window's H key atoms
+    (single_to_keys: a 0/1 matrix product, zero rows past the ends).  Here,
+    when the stack's layers run the fused path and ``to_keys`` is verified to
+    be that gather (``window_key_offset``), nothing is gathered or repeated:
+    each layer projects q | k | v | g on the atom rows and the attention kernel
+    reads each window's keys, key mask and the shared bias by address.
+    Otherwise upstream."""
+    stack = getattr(self, "diffusion_transformer", None)
+    w, h = self.attn_window_queries, self.attn_window_keys
+    if args or kwargs or stack is None or not _patched_with(stack, stack_forward) or not _plain(stack):
+        return type(self).forward(self, q, c, bias, to_keys, mask, multiplicity, *args, **kwargs)
+    layers = list(stack.layers)
+    b, n, d = q.shape
+    nw = n // w if w else 0
+    ok = (inference(self) and layers and getattr(stack, "pair_bias_attn", True) and nw > 0 and n % w == 0
+          and isinstance(bias, torch.Tensor) and bias.dim() == 5 and bias.shape[0] * multiplicity == b
+          and tuple(bias.shape[1:4]) == (nw, w, h) and bias.shape[4] % len(layers) == 0
+          and bias.dtype == torch.float32 and c.shape[:2] == (b, n) and mask.shape == (b, n))
+    if ok:
+        qw, cw = q.reshape(b * nw, w, d), c.reshape(b * nw, w, -1)
+        ok = all(_windowed_layer_ok(layer, qw, cw) for layer in layers)
+    koff = window_key_offset(to_keys, n, w, h, q.device) if ok else None
+    if koff is None:
+        return type(self).forward(self, q, c, bias, to_keys, mask, multiplicity, *args, **kwargs)
+    keys = _WindowKeys(nw, koff, multiplicity * nw, mask.float().reshape(-1).contiguous())
+    heads = bias.shape[4] // len(layers)
+    side = _Side(cw)
+    a = qw
+    for i, layer in enumerate(layers):
+        a = _layer_with_side(layer, a, cw, side, bias[..., i * heads:(i + 1) * heads], None, None, 1, keys)
+    return a.view(b, n, d)

@@ -105,6 +105,36 @@ def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
     return ops.seq_attention_batched(q, k, v, bias, m, g, module.inf, bias_div=multiplicity)
 
 
+def windowed_ok(module) -> bool:
+    """``windowed_attention`` applies: a patched, unhooked AttentionPairBias with
+    a given bias, 24 / 32 / 48 dims per head and no bias on proj_k / proj_v (a
+    zero key row then projects to zero, as the gather's zero rows do)."""
+    fwd = vars(module).get("forward")
+    heads, width = module.num_heads, module.c_s
+    return (getattr(fwd, "__func__", None) is prepared_forward and not module._forward_hooks
+            and not module._forward_pre_hooks and not module.compute_pair_bias and not module.training
+            and width % heads == 0 and width // heads in (24, 32, 48) and heads <= 64
+            and module.proj_k.bias is None and module.proj_v.bias is None)
+
+
+def windowed_attention(module, s, bias, keys):
+    """``sigmoid(proj_g(s)) * attention`` of AttentionPairBias ``module`` (before
+    ``proj_o``) for query windows s [E, W, c_s] whose keys are the window gather
+    of the same rows (upstream ``to_keys``): q | k | v | g are one projection of
+    the atom rows and the kernel reads each window's keys by address
+    (``ops.seq_attention_windowed``), so neither the gathered rows nor their
+    projection is materialised.  ``keys`` carries the gather (``windows``,
+    ``offset``, ``bias_group``, the atom ``mask``); ``bias`` is this layer's
+    [Eb, ..., W, NK, heads] view of the atom bias."""
+    e, w, width = s.shape
+    lin = (module.proj_q, module.proj_k, module.proj_v, module.proj_g)
+    proj = _joint_projection(module, "qkvg", s.reshape(e * w, width), lin)
+    q, k, v, g = proj.split(width, dim=-1)
+    return ops.seq_attention_windowed(q.view(e, w, width), k, v, bias.float(), keys.mask, g.view(e, w, width),
+                                      module.inf, windows=keys.windows, key_offset=keys.offset,
+                                      bias_group=keys.bias_group)
+
+
 def prepared_forward(module, s, z, mask, k_in, multiplicity=1):
     """Drop-in for the score model's ``AttentionPairBias.forward`` (reference
     pair_bias.py:15-36, installed there on the token transformer's; here also

@@ -247,6 +247,26 @@ int bmx_seq_attention_batched_fwd(const float* q, const float* k, const float* v
                                   int64_t sq, int64_t sk, int64_t sbias, int64_t smask, int64_t bias_div, int heads,
                                   int head_dim, float inf, float* out, bmx_stream_t stream);
 
+/* bmx_seq_attention_batched_fwd for the atom transformer's windows, with upstream's to_keys gather
+ * (single_to_keys through its indexing matrix, then AttentionPairBias with k_in = to_keys(s)) done by
+ * addressing: element b (window b % windows of sample b / windows) has its nq query rows at rows
+ * b * nq .. of q, g (row stride ldq) and reads key j from row b * nq + key_offset + j of k, v (row
+ * stride ldk; k, v projected on the atom rows, batch * nq rows) and mask ([batch * nq], the atom
+ * mask), present only while 0 <= (b % windows) * nq + key_offset + j < windows * nq; an absent key
+ * is a zero key / value row with mask 0, as the zero rows single_to_keys writes.  The bias of
+ * element b is element (b / bias_group) * windows + b % windows (upstream repeat_interleave of the
+ * per-structure window bias over the samples: bias_group = samples * windows) at element / head /
+ * query / key strides sbias, sbias_h, sbias_q (>= 1), sbias_k (any layout, e.g. one layer's heads of
+ * the [B, windows, nq, nk, layers * heads] atom bias in place).  out [batch][nq][heads * D]
+ * contiguous.  Replaces AttentionPairBias.forward's attention with upstream's to_keys
+ * (pair_bias.py:21-36; the keys that transformersv2.AtomTransformer gathers). */
+int bmx_seq_attention_windowed_fwd(const float* q, const float* k, const float* v, const float* bias,
+                                   const float* mask, const float* g, int64_t batch, int64_t nq, int64_t nk,
+                                   int64_t ldq, int64_t ldk, int64_t windows, int64_t key_offset,
+                                   int64_t bias_group, int64_t sbias, int64_t sbias_h, int64_t sbias_q,
+                                   int64_t sbias_k, int heads, int head_dim, float inf, float* out,
+                                   bmx_stream_t stream);
+
 /* bmx_seq_attention_batched_fwd with both products on bf16 MFMA, each operand split into bf16 high
  * and low parts (x y ~ xh yh + xh yl + xl yh: about 2^-16 relative per product, the same form as the
  * split-bf16 fp32 linears of the diffusion blocks) instead of fp32 MFMA; same arguments and result,

@@ -207,3 +207,20 @@ def test_msa_template_and_confidence_stacks_are_patched_by_class_and_suffix():
     with torch.inference_mode():
         assert torch.equal(template(z, pm), want)
     adapters.uninstall(model)
+
+
+def test_window_probe_on_cpu():
+    """The to_keys probe that gates the atom transformer's addressed key
+    windows: upstream's single_to_keys partial passes with offset (W - H) / 2;
+    another window layout, or a to_keys of another shape, does not."""
+    import functools
+
+    from boltz_lumi_amd.diffusion import window_key_offset
+
+    n, w, h = 6 * 32, 32, 128
+    index = R.get_indexing_matrix(n // w, w, h)
+    good = functools.partial(R.single_to_keys, indexing_matrix=index, w=w, h=h)
+    assert window_key_offset(good, n, w, h, "cpu") == -48
+    assert window_key_offset(functools.partial(R.single_to_keys, indexing_matrix=index.flip(0), w=w, h=h),
+                             n, w, h, "cpu") is None
+    assert window_key_offset(lambda x: torch.zeros(1, n // w, h - 1, 1), n, w, h, "cpu") is None

@@ -82,11 +82,13 @@ def test_configs4_stacks_match_fp32_oracle(gpu, monkeypatch):
     host.structure_module.score_model = copy.deepcopy(ref).to(gpu)
     patched = adapters.install(host, require_boltz2=False)
     layers = 24 + 3 + 3
-    # per layer: the layer, AdaLN, the transition's AdaLN, the transition, the attention; and the three stacks
-    assert patched == 5 * layers + 3
-    launches = []
-    original = ops.seq_attention_batched
+    # per layer: the layer, AdaLN, the transition's AdaLN, the transition, the attention; the three stacks and
+    # the two atom transformers
+    assert patched == 5 * layers + 3 + 2
+    launches, windowed = [], []
+    original, original_w = ops.seq_attention_batched, ops.seq_attention_windowed
     monkeypatch.setattr(ops, "seq_attention_batched", lambda *a, **k: launches.append(1) or original(*a, **k))
+    monkeypatch.setattr(ops, "seq_attention_windowed", lambda *a, **k: windowed.append(1) or original_w(*a, **k))
 
     t_cpu = step_inputs(7, "cpu")
     print("configs[4] stacks: CPU oracle, 5 samples", flush=True)
@@ -99,7 +101,8 @@ def test_configs4_stacks_match_fp32_oracle(gpu, monkeypatch):
         packed = prepare_token_bias(t["token_bias"])  # what optimized_sample hands the token transformer
         r_got, q_got, a_got = run_stacks(host.structure_module.score_model, t, packed, index.to(gpu))
     torch.cuda.synchronize()
-    assert len(launches) == layers  # every attention ran on the fused kernel
+    # every attention ran on a fused kernel; the atom transformers' read their key windows by address
+    assert len(launches) == 24 and len(windowed) == 6
     err_r, err_q, err_a = max_rel(r_got, r_ref), max_rel(q_got, q_ref), max_rel(a_got, a_ref)
     print(f"configs[4] stacks max_rel: coordinate update {err_r:.2e}, atoms {err_q:.2e}, tokens {err_a:.2e}",
           flush=True)
