@@ -578,7 +578,7 @@ def diffusion_step(args):
     import torch
     from torch import nn
     from boltz_lumi_amd import adapters, ops
-    from boltz_lumi_amd.pair_bias import prepare_token_bias
+    from boltz_lumi_amd.pair_bias import prepare_token_bias, prepare_window_bias
 
     if ROOT not in sys.path:
         sys.path.insert(0, ROOT)
@@ -602,6 +602,8 @@ def diffusion_step(args):
     t = {k: v.to(dev) for k, v in t.items()}
     index = R.get_indexing_matrix(nw, w, h, device=dev)
     packed = prepare_token_bias(t["token_bias"])
+    # the window biases as optimized_sample hands them to the atom transformers (channel-major)
+    t["enc_bias"], t["dec_bias"] = prepare_window_bias(t["enc_bias"]), prepare_window_bias(t["dec_bias"])
 
     def to_keys(x):
         return R.single_to_keys(x, index, w, h)
@@ -698,6 +700,7 @@ def diffusion_kernel_times(stacks, t, packed, samples, tokens):
     shape; launches per step count every layer."""
     import torch
     from boltz_lumi_amd import ops
+    from boltz_lumi_amd.pair_bias import prepare_window_bias
 
     dev = t["a"].device
     g = torch.Generator().manual_seed(1)
@@ -718,14 +721,20 @@ def diffusion_kernel_times(stacks, t, packed, samples, tokens):
          lambda: ops.seq_attention_batched(qq, kk, vv, bias, mask, gg, 1e6, bias_div=samples),
          3 * 4.0 * 16 * 48 * tokens * tokens * samples, samples * tokens * d * 16 + 16 * tokens * tokens * 4, 24,
          PEAK_BF16_TFLOPS)
+    # the atom transformer's attention as the installed stacks run it: q | k | v | g of the atom rows,
+    # each window's 128 keys read by address (keys past a sample's ends absent), and one layer's 4
+    # heads of the [1, 256, 32, 128, 12] window bias in place, shared by the samples; HBM bytes:
+    # q, k, v, g and out once per atom, the bias slice once
     nw = 8192 // 32
-    aq = torch.randn(samples * nw, 32, 2 * 128, generator=g).to(dev)
-    ak = torch.randn(samples * nw, 128, 2 * 128, generator=g).to(dev)
-    ab = torch.randn(samples * nw, 4, 32, 128, generator=g).to(dev)
-    am = torch.ones(samples * nw, 128, device=dev)
+    proj = torch.randn(samples * 8192, 4 * 128, generator=g).to(dev)
+    pq, pk, pv, pg = proj.split(128, dim=-1)
+    ab = prepare_window_bias(torch.randn(1, nw, 32, 128, 12, generator=g).to(dev))[..., 4:8]
+    am = torch.ones(samples * 8192, device=dev)
     rate("seq_attention (atom windows, 4 x 32)",
-         lambda: ops.seq_attention_batched(aq[..., :128], ak[..., :128], ak[..., 128:], ab, am, aq[..., 128:], 1e6),
-         4.0 * 4 * 32 * 32 * 128 * samples * nw, samples * nw * (32 * 512 + 128 * 1024 + 4 * 32 * 128 * 4), 6)
+         lambda: ops.seq_attention_windowed(pq.view(samples * nw, 32, 128), pk, pv, ab, am,
+                                            pg.view(samples * nw, 32, 128), 1e6, windows=nw, key_offset=-48,
+                                            bias_group=samples * nw),
+         4.0 * 4 * 32 * 32 * 128 * samples * nw, samples * 8192 * 5 * 128 * 4 + nw * 32 * 128 * 4 * 4, 6)
     per_step = {"adaln": 48, "gated_swiglu": 24, "gate": 24}
     for name, rec in elementwise_kernel_rates(m, d, 2 * d, g, dev).items():
         out[f"{name} (token)"] = {"ms": rec["ms"], "launches_per_step": per_step[name],

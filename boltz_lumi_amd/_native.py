@@ -59,7 +59,7 @@ SIGNATURES = {
                                              _P]),
     "bmx_seq_attention_fwd": (c_int, [_P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int, c_int, c_float, _P, _P]),
     "bmx_seq_attention_batched_fwd": (c_int, [_P, _P, _P, _P, _P, _P] + [c_int64] * 10 + [c_int, c_int, c_float, _P, _P]),
-    "bmx_seq_attention_windowed_fwd": (c_int, [_P, _P, _P, _P, _P, _P] + [c_int64] * 12
+    "bmx_seq_attention_windowed_fwd": (c_int, [_P, _P, _P, _P, _P, _P] + [c_int64] * 13
                                        + [c_int, c_int, c_float, _P, _P]),
     "bmx_seq_attention_x3_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int, c_int]),
     "bmx_seq_attention_x3_batched_fwd": (c_int, [_P, _P, _P, _P, _P, _P] + [c_int64] * 10

@@ -99,8 +99,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 // broadcast one mask); out element b is [nq][heads * D] at stride nq * heads * D.
 //
 // The fp32 kernel also takes (defaults give the form above):
-//  * bias element (b / bdiv) * bwin + b % bwin, at head / query / key strides
-//    sbh, sbq, sbk (sbq == 0: dense [heads][nq][nk]);
+//  * bias element of b at (b / bdiv) * sbg + (b % bwin) * sbias (sbg < 0:
+//    bwin * sbias, so element (b / bdiv) * bwin + b % bwin), with head / query
+//    / key strides sbh, sbq, sbk (sbq == 0: dense [heads][nq][nk]);
 //  * windowed keys (nw > 0; the atom transformer's to_keys gather): element b
 //    is window b % nw of its sample, and its key j is row koff + j of its k / v
 //    / mask block (sk = wq * ldk, smask = wq), present only while
@@ -110,7 +111,7 @@ struct SeqAttnShape {
   int nq, nk, bdiv;
   int64_t ldq, ldk, sq, sk, sbias, smask;
   int bwin = 1;
-  int64_t sbh = 0, sbq = 0, sbk = 1;
+  int64_t sbh = 0, sbq = 0, sbk = 1, sbg = -1;
   int nw = 0, wq = 0, koff = 0;
 };
 
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
                                                             const float* __restrict__ bias,
                                                             const float* __restrict__ mask,
                                                             const float* __restrict__ g, SeqAttnShape sh, int heads,
-                                                            float inf, float rscale, bool vec,
+                                                            float inf, float rscale, int vec,
                                                             float* __restrict__ out) {
   constexpr int KS = D / 4;          // QK^T MFMA steps
   constexpr int DT = (D + 15) / 16;  // O^T d tiles
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
     g += b * sh.sq;
     k += b * sh.sk;
     v += b * sh.sk;
-    bias += ((b / sh.bdiv) * sh.bwin + b % sh.bwin) * sh.sbias;
+    bias += (b / sh.bdiv) * sh.sbg + (b % sh.bwin) * sh.sbias;
     mask += b * sh.smask;
     out += b * nq * HD;
     if (sh.nw > 0) {
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
   __shared__ float part_o[kAttnWaves][16 * DT][kAttnQ];
   __shared__ float part_m[kAttnWaves][kAttnQ], part_l[kAttnWaves][kAttnQ];
   const int h = blockIdx.y, q0 = blockIdx.x * kAttnQ;
-  const int w = threadIdx.x >> 6, l = lane_id(), gi = l >> 4, c = l & 15;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id(), gi = l >> 4, c = l & 15;
   const int qc = min(q0 + c, nq - 1);  // rows past the end re-read the last one and are not stored
   float qf[KS];
 #pragma unroll
@@ -164,28 +165,40 @@ __global__ __launch_bounds__(256) void seq_attention_kernel(const float* __restr
   float m = -3.4e38f, lsum = 0.f;
   constexpr int kStep = 16 * TILES;
   for (int key0 = w * kStep; key0 < nk; key0 += kAttnWaves * kStep) {
-    const bool full = vec && key0 + kStep <= nk;
     f32x4 st[TILES];
     float tmax = -INFINITY;
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
+      // 16-byte bias / mask loads for a tile whose 16 keys all exist (and, for
+      // the mask, are all present)
+      const int t0 = key0 + 16 * t;
+      const bool bfull = (vec & 1) && t0 + 16 <= nk;
+      const bool mfull = (vec & 2) && t0 >= klo && t0 + 16 <= khi;
       const int kj = key0 + 16 * t + c;
       const bool kin = kj >= klo && kj < khi;
       const float* krow = k + (int64_t)min(max(kj, klo), khi - 1) * ldk + h * D + KS * gi;
+      float kv[KS];  // loaded unconditionally (the row is clamped in range), then selected
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kv[s] = krow[s];
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < KS; ++s) acc = mfma16f32(kin ? krow[s] : 0.f, qf[s], acc);
+      for (int s = 0; s < KS; ++s) acc = mfma16f32(kin ? kv[s] : 0.f, qf[s], acc);
       const int kb = key0 + 16 * t + 4 * gi;  // this lane's keys kb .. kb + 3
       f32x4 b4, m4;
-      if (full) {
+      if (bfull) {
         b4 = *(const f32x4*)(brow + kb);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) b4[r] = brow[(int64_t)min(kb + r, nk - 1) * sh.sbk];
+      }
+      if (mfull) {
         m4 = *(const f32x4*)(mask + kb);
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int j = kb + r;
-          b4[r] = brow[(int64_t)min(j, nk - 1) * sh.sbk];
-          m4[r] = j >= klo && j < khi ? mask[j] : 0.f;
+          const float mj = mask[min(max(j, klo), khi - 1)];
+          m4[r] = j >= klo && j < khi ? mj : 0.f;
         }
       }
 #pragma unroll
@@ -258,10 +271,12 @@ int launch_seq_attention(const char* name, const float* q, const float* k, const
     sh.sbq = sh.nk;
     sh.sbk = 1;
   }
-  // 16-byte bias / mask loads where every row start is aligned and keys are
-  // plain rows; scalar loads otherwise
-  const bool vec = sh.nw == 0 && sh.sbk == 1 && sh.nk % 4 == 0 && sh.sbias % 4 == 0 && sh.sbh % 4 == 0 &&
-                   sh.sbq % 4 == 0 && sh.smask % 4 == 0 && (uintptr_t)bias % 16 == 0 && (uintptr_t)mask % 16 == 0;
+  if (sh.sbg < 0) sh.sbg = sh.sbias * sh.bwin;
+  // 16-byte bias (bit 0) / mask (bit 1) loads where every row start is
+  // aligned; scalar loads otherwise
+  const int vec = (sh.sbk == 1 && sh.nk % 4 == 0 && sh.sbias % 4 == 0 && sh.sbg % 4 == 0 && sh.sbh % 4 == 0 &&
+                   sh.sbq % 4 == 0 && (uintptr_t)bias % 16 == 0 ? 1 : 0) |
+                  (sh.smask % 4 == 0 && sh.koff % 4 == 0 && (uintptr_t)mask % 16 == 0 ? 2 : 0);
   const dim3 grid((unsigned)((sh.nq + kAttnQ - 1) / kAttnQ), (unsigned)heads, (unsigned)batch);
   const float rscale = 1.f / sqrtf((float)head_dim);
 #define SEQ_ATTN(DIM, TILES) \
@@ -365,7 +380,7 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
                                                                const float* __restrict__ bias,
                                                                const float* __restrict__ mask,
                                                                const float* __restrict__ g, SeqAttnShape sh, int heads,
-                                                               float inf, float rscale, bool vec,
+                                                               int64_t batch, float inf, float rscale, bool vec,
                                                                float* __restrict__ out) {
   constexpr int DK = (D + 31) / 32;              // QK^T k steps
   constexpr int DT = (D + 15) / 16;              // O^T d tiles
@@ -377,8 +392,19 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
   const int HD = heads * D;
   const int nq = sh.nq, nk = sh.nk;
   const int64_t ldq = sh.ldq, nkp = x3_nkp(nk);
-  const int64_t b = blockIdx.z;
-  const int h = blockIdx.y;
+  // Blocks are dispatched round-robin over the 8 XCDs (block L on XCD L % 8).
+  // Work item p = (L % 8) * per_xcd + L / 8 runs in the order (bias element,
+  // head, query block, element sharing the bias): the bdiv elements that read
+  // one bias tile follow each other on one XCD, which fetches the tile into
+  // its L2 once instead of once per element.
+  const int qblocks = (nq + kX3Q - 1) / kX3Q;
+  const int64_t groups = (batch + sh.bdiv - 1) / sh.bdiv;
+  const int64_t per_xcd = (groups * sh.bdiv * heads * qblocks + 7) / 8;
+  const int64_t p = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  const int64_t rest = p / sh.bdiv;
+  const int64_t b = rest / ((int64_t)qblocks * heads) * sh.bdiv + p % sh.bdiv;
+  if (b >= batch) return;  // the padding of the last XCD's run (whole block)
+  const int h = (int)((rest / qblocks) % heads), qb = (int)(rest % qblocks);
   q += b * sh.sq;
   g += b * sh.sq;
   bias += (b / sh.bdiv) * sh.sbias;
@@ -387,7 +413,7 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
   const bf16* k_src[2] = {kh + (b * heads + h) * nkp * D, kl + (b * heads + h) * nkp * D};
   const bf16* v_src[2] = {vth + (b * heads + h) * D * nkp, vtl + (b * heads + h) * D * nkp};
   const int l = lane_id(), gi = l >> 4, c = l & 15, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int qw = blockIdx.x * kX3Q + 16 * w;     // this wave's 16 queries
+  const int qw = qb * kX3Q + 16 * w;             // this wave's 16 queries
   const int qc = min(qw + c, nq - 1);            // rows past the end re-read the last one and are not stored
   const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
 
@@ -554,11 +580,12 @@ int launch_seq_attention_x3(const char* name, const float* q, const float* k, co
   if (int rc = check_launch(name)) return rc;
   const bool vec = sh.nk % 4 == 0 && sh.sbias % 4 == 0 && sh.smask % 4 == 0 && (uintptr_t)bias % 16 == 0 &&
                    (uintptr_t)mask % 16 == 0;
-  const dim3 grid((unsigned)((sh.nq + kX3Q - 1) / kX3Q), (unsigned)heads, (unsigned)batch);
+  const int64_t items = (batch + sh.bdiv - 1) / sh.bdiv * sh.bdiv * heads * ((sh.nq + kX3Q - 1) / kX3Q);
+  const dim3 grid((unsigned)(8 * ((items + 7) / 8)));
   const float rscale = 1.f / sqrtf((float)head_dim);
-#define SEQ_ATTN_X3(DIM)                                                                                          \
-  seq_attention_x3_kernel<DIM><<<grid, 256, 0, stream>>>(q, kh, kl, vth, vtl, bias, mask, g, sh, heads, inf, rscale, \
-                                                         vec, out)
+#define SEQ_ATTN_X3(DIM)                                                                                       \
+  seq_attention_x3_kernel<DIM><<<grid, 256, 0, stream>>>(q, kh, kl, vth, vtl, bias, mask, g, sh, heads, batch, \
+                                                         inf, rscale, vec, out)
   if (head_dim == 24) SEQ_ATTN_X3(24);
   else if (head_dim == 32) SEQ_ATTN_X3(32);
   else SEQ_ATTN_X3(48);
@@ -629,8 +656,8 @@ int bmx_seq_attention_batched_fwd(const float* q, const float* k, const float* v
 int bmx_seq_attention_windowed_fwd(const float* q, const float* k, const float* v, const float* bias,
                                    const float* mask, const float* g, int64_t batch, int64_t nq, int64_t nk,
                                    int64_t ldq, int64_t ldk, int64_t windows, int64_t key_offset,
-                                   int64_t bias_group, int64_t sbias, int64_t sbias_h, int64_t sbias_q,
-                                   int64_t sbias_k, int heads, int head_dim, float inf, float* out,
+                                   int64_t bias_group, int64_t sbias_group, int64_t sbias, int64_t sbias_h,
+                                   int64_t sbias_q, int64_t sbias_k, int heads, int head_dim, float inf, float* out,
                                    hipStream_t stream) {
   BMX_REQUIRE(batch >= 0 && batch <= 65535, "bmx_seq_attention_windowed_fwd: batch must be in [0, 65535]");
   BMX_REQUIRE(nq >= 1 && nq <= 4096 && nk >= 1 && nk <= 4096,
@@ -648,13 +675,15 @@ int bmx_seq_attention_windowed_fwd(const float* q, const float* k, const float* 
               "sees its own queries)");
   BMX_REQUIRE(bias_group >= 1 && bias_group % windows == 0,
               "bmx_seq_attention_windowed_fwd: bias_group must be a positive multiple of windows");
-  BMX_REQUIRE(sbias >= 0 && sbias_h >= 0 && sbias_q >= 1 && sbias_k >= 0 && bias_group <= (1 << 30),
+  BMX_REQUIRE(sbias_group >= 0 && sbias >= 0 && sbias_h >= 0 && sbias_q >= 1 && sbias_k >= 0 &&
+                  bias_group <= (1 << 30),
               "bmx_seq_attention_windowed_fwd: bias strides must be >= 0 (the query stride >= 1)");
   BMX_REQUIRE(inf > 0.f, "bmx_seq_attention_windowed_fwd: inf must be positive");
   if (batch == 0) return BMX_OK;
   BMX_REQUIRE(q && k && v && bias && mask && g && out, "bmx_seq_attention_windowed_fwd: null pointer");
   SeqAttnShape sh{(int)nq, (int)nk, (int)bias_group, ldq, ldk, nq * ldq, nq * ldk, sbias, nq};
   sh.bwin = (int)windows;
+  sh.sbg = sbias_group;
   sh.sbh = sbias_h;
   sh.sbq = sbias_q;
   sh.sbk = sbias_k;

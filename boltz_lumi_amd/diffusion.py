@@ -24,20 +24,26 @@ import torch
 from . import ops
 from ._guards import autocast_off, gfx950_tensor, inference
 from .atom_conditioning import atom_conditioning_cache
-from .pair_bias import prepare_token_bias, windowed_attention, windowed_ok
+from .pair_bias import prepare_token_bias, prepare_window_bias, window_bias_prepared, windowed_attention, windowed_ok
 
 
 def optimized_sample(self, *args, **kwargs):
     """Drop-in for ``AtomDiffusion.sample`` (reference diffusion.py:13-23): in
     inference the token transformer's fixed bias is packed head-major once
     (``prepare_token_bias``, so each layer's attention reads a dense slice),
-    and with one sample of one structure the atom conditioning projections are
-    memoised for the call (``atom_conditioning_cache``)."""
+    the atom encoder's and decoder's window biases channel-major
+    (``prepare_window_bias``; beyond the reference), and with one sample of one
+    structure the atom conditioning projections are memoised for the call
+    (``atom_conditioning_cache``)."""
     sample = type(self).sample
     if torch.is_grad_enabled() or self.training or "diffusion_conditioning" not in kwargs:
         return sample(self, *args, **kwargs)
     conditioning = dict(kwargs["diffusion_conditioning"])
     conditioning["token_trans_bias"] = prepare_token_bias(conditioning["token_trans_bias"])
+    for name in ("atom_enc_bias", "atom_dec_bias"):
+        value = conditioning.get(name)
+        if isinstance(value, torch.Tensor) and value.dim() == 5 and value.is_cuda:
+            conditioning[name] = prepare_window_bias(value)
     kwargs["diffusion_conditioning"] = conditioning
     single = kwargs.get("multiplicity", 1) == 1 and conditioning["c"].shape[0] == 1
     with atom_conditioning_cache(self.score_model) if single else nullcontext():
@@ -393,6 +399,8 @@ def atom_transformer_forward(self, q, c, bias, to_keys, mask, multiplicity=1, *a
     if koff is None:
         return type(self).forward(self, q, c, bias, to_keys, mask, multiplicity, *args, **kwargs)
     keys = _WindowKeys(nw, koff, multiplicity * nw, mask.float().reshape(-1).contiguous())
+    if not window_bias_prepared(bias):
+        bias = prepare_window_bias(bias)
     heads = bias.shape[4] // len(layers)
     side = _Side(cw)
     a = qw

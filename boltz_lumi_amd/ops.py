@@ -756,24 +756,24 @@ def seq_attention_windowed(q, k, v, bias, mask, g, inf, *, windows, key_offset, 
     rows, rows at one stride), mask [E * W] (the atom mask).  Window e reads
     key j from atom row e * W + key_offset + j of its sample; keys past the
     sample's ends are zero keys and values with mask 0 (upstream's zero rows of
-    single_to_keys).  bias [Eb, W, NK, H] or [Eb / windows, windows, W, NK, H]
-    in any strides (one layer's heads of the atom bias, in place); window e
-    uses bias element (e // bias_group) * windows + e % windows.  Returns a
+    single_to_keys).  bias [B, windows, W, NK, H] (or [B * windows, W, NK, H])
+    in any strides (one layer's heads of the atom bias, in place): window e
+    uses window e % windows of structure e // bias_group.  Returns a
     contiguous fp32 [E, W, H * D]."""
     _cuda(q, k, v, bias, mask, g)
-    if bias.dim() == 5:
-        _check(bias.shape[0] <= 1 or bias.stride(0) == bias.shape[1] * bias.stride(1), "bias windows must collapse")
-        bias = bias.flatten(0, 1) if bias.shape[0] > 1 else bias[0]
-    _check(q.dim() == 3 and bias.dim() == 4 and k.dim() == 2 and mask.dim() == 1, "expected 3-d q, 2-d k, 4-d bias")
+    if bias.dim() == 4:  # [Eb, W, NK, H]: structures of ``windows`` consecutive elements
+        _check(bias.shape[0] % windows == 0, "bias elements must be whole structures")
+        bias = bias.unflatten(0, (bias.shape[0] // windows, windows))
+    _check(q.dim() == 3 and bias.dim() == 5 and k.dim() == 2 and mask.dim() == 1, "expected 3-d q, 2-d k, 5-d bias")
     e, w, width = q.shape
-    nk, heads = bias.shape[2], bias.shape[3]
+    nk, heads = bias.shape[3], bias.shape[4]
     _check(width % heads == 0 and width // heads in (24, 32, 48), "expected H heads of 24, 32 or 48 dims")
     _check(g.shape == q.shape and g.stride() == q.stride() and q.stride(2) == 1 and q.stride(0) == w * q.stride(1),
            "q / g must be [E, W, H * D] windows with dense rows, sharing strides")
     _check(k.shape == (e * w, width) and v.shape == k.shape and k.stride() == v.stride() and k.stride(1) == 1,
            "k / v must be [E * W, H * D] with dense rows, sharing strides")
     _check(mask.shape == (e * w,) and mask.is_contiguous() and mask.dtype == torch.float32, "mask must be fp32 [E * W]")
-    _check(bias.dtype == torch.float32 and bias.shape[1] == w and bias.shape[0] * bias_group == e * windows
+    _check(bias.dtype == torch.float32 and tuple(bias.shape[1:3]) == (windows, w) and bias.shape[0] * bias_group == e
            and e % windows == 0 and bias_group % windows == 0, "bias does not match the windows")
     for t in (q, k, v, g):
         _check(t.dtype == torch.float32, "expected fp32 q / k / v / g")
@@ -781,8 +781,8 @@ def seq_attention_windowed(q, k, v, bias, mask, g, inf, *, windows, key_offset, 
     if e:
         N.call("bmx_seq_attention_windowed_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(),
                mask.data_ptr(), g.data_ptr(), e, w, nk, q.stride(1), k.stride(0), windows, key_offset, bias_group,
-               bias.stride(0), bias.stride(3), bias.stride(1), bias.stride(2), heads, width // heads, float(inf),
-               out.data_ptr(), _stream(q))
+               bias.stride(0), bias.stride(1), bias.stride(4), bias.stride(2), bias.stride(3), heads, width // heads,
+               float(inf), out.data_ptr(), _stream(q))
     return out
 
 

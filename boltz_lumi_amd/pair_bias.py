@@ -36,6 +36,27 @@ def prepare_token_bias(value: torch.Tensor) -> torch.Tensor:
     return dense.movedim(1, -1)
 
 
+def prepare_window_bias(value: torch.Tensor) -> torch.Tensor:
+    """The atom transformer's window bias, logically [B, K, W, H, layers * heads]
+    (values unchanged, fp32), stored channel-major: every head's [K, W, H] block
+    is dense, so a layer's heads (``value[..., l*heads:(l+1)*heads]``) give the
+    windowed attention 16-byte bias rows.  Like ``prepare_token_bias`` for the
+    token transformer; done once per sampling call, or per stack call where the
+    bias arrives in upstream's layout."""
+    dense = torch.empty((value.shape[0], value.shape[4]) + tuple(value.shape[1:4]), device=value.device,
+                        dtype=torch.float32)
+    dense.copy_(value.movedim(-1, 1))
+    return dense.movedim(1, -1)
+
+
+def window_bias_prepared(value: torch.Tensor) -> bool:
+    """``value`` has the layout ``prepare_window_bias`` writes."""
+    if value.dim() != 5 or value.dtype != torch.float32:
+        return False
+    _, k, w, h, _ = value.shape
+    return value.stride()[1:] == (w * h, h, 1, k * w * h)
+
+
 def _joint_projection(module, name, x, linears):
     """``cat([lin(x) for lin in linears], -1)`` as one GEMM (fp32 result) with the
     concatenated weights cached on ``module``: in the autocast dtype under

@@ -253,18 +253,19 @@ int bmx_seq_attention_batched_fwd(const float* q, const float* k, const float* v
  * b * nq .. of q, g (row stride ldq) and reads key j from row b * nq + key_offset + j of k, v (row
  * stride ldk; k, v projected on the atom rows, batch * nq rows) and mask ([batch * nq], the atom
  * mask), present only while 0 <= (b % windows) * nq + key_offset + j < windows * nq; an absent key
- * is a zero key / value row with mask 0, as the zero rows single_to_keys writes.  The bias of
- * element b is element (b / bias_group) * windows + b % windows (upstream repeat_interleave of the
- * per-structure window bias over the samples: bias_group = samples * windows) at element / head /
- * query / key strides sbias, sbias_h, sbias_q (>= 1), sbias_k (any layout, e.g. one layer's heads of
- * the [B, windows, nq, nk, layers * heads] atom bias in place).  out [batch][nq][heads * D]
+ * is a zero key / value row with mask 0, as the zero rows single_to_keys writes.  Element b reads
+ * the bias of window b % windows of structure b / bias_group (upstream repeat_interleave of the
+ * per-structure window bias over the samples: bias_group = samples * windows) at structure /
+ * window / head / query / key strides sbias_group, sbias, sbias_h, sbias_q (>= 1), sbias_k (any
+ * layout, e.g. one layer's heads of the [B, windows, nq, nk, layers * heads] atom bias in place or
+ * stored channel-major).  out [batch][nq][heads * D]
  * contiguous.  Replaces AttentionPairBias.forward's attention with upstream's to_keys
  * (pair_bias.py:21-36; the keys that transformersv2.AtomTransformer gathers). */
 int bmx_seq_attention_windowed_fwd(const float* q, const float* k, const float* v, const float* bias,
                                    const float* mask, const float* g, int64_t batch, int64_t nq, int64_t nk,
                                    int64_t ldq, int64_t ldk, int64_t windows, int64_t key_offset,
-                                   int64_t bias_group, int64_t sbias, int64_t sbias_h, int64_t sbias_q,
-                                   int64_t sbias_k, int heads, int head_dim, float inf, float* out,
+                                   int64_t bias_group, int64_t sbias_group, int64_t sbias, int64_t sbias_h,
+                                   int64_t sbias_q, int64_t sbias_k, int heads, int head_dim, float inf, float* out,
                                    bmx_stream_t stream);
 
 /* bmx_seq_attention_batched_fwd with both products on bf16 MFMA, each operand split into bf16 high

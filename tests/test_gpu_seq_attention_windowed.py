@@ -4,10 +4,12 @@ gathered through the oracle's single_to_keys / get_indexing_matrix (upstream
 encodersv2, zero rows past the ends), the per-structure window bias repeated
 over the samples (upstream repeat_interleave) and read in place as one
 layer's heads of the [B, windows, W, H, layers * heads] atom bias, the key
-mask gathered the same way (pair_bias.py:21-36 math).  Cases: first and last
-windows with absent keys, padded atoms at the end of a sample (a window whose
-keys are all masked), two structures with two samples each, head widths 24,
-32 and 48.  Also the to_keys probe that gates the path."""
+mask gathered the same way (pair_bias.py:21-36 math).  Cases: the bias in
+upstream's layout and channel-major (prepare_window_bias), first and last
+windows with absent keys, padded atoms at the end of a sample (every window
+keeps a valid key: a fully masked row's softmax of -1e6-shifted logits is
+quantised by fp32 in upstream too), two structures with two samples each, head
+widths 24, 32 and 48.  Also the to_keys probe that gates the path."""
 
 import functools
 
@@ -15,6 +17,7 @@ import pytest
 import torch
 
 from boltz_lumi_amd import diffusion, ops
+from boltz_lumi_amd.pair_bias import prepare_window_bias, window_bias_prepared
 from oracle import boltz_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -39,16 +42,18 @@ def reference(q, k, v, bias5, mask, g, index, w, h, mult, heads, layer, inf):
     return torch.sigmoid(g.double()) * o
 
 
-CASES = [  # structures, samples each, atoms, heads, head dim, padded atoms at the end
-    (1, 2, 8 * 32, 4, 32, 0),
-    (2, 2, 6 * 32, 4, 32, 40),
-    (1, 3, 5 * 32, 2, 24, 7),
-    (1, 1, 4 * 32, 2, 48, 0),
+CASES = [  # structures, samples each, atoms, heads, head dim, padded atoms at the end, bias channel-major
+    (1, 2, 8 * 32, 4, 32, 0, True),
+    (1, 2, 8 * 32, 4, 32, 0, False),
+    (2, 2, 6 * 32, 4, 32, 40, True),
+    (2, 2, 6 * 32, 4, 32, 40, False),
+    (1, 3, 5 * 32, 2, 24, 7, True),
+    (1, 1, 4 * 32, 2, 48, 0, False),
 ]
 
 
-@pytest.mark.parametrize("structures,mult,n,heads,d,pad", CASES)
-def test_windowed_attention_matches_gathered_fp64(gpu, structures, mult, n, heads, d, pad):
+@pytest.mark.parametrize("structures,mult,n,heads,d,pad,prepared", CASES)
+def test_windowed_attention_matches_gathered_fp64(gpu, structures, mult, n, heads, d, pad, prepared):
     w, h, layers, layer, inf = 32, 128, 3, 1, 1e6
     g_ = torch.Generator().manual_seed(n + heads + pad)
     b, nw, width = structures * mult, n // 32, heads * d
@@ -63,6 +68,9 @@ def test_windowed_attention_matches_gathered_fp64(gpu, structures, mult, n, head
     want = reference(q.reshape(e, w, width), k, v, bias5, mask, g.reshape(e, w, width), index, w, h, mult, heads,
                      layer, inf)
     pd, bd, md = proj.to(gpu), bias5.to(gpu), mask.reshape(-1).to(gpu)
+    if prepared:  # the layout optimized_sample hands the atom transformers
+        bd = prepare_window_bias(bd)
+        assert window_bias_prepared(bd) and torch.equal(bd, bias5.to(gpu))
     qd, kd, vd, gd = pd.split(width, dim=-1)
     with torch.inference_mode():
         got = ops.seq_attention_windowed(qd.view(e, w, width), kd, vd, bd[..., layer * heads:(layer + 1) * heads], md,
