@@ -300,15 +300,18 @@ int launch_seq_attention(const char* name, const float* q, const float* k, const
 // [b][h][d][key'], keys padded with zeros to a multiple of the 64-key stage
 // and, in V^T, permuted inside each 32-key block into the order in which a
 // lane holds P: slot 8 gi + e of a block holds key 4 gi + e (e < 4) or
-// 16 + 4 gi + e - 4.  A block serves 64 queries of one head (16 per wave) and
+// 16 + 4 gi + e - 4; and each key's additive mask term (1 - mask) * -inf as
+// fp32 [b][key'], -infinity past nk, so that a logit is (q.k / sqrt(D) +
+// bias) + term with no per-key select.  A block serves 64 queries of one head (16 per wave) and
 // walks the keys in 64-key stages that LDS DMA copies into a double-buffered
 // LDS stage shared by the four waves (K tiles dense, V^T rows of 64 slots with
 // their 16-byte chunks XOR-swizzled by d & 7), so each K / V element is read
 // from L2 once per 64 queries.  v_mfma_f32_16x16x32_bf16 (lane l, gi = l / 16:
 // A holds A[l%16][8 gi .. 8 gi + 7], B holds B[8 gi .. 8 gi + 7][l%16], D
 // register r holds D[4 gi + r][l%16]); per stage and wave:
-//   S^T[key][q] = K Q^T         four 16-key tiles, ceil(D / 32) k steps of 32
-//                               dims (dims past D are zero), 3 terms;
+//   S^T[key][q] = K Q^T         four 16-key tiles, k steps of 32 dims (a last
+//                               step of 16 dims on v_mfma_f32_16x16x16_bf16 for
+//                               D = 48; dims past D are zero), 3 terms;
 //   O^T[d][q] += V^T P^T        two 32-key k steps per 16-dim tile, 3 terms,
 //                               P^T from the lane's probabilities.
 constexpr int kX3Stage = 64;  // keys per LDS stage
@@ -324,13 +327,20 @@ __device__ __forceinline__ int x3_slot(int key_in_block) {
 // V[b][kb*32 + e][c] for the block's 32 keys (zeros past nk).
 __global__ __launch_bounds__(256) void seq_attn_split_kernel(const float* __restrict__ k, const float* __restrict__ v,
                                                              int nk, int64_t ldk, int64_t sk, int heads, int d,
+                                                             const float* __restrict__ mask, int64_t smask, float inf,
                                                              bf16* __restrict__ kh, bf16* __restrict__ kl,
-                                                             bf16* __restrict__ vth, bf16* __restrict__ vtl) {
+                                                             bf16* __restrict__ vth, bf16* __restrict__ vtl,
+                                                             float* __restrict__ mterm) {
   const int hd = heads * d;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= hd) return;
-  const int kb = blockIdx.y, hh = c / d, dd = c % d;
+  const int kb = blockIdx.y;
   const int64_t b = blockIdx.z, nkp = x3_nkp(nk);
+  if (blockIdx.x == 0 && threadIdx.x < 32) {  // the additive mask term of key kb * 32 + lane; -inf past nk
+    const int key = kb * 32 + threadIdx.x;
+    mterm[b * nkp + key] = key < nk ? (1.f - mask[b * smask + key]) * -inf : -INFINITY;
+  }
+  if (c >= hd) return;
+  const int hh = c / d, dd = c % d;
   const float* kb_src = k + b * sk + c;
   const float* vb_src = v + b * sk + c;
   bf16* kh_dst = kh + ((b * heads + hh) * nkp) * d + dd;
@@ -360,6 +370,11 @@ __global__ __launch_bounds__(256) void seq_attn_split_kernel(const float* __rest
   }
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f32x4 mfma16bf_k16(bf16x4 a, bf16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c, 0,
+                                                   0, 0);
+}
 __device__ __forceinline__ f32x4 mfma16bf(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -377,12 +392,13 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
                                                                const bf16* __restrict__ kh, const bf16* __restrict__ kl,
                                                                const bf16* __restrict__ vth,
                                                                const bf16* __restrict__ vtl,
+                                                               const float* __restrict__ mterm,
                                                                const float* __restrict__ bias,
-                                                               const float* __restrict__ mask,
                                                                const float* __restrict__ g, SeqAttnShape sh, int heads,
-                                                               int64_t batch, float inf, float rscale, bool vec,
+                                                               int64_t batch, float rscale, bool vec,
                                                                float* __restrict__ out) {
-  constexpr int DK = (D + 31) / 32;              // QK^T k steps
+  constexpr bool T16 = D % 32 == 16;             // the last 16 dims on a K = 16 MFMA
+  constexpr int DK = T16 ? D / 32 : (D + 31) / 32;  // QK^T k steps of 32 dims
   constexpr int DT = (D + 15) / 16;              // O^T d tiles
   constexpr int kTile = kX3Stage * D * 2;        // bytes of one K (or V^T) tile, hi or lo
   constexpr int kStage = 4 * kTile;              // K hi, K lo, V^T hi, V^T lo
@@ -408,7 +424,7 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
   q += b * sh.sq;
   g += b * sh.sq;
   bias += (b / sh.bdiv) * sh.sbias;
-  mask += b * sh.smask;
+  mterm += b * nkp;
   out += b * nq * HD;
   const bf16* k_src[2] = {kh + (b * heads + h) * nkp * D, kl + (b * heads + h) * nkp * D};
   const bf16* v_src[2] = {vth + (b * heads + h) * D * nkp, vtl + (b * heads + h) * D * nkp};
@@ -457,6 +473,13 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
       ql[ks][e] = (bf16)(x - (float)qh[ks][e]);
     }
   }
+  bf16x4 qh4, ql4;  // dims 32 DK + 4 gi .. + 3 (T16)
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float x = T16 ? q[(int64_t)qc * ldq + h * D + 32 * DK + 4 * gi + e] : 0.f;
+    qh4[e] = (bf16)x;
+    ql4[e] = (bf16)(x - (float)qh4[e]);
+  }
   const float* brow = bias + ((int64_t)h * nq + qc) * nk;
   const bf16x8 zero8 = {};
   f32x4 o[DT];
@@ -490,22 +513,25 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
         acc = mfma16bf(ah, ql[ks], acc);
         acc = mfma16bf(al, qh[ks], acc);
       }
+      if (T16) {
+        const int off = ((16 * t + c) * D + 32 * DK + 4 * gi) * 2;
+        const bf16x4 ah = *(const bf16x4*)(sb + off), al = *(const bf16x4*)(sb + kTile + off);
+        acc = mfma16bf_k16(ah, qh4, acc);
+        acc = mfma16bf_k16(ah, ql4, acc);
+        acc = mfma16bf_k16(al, qh4, acc);
+      }
       const int kb = key0 + 16 * t + 4 * gi;  // this lane's keys kb .. kb + 3
-      f32x4 b4, m4;
+      f32x4 b4;
       if (full) {
         b4 = *(const f32x4*)(brow + kb);
-        m4 = *(const f32x4*)(mask + kb);
       } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          b4[r] = brow[min(kb + r, nk - 1)];
-          m4[r] = mask[min(kb + r, nk - 1)];
-        }
+        for (int r = 0; r < 4; ++r) b4[r] = brow[min(kb + r, nk - 1)];
       }
+      const f32x4 m4 = *(const f32x4*)(mterm + kb);  // (1 - mask) * -inf, -inf past nk
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float x = (acc[r] * rscale + b4[r]) + (1.f - m4[r]) * -inf;
-        sc[t][r] = kb + r < nk ? x : -INFINITY;
+        sc[t][r] = (acc[r] * rscale + b4[r]) + m4[r];
         tmax = fmaxf(tmax, sc[t][r]);
       }
     }
@@ -563,7 +589,7 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
 
 size_t x3_workspace_bytes(int64_t batch, int64_t nk, int heads, int head_dim) {
   const size_t tile = (size_t)(batch * heads * head_dim * x3_nkp(nk)) * sizeof(bf16);  // K and V^T alike
-  return 4 * ((tile + 255) / 256 * 256);
+  return 4 * ((tile + 255) / 256 * 256) + (size_t)(batch * x3_nkp(nk)) * sizeof(float);
 }
 
 int launch_seq_attention_x3(const char* name, const float* q, const float* k, const float* v, const float* bias,
@@ -575,17 +601,18 @@ int launch_seq_attention_x3(const char* name, const float* q, const float* k, co
   bf16* kl = (bf16*)((char*)ws + tile);
   bf16* vth = (bf16*)((char*)ws + 2 * tile);
   bf16* vtl = (bf16*)((char*)ws + 3 * tile);
+  float* mterm = (float*)((char*)ws + 4 * tile);
   const dim3 sgrid((unsigned)((hd + 255) / 256), (unsigned)(nkp / 32), (unsigned)batch);
-  seq_attn_split_kernel<<<sgrid, 256, 0, stream>>>(k, v, sh.nk, sh.ldk, sh.sk, heads, head_dim, kh, kl, vth, vtl);
+  seq_attn_split_kernel<<<sgrid, 256, 0, stream>>>(k, v, sh.nk, sh.ldk, sh.sk, heads, head_dim, mask, sh.smask, inf,
+                                                    kh, kl, vth, vtl, mterm);
   if (int rc = check_launch(name)) return rc;
-  const bool vec = sh.nk % 4 == 0 && sh.sbias % 4 == 0 && sh.smask % 4 == 0 && (uintptr_t)bias % 16 == 0 &&
-                   (uintptr_t)mask % 16 == 0;
+  const bool vec = sh.nk % 4 == 0 && sh.sbias % 4 == 0 && (uintptr_t)bias % 16 == 0;  // 16-byte bias rows
   const int64_t items = (batch + sh.bdiv - 1) / sh.bdiv * sh.bdiv * heads * ((sh.nq + kX3Q - 1) / kX3Q);
   const dim3 grid((unsigned)(8 * ((items + 7) / 8)));
   const float rscale = 1.f / sqrtf((float)head_dim);
 #define SEQ_ATTN_X3(DIM)                                                                                       \
-  seq_attention_x3_kernel<DIM><<<grid, 256, 0, stream>>>(q, kh, kl, vth, vtl, bias, mask, g, sh, heads, batch, \
-                                                         inf, rscale, vec, out)
+  seq_attention_x3_kernel<DIM><<<grid, 256, 0, stream>>>(q, kh, kl, vth, vtl, mterm, bias, g, sh, heads, batch, \
+                                                         rscale, vec, out)
   if (head_dim == 24) SEQ_ATTN_X3(24);
   else if (head_dim == 32) SEQ_ATTN_X3(32);
   else SEQ_ATTN_X3(48);

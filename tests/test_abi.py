@@ -42,8 +42,9 @@ def test_workspace_queries(lib):
     assert lib.bmx_triattn_workspace_bytes(1024) > 3 * 1024 * 1024 * 128 * 2
     assert lib.bmx_triattn_proj_rows() == 3 * 128 + 32
     # split K (hi, lo) and split V^T (hi, lo), keys padded to the 64-key stage: 5 x 1024 x 768 -> 4 x 7.5 MiB
-    assert lib.bmx_seq_attention_x3_workspace_bytes(5, 1024, 16, 48) == 4 * 5 * 1024 * 768 * 2
-    assert lib.bmx_seq_attention_x3_workspace_bytes(1, 17, 4, 32) == 4 * 64 * 128 * 2
+    # K hi / lo and V^T hi / lo (bf16, keys padded to 64, 256-byte aligned) and the fp32 mask terms
+    assert lib.bmx_seq_attention_x3_workspace_bytes(5, 1024, 16, 48) == 4 * 5 * 1024 * 768 * 2 + 5 * 1024 * 4
+    assert lib.bmx_seq_attention_x3_workspace_bytes(1, 17, 4, 32) == 4 * 64 * 128 * 2 + 64 * 4
     assert lib.bmx_seq_attention_x3_workspace_bytes(0, 17, 4, 32) == 0
 
 
