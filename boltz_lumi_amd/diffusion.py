@@ -1,17 +1,20 @@
-"""Diffusion AdaLN / conditioned-transition forwards patched onto the score
-model, and the ``structure_module.sample`` wrapper.
+"""Diffusion forwards patched onto the score model (AdaLN, conditioned
+transition, transformer layer, transformer stack, atom transformer) and the
+``structure_module.sample`` wrapper.
 
 Reference: src/boltz_lumi/diffusion.py (optimized_sample :13-23, adaln_forward
 :52-57, transition_forward :60-68, eligibility :37-49).  As in the reference the
-AdaLN / transition forwards run in fp32 with autocast off.  AdaLN's a_norm + sigmoid(s_scale) modulation
-+ s_bias become one LN/modulate kernel; the SwiGLU gate and the output gate
-are fused epilogues.  The conditioning projections are still called as
-submodules while ``atom_conditioning_cache`` memoises them (reference
-atom_conditioning.py:12-45); otherwise they and the projections of the
-activation a (swish_gate, a_to_b, b_to_a), all fp32 hipBLASLt GEMMs in the
-reference, run as split-bf16 GEMMs with fp32 accumulation from 512 input
-channels up (``ops.linear_fp32``, about 2^-16 relative per product).  Guard failures call
-the class forward.
+forwards run in fp32 with autocast off.  AdaLN's a_norm + sigmoid(s_scale)
+modulation + s_bias is one LN/modulate kernel; the SwiGLU gate and the output
+gates are fused epilogues.  Beyond the reference, a DiffusionTransformer builds
+the operands of its conditioning s once per call and each layer runs its six
+conditioning projections as two GEMMs (LayerNorm(s) with the s_norm affines
+folded into the weights, and s), and an AtomTransformer reads its key windows
+by address instead of gathering them.  Memoised (``atom_conditioning_cache``,
+reference atom_conditioning.py:12-45) or hooked projections are called as
+submodules.  The linears, fp32 hipBLASLt GEMMs in the reference, run as
+split-bf16 GEMMs with fp32 accumulation from 512 input channels up (about 2^-16
+relative per product).  Guard failures call the class forward.
 """
 
 from __future__ import annotations
