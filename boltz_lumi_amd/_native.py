@@ -37,6 +37,8 @@ SIGNATURES = {
     "bmx_layernorm_split3_bf16": (c_int, [_P, c_int64, c_int, c_int64, c_float, _P, _P]),
     "bmx_adaln_split3_bf16": (c_int, [_P, _P, _P, c_int64, c_int64, c_int, c_float, _P, _P]),
     "bmx_swiglu_split3_bf16": (c_int, [_P, c_int64, c_int64, c_int64, _P, _P]),
+    "bmx_gated_residual_adaln_split3_bf16": (c_int, [_P, _P, c_int64, _P, _P, _P, _P, c_int64, c_int64, c_int, c_float,
+                                                     _P, _P]),
     "bmx_adaln_strided": (c_int, [_P, _P, _P, c_int64, _P, c_int, c_int64, c_int, c_float, _P]),
     "bmx_gated_residual": (c_int, [_P, _P, c_int64, _P, _P, c_int64, c_int64, _P]),
     "bmx_diffusion_epilogue": (c_int, [c_int, _P, _P, _P, _P, c_int, c_int64, c_int64, _P]),

@@ -19,6 +19,8 @@
 //  bmx_layernorm_split3_bf16  LayerNorm without affine of x    -> operand
 //  bmx_adaln_split3_bf16      sigmoid(scale) * LN(a) + shift    -> operand
 //  bmx_swiglu_split3_bf16     silu(g) * x * b of one projection -> operand
+//  bmx_gated_residual_adaln_split3_bf16  c + sigmoid(g) * a -> out, and the AdaLN
+//                             operand of that new row
 //
 // None has a reference counterpart: the reference leaves these fp32 linears
 // and the passes in front of them to torch (diffusion.py:52-68,
@@ -141,6 +143,52 @@ __global__ __launch_bounds__(256) void adaln_split3_kernel(const float* __restri
   put_tail(o, d, lane);
 }
 
+// The residual update of a diffusion layer and the next AdaLN in one pass:
+// r = c + sigmoid(g) * a (the MODULATION epilogue; g and the modulation rows at
+// strides ldg / ldm) is written to out (which may alias c), then the operand
+// row of sigmoid(scale) * LN(r) + shift, rounded as bmx_adaln_split3_bf16.
+__global__ __launch_bounds__(256) void gated_residual_adaln_split3_kernel(
+    const float* __restrict__ a, const float* __restrict__ g, int64_t ldg, const float* c, float* out,
+    const float* __restrict__ scale, const float* __restrict__ shift, int64_t ldm, bf16* __restrict__ op,
+    int64_t rows, int d, float eps) {
+#pragma clang fp contract(off)
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63, chunks = d >> 2;
+  f32x4 v[kRowChunks], sc[kRowChunks], sh[kRowChunks];
+#pragma unroll
+  for (int u = 0; u < kRowChunks; ++u) {
+    const int col = 4 * min(lane + kWave * u, chunks - 1);
+    const f32x4 av = load4(a + row * d + col), gv = load4(g + row * ldg + col), cv = load4(c + row * d + col);
+    sc[u] = load4(scale + row * ldm + col);
+    sh[u] = load4(shift + row * ldm + col);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float prod = sigmoid_f(gv[e]) * av[e];
+      v[u][e] = prod + cv[e];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kRowChunks; ++u)
+    if (lane + kWave * u < chunks) store4(out + row * d + 4 * (lane + kWave * u), v[u]);
+  const RowNorm n = row_norm(v, lane, chunks, d, eps);
+  bf16* o = op + row * (3 * (int64_t)d + kTail);
+#pragma unroll
+  for (int u = 0; u < kRowChunks; ++u) {
+    if (lane + kWave * u < chunks) {
+      f32x4 r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float an = (v[u][e] - n.mean) * n.inv;
+        const float prod = sigmoid_f(sc[u][e]) * an;
+        r[e] = prod + sh[u][e];
+      }
+      put_split(o, d, 4 * (lane + kWave * u), r);
+    }
+  }
+  put_tail(o, d, lane);
+}
+
 // Row r of u holds [x | g | b] (3 cols values at stride ldu): the swish gate's
 // two halves and the a_to_b projection of the conditioned transition.  The
 // operand row is silu(g) * x * b, rounded as the GATED_SWIGLU epilogue.
@@ -211,6 +259,26 @@ int bmx_adaln_split3_bf16(const float* a, const float* scale, const float* shift
               "bmx_adaln_split3_bf16: a, scale, shift must be 16-byte and out 8-byte aligned");
   adaln_split3_kernel<<<row_blocks(rows), 256, 0, stream>>>(a, scale, shift, ld_mod, (bf16*)out, rows, dim, eps);
   return check_launch("bmx_adaln_split3_bf16");
+}
+
+int bmx_gated_residual_adaln_split3_bf16(const float* a, const float* gate, int64_t ld_gate, const float* c,
+                                         float* out, const float* scale, const float* shift, int64_t ld_mod,
+                                         int64_t rows, int dim, float eps, void* op, hipStream_t stream) {
+  BMX_REQUIRE(rows >= 0 && dim > 0 && dim % 4 == 0 && dim <= 4 * kWave * kRowChunks && ld_gate >= dim &&
+                  ld_gate % 4 == 0 && ld_mod >= dim && ld_mod % 4 == 0,
+              "bmx_gated_residual_adaln_split3_bf16: need 0 < dim <= 1024, dim %% 4 == 0, ld_gate and ld_mod >= dim "
+              "and multiples of 4");
+  BMX_REQUIRE(eps > 0.f, "bmx_gated_residual_adaln_split3_bf16: eps must be positive");
+  BMX_REQUIRE(rows < (int64_t)1 << 33, "bmx_gated_residual_adaln_split3_bf16: too many rows");
+  if (rows == 0) return BMX_OK;
+  BMX_REQUIRE(a && gate && c && out && scale && shift && op, "bmx_gated_residual_adaln_split3_bf16: null pointer");
+  BMX_REQUIRE(((uintptr_t)a | (uintptr_t)gate | (uintptr_t)c | (uintptr_t)out | (uintptr_t)scale | (uintptr_t)shift) %
+                      16 == 0 &&
+                  (uintptr_t)op % 8 == 0,
+              "bmx_gated_residual_adaln_split3_bf16: fp32 operands must be 16-byte and op 8-byte aligned");
+  gated_residual_adaln_split3_kernel<<<row_blocks(rows), 256, 0, stream>>>(a, gate, ld_gate, c, out, scale, shift,
+                                                                           ld_mod, (bf16*)op, rows, dim, eps);
+  return check_launch("bmx_gated_residual_adaln_split3_bf16");
 }
 
 int bmx_swiglu_split3_bf16(const float* u, int64_t ldu, int64_t rows, int64_t cols, void* out, hipStream_t stream) {

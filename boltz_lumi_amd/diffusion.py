@@ -27,7 +27,8 @@ import torch
 from . import ops
 from ._guards import autocast_off, gfx950_tensor, inference
 from .atom_conditioning import atom_conditioning_cache
-from .pair_bias import prepare_token_bias, prepare_window_bias, window_bias_prepared, windowed_attention, windowed_ok
+from .pair_bias import (attention_from_operand, operand_ok, prepare_token_bias, prepare_window_bias,
+                        window_bias_prepared, windowed_attention, windowed_ok)
 
 
 def optimized_sample(self, *args, **kwargs):
@@ -226,24 +227,39 @@ def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity, keys=N
     scale_a, shift_a, scale_t, shift_t = mods.split(d, dim=-1)
     gate_a, gate_t = gates.split(d, dim=-1)
     rows = a.reshape(-1, d)
-    b = ops.adaln_modulate(rows, scale_a, shift_a, self.adaln.a_norm.eps).view(a.shape)
-    if keys is not None:
-        att = self.pair_bias_attn
+    att = self.pair_bias_attn
+    o = None
+    if keys is None and to_keys is None and side.split and operand_ok(att):
+        # the AdaLN output only as the q | k | v | g GEMM's split operand
+        o = attention_from_operand(att, ops.adaln_split3(rows, scale_a, shift_a, self.adaln.a_norm.eps), a.shape, bias,
+                                   mask, multiplicity)
+    if o is not None:
+        b = att.proj_o(o) if "forward" in vars(att.proj_o) else ops.linear_fp32(o, att.proj_o)
+    elif keys is not None:
+        b = ops.adaln_modulate(rows, scale_a, shift_a, self.adaln.a_norm.eps).view(a.shape)
         o = windowed_attention(att, b, bias, keys)
         b = att.proj_o(o) if "forward" in vars(att.proj_o) else ops.linear_fp32(o, att.proj_o)
     else:
+        b = ops.adaln_modulate(rows, scale_a, shift_a, self.adaln.a_norm.eps).view(a.shape)
         k_in = b
         if to_keys is not None:
             k_in = to_keys(b)
             mask = to_keys(mask.unsqueeze(-1)).squeeze(-1)
         b = self.pair_bias_attn(s=b, z=bias, mask=mask, multiplicity=multiplicity, k_in=k_in)
+    t_eps = tr.adaln.a_norm.eps
+    x_op = None
     if b.shape == a.shape and b.dtype == torch.float32:
-        rows = ops.gated_residual(b.reshape(-1, d).contiguous(), gate_a, rows)
+        if side.split:  # the residual update and the transition's AdaLN operand in one pass
+            rows, x_op = ops.gated_residual_adaln_split3(b.reshape(-1, d).contiguous(), gate_a, rows, scale_t, shift_t,
+                                                         t_eps)
+        else:
+            rows = ops.gated_residual(b.reshape(-1, d).contiguous(), gate_a, rows)
     else:
         rows = (a + torch.sigmoid(gate_a).reshape(a.shape) * b).reshape(-1, d)
-    t_eps = tr.adaln.a_norm.eps
     if side.split:
-        u = ops.mm_split(ops.adaln_split3(rows, scale_t, shift_t, t_eps), ops.x3_weight(
+        if x_op is None:
+            x_op = ops.adaln_split3(rows, scale_t, shift_t, t_eps)
+        u = ops.mm_split(x_op, ops.x3_weight(
             tr, "swish_a2b_x3", (tr.swish_gate[0].weight, tr.a_to_b.weight), (tr.swish_gate[0].bias, tr.a_to_b.bias)))
         b2a = tr.b_to_a
         y = ops.mm_split(ops.swiglu_split3(u, tr.a_to_b.out_features),

@@ -288,6 +288,29 @@ def adaln_split3(a, scale, shift, eps):
     return out
 
 
+def gated_residual_adaln_split3(a, gate, c, scale, shift, eps, out=None):
+    """``r = c + sigmoid(gate) * a`` (fp32, into ``out``, which may be ``c``) and
+    the split-bf16 operand of ``sigmoid(scale) * LN_noaffine(r) + shift`` in one
+    pass (``bmx_gated_residual_adaln_split3_bf16``); gate, scale and shift may
+    be column slices.  Returns (r, operand)."""
+    _cuda(a, gate, c, scale, shift)
+    _check(a.dtype == c.dtype == torch.float32 and a.is_contiguous() and c.is_contiguous() and a.shape == c.shape,
+           "expected contiguous fp32 a and c of one shape")
+    d = a.shape[-1]
+    _check(0 < d <= 1024 and d % 4 == 0, "expected a multiple of 4 channels, at most 1024")
+    ldg = _same_rows(a, gate)
+    ldm = _same_rows(a, scale, shift)
+    if out is None:
+        out = torch.empty_like(a)
+    _check(out.shape == a.shape and out.is_contiguous() and out.dtype == torch.float32, "bad out")
+    op = _split_out(a, d)
+    rows = a.numel() // d
+    if rows:
+        N.call("bmx_gated_residual_adaln_split3_bf16", a.data_ptr(), gate.data_ptr(), ldg, c.data_ptr(), out.data_ptr(),
+               scale.data_ptr(), shift.data_ptr(), ldm, rows, d, float(eps), op.data_ptr(), _stream(a))
+    return out, op
+
+
 def swiglu_split3(u, cols):
     """Split-bf16 operand of ``silu(g) * x * b`` for rows [x | g | b | ...] of
     fp32 ``u`` (``cols`` values each; ``bmx_swiglu_split3_bf16``)."""

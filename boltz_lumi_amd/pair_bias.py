@@ -111,6 +111,14 @@ def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
     else:  # q | g on the queries and k | v on the key rows, two GEMMs whose column slices the kernel reads
         q, g = _joint_projection(module, "qg", s, (module.proj_q, module.proj_g)).split(width, dim=-1)
         k, v = _joint_projection(module, "kv", k_in, (module.proj_k, module.proj_v)).split(width, dim=-1)
+    return _attend(module, q, k, v, g, z, mask, multiplicity, bias)
+
+
+def _attend(module, q, k, v, g, z, mask, multiplicity, bias=None):
+    """The attention of ``fused_attention`` from its projections ([B, NQ / NK,
+    H * D] column slices), or None where shapes do not match."""
+    heads = module.num_heads
+    batch, nq, nk = q.shape[0], q.shape[1], k.shape[1]
     if bias is None:
         bias = module.proj_z(z)
     bias = bias.float()
@@ -124,6 +132,30 @@ def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
     if m.stride(1) != 1:
         m = m.contiguous()
     return ops.seq_attention_batched(q, k, v, bias, m, g, module.inf, bias_div=multiplicity)
+
+
+def operand_ok(module) -> bool:
+    """``attention_from_operand`` applies: a patched, unhooked AttentionPairBias
+    with a given bias, 24 / 32 / 48 dims per head, whose linears run split
+    (``ops.use_split``)."""
+    fwd = vars(module).get("forward")
+    heads, width = module.num_heads, module.c_s
+    return (getattr(fwd, "__func__", None) is prepared_forward and not module._forward_hooks
+            and not module._forward_pre_hooks and not module.compute_pair_bias and not module.training
+            and width % heads == 0 and width // heads in (24, 32, 48) and heads <= 64 and ops.use_split(width))
+
+
+def attention_from_operand(module, op, shape, z, mask, multiplicity=1):
+    """``fused_attention(module, s, z, mask, s, multiplicity)`` when the caller
+    holds s only as its split-bf16 operand ``op`` ([B * N, 3 c_s + 64], e.g.
+    the AdaLN output written by ``ops.adaln_split3``): the q | k | v | g
+    projection is one GEMM of ``op``.  ``shape`` is s's [B, N, c_s]."""
+    width = module.c_s
+    lin = (module.proj_q, module.proj_k, module.proj_v, module.proj_g)
+    w3 = ops.x3_weight(module, "qkvg_x3", tuple(m.weight for m in lin), tuple(m.bias for m in lin))
+    proj = ops.mm_split(op, w3).view(tuple(shape[:-1]) + (4 * width,))
+    q, k, v, g = proj.split(width, dim=-1)
+    return _attend(module, q, k, v, g, z, mask, multiplicity)
 
 
 def windowed_ok(module) -> bool:

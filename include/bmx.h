@@ -118,6 +118,16 @@ int bmx_adaln_split3_bf16(const float* a, const float* scale, const float* shift
  * one swish_gate|a_to_b projection, the input of b_to_a (diffusion.py:60-68). */
 int bmx_swiglu_split3_bf16(const float* u, int64_t ldu, int64_t rows, int64_t cols, void* out, bmx_stream_t stream);
 
+/* out = c + sigmoid(gate) * a (the MODULATION epilogue: a diffusion layer's gated residual
+ * update; gate rows at stride ld_gate; out may alias c), then the operand rows of
+ * sigmoid(scale) * LN_noaffine(out) + shift (scale / shift rows at stride ld_mod), as
+ * bmx_gated_residual followed by bmx_adaln_split3_bf16 in one pass: the attention's residual
+ * update and the conditioned transition's AdaLN (transformersv2 DiffusionTransformerLayer;
+ * diffusion.py:52-68). */
+int bmx_gated_residual_adaln_split3_bf16(const float* a, const float* gate, int64_t ld_gate, const float* c,
+                                         float* out, const float* scale, const float* shift, int64_t ld_mod,
+                                         int64_t rows, int dim, float eps, void* op, bmx_stream_t stream);
+
 /* P = softmax(round(round(S + mask) + bias)) over the last axis, rounding to dtype.
  * shape = {B, I, H, Q, K}; element strides of scores [B,I,H,Q,K], bias [B,1,H,Q,K], mask [B,I,1,1,K].
  * out is contiguous.  Replaces ordered_softmax (kernels/triangle_softmax.py:117-161) and

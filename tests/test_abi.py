@@ -106,6 +106,9 @@ def test_argument_validation_needs_no_gpu(lib):
     assert rc == N.BMX_EINVAL and b"ld_mod" in lib.bmx_last_error()
     rc = lib.bmx_gated_residual(fake, fake, 768, None, fake, 4, 768, None)
     assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
+    rc = lib.bmx_gated_residual_adaln_split3_bf16(fake, fake, 700, fake, fake, fake, fake, 768, 4, 768,
+                                                  ctypes.c_float(1e-5), fake, None)
+    assert rc == N.BMX_EINVAL and b"ld_gate" in lib.bmx_last_error()
     # windowed attention: the windows must tile the batch and see their own queries
     wargs = [fake] * 6 + [10, 32, 128, 512, 512, 4, -48, 8, 0, 0, 1, 1536, 12]
     rc = lib.bmx_seq_attention_windowed_fwd(*wargs, 4, 32, ctypes.c_float(1e6), fake, None)

@@ -98,6 +98,24 @@ def test_gated_residual_matches_modulation(gpu, rows, cols):
     assert ((want.double() - eager).abs().max() / eager.abs().max()).item() < 1e-6
 
 
+@pytest.mark.parametrize("rows,dim", [(37, 768), (5, 128), (3, 1024)])
+def test_gated_residual_adaln_split3_matches_the_two_kernels(gpu, rows, dim):
+    """One pass of the residual update and the next AdaLN operand gives the bits
+    of gated_residual followed by adaln_split3; in place (out = c) too."""
+    g = torch.Generator().manual_seed(rows * dim)
+    y, c = (torch.randn(rows, dim, generator=g).to(gpu) for _ in range(2))
+    proj = torch.randn(rows, 3 * dim, generator=g).to(gpu)  # gate | scale | shift of one projection
+    gate, scale, shift = proj.split(dim, dim=-1)
+    with torch.inference_mode():
+        r_want = ops.gated_residual(y, gate, c)
+        op_want = ops.adaln_split3(r_want, scale, shift, 1e-5)
+        r_got, op_got = ops.gated_residual_adaln_split3(y, gate, c, scale, shift, 1e-5)
+        c2 = c.clone()
+        r_in, op_in = ops.gated_residual_adaln_split3(y, gate, c2, scale, shift, 1e-5, out=c2)
+    assert torch.equal(r_got, r_want) and torch.equal(op_got, op_want)
+    assert r_in.data_ptr() == c2.data_ptr() and torch.equal(c2, r_want) and torch.equal(op_in, op_want)
+
+
 @pytest.mark.parametrize("m,k,n", [(37, 768, 4608), (5, 512, 8), (130, 1536, 768)])
 def test_split_gemm_with_folded_bias_is_near_fp32(gpu, m, k, n):
     """mm_split of a strided operand source against x3_weight of two stacked
