@@ -66,6 +66,8 @@ SIGNATURES = {
     "bmx_seq_attention_x3_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int, c_int]),
     "bmx_seq_attention_x3_batched_fwd": (c_int, [_P, _P, _P, _P, _P, _P] + [c_int64] * 10
                                          + [c_int, c_int, c_float, _P, _P, c_size_t, _P]),
+    "bmx_seq_attention_x3_batched_split_fwd": (c_int, [_P, _P, _P, _P, _P, _P] + [c_int64] * 10
+                                               + [c_int, c_int, c_float, _P, _P, c_size_t, _P]),
 }
 
 

@@ -396,7 +396,7 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
                                                                const float* __restrict__ bias,
                                                                const float* __restrict__ g, SeqAttnShape sh, int heads,
                                                                int64_t batch, float rscale, bool vec,
-                                                               float* __restrict__ out) {
+                                                               float* __restrict__ out, bf16* __restrict__ op) {
   constexpr bool T16 = D % 32 == 16;             // the last 16 dims on a K = 16 MFMA
   constexpr int DK = T16 ? D / 32 : (D + 31) / 32;  // QK^T k steps of 32 dims
   constexpr int DT = (D + 15) / 16;              // O^T d tiles
@@ -425,7 +425,7 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
   g += b * sh.sq;
   bias += (b / sh.bdiv) * sh.sbias;
   mterm += b * nkp;
-  out += b * nq * HD;
+  if (out) out += b * nq * HD;
   const bf16* k_src[2] = {kh + (b * heads + h) * nkp * D, kl + (b * heads + h) * nkp * D};
   const bf16* v_src[2] = {vth + (b * heads + h) * D * nkp, vtl + (b * heads + h) * D * nkp};
   const int l = lane_id(), gi = l >> 4, c = l & 15, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -573,6 +573,9 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
   const int i = qw + c;
   if (i < nq) {
     const float inv = 1.f / lsum;
+    // op: the row as the split-bf16 operand of the next linear, [hi | hi | lo | 1 1 0 ...]
+    // over 3 HD + 64 columns (the tail written by the head-0 blocks)
+    bf16* orow = op ? op + ((int64_t)b * nq + i) * (3 * HD + 64) : nullptr;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const int d0 = 16 * dt + 4 * gi;
@@ -581,8 +584,27 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
         f32x4 r;
 #pragma unroll
         for (int e = 0; e < 4; ++e) r[e] = sigmoid_f(gv[e]) * (o[dt][e] * inv);
-        store4(out + (int64_t)i * HD + h * D + d0, r);
+        if (orow) {
+          bf16x4 hi, lo;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            hi[e] = (bf16)r[e];
+            lo[e] = (bf16)(r[e] - (float)hi[e]);
+          }
+          *(bf16x4*)(orow + h * D + d0) = hi;
+          *(bf16x4*)(orow + HD + h * D + d0) = hi;
+          *(bf16x4*)(orow + 2 * HD + h * D + d0) = lo;
+        } else {
+          store4(out + (int64_t)i * HD + h * D + d0, r);
+        }
       }
+    }
+    if (orow && h == 0) {  // lanes gi = 0..3 write 16 tail columns each
+      bf16x8 t = {};
+      if (gi == 0) t[0] = t[1] = (bf16)1.f;
+      *(bf16x8*)(orow + 3 * HD + 16 * gi) = t;
+      t[0] = t[1] = (bf16)0.f;
+      *(bf16x8*)(orow + 3 * HD + 16 * gi + 8) = t;
     }
   }
 }
@@ -594,7 +616,7 @@ size_t x3_workspace_bytes(int64_t batch, int64_t nk, int heads, int head_dim) {
 
 int launch_seq_attention_x3(const char* name, const float* q, const float* k, const float* v, const float* bias,
                             const float* mask, const float* g, int64_t batch, const SeqAttnShape& sh, int heads,
-                            int head_dim, float inf, float* out, void* ws, hipStream_t stream) {
+                            int head_dim, float inf, float* out, bf16* op, void* ws, hipStream_t stream) {
   const int64_t hd = (int64_t)heads * head_dim, nkp = x3_nkp(sh.nk);
   const size_t tile = ((size_t)(batch * hd * nkp) * sizeof(bf16) + 255) / 256 * 256;
   bf16* kh = (bf16*)ws;
@@ -612,7 +634,7 @@ int launch_seq_attention_x3(const char* name, const float* q, const float* k, co
   const float rscale = 1.f / sqrtf((float)head_dim);
 #define SEQ_ATTN_X3(DIM)                                                                                       \
   seq_attention_x3_kernel<DIM><<<grid, 256, 0, stream>>>(q, kh, kl, vth, vtl, mterm, bias, g, sh, heads, batch, \
-                                                         rscale, vec, out)
+                                                         rscale, vec, out, op)
   if (head_dim == 24) SEQ_ATTN_X3(24);
   else if (head_dim == 32) SEQ_ATTN_X3(32);
   else SEQ_ATTN_X3(48);
@@ -754,7 +776,39 @@ int bmx_seq_attention_x3_batched_fwd(const float* q, const float* k, const float
               need, workspace_bytes);
   const SeqAttnShape sh{(int)nq, (int)nk, (int)bias_div, ldq, ldk, sq, sk, sbias, smask};
   return launch_seq_attention_x3("bmx_seq_attention_x3_batched_fwd", q, k, v, bias, mask, g, batch, sh, heads,
-                                 head_dim, inf, out, workspace, stream);
+                                 head_dim, inf, out, nullptr, workspace, stream);
+}
+
+int bmx_seq_attention_x3_batched_split_fwd(const float* q, const float* k, const float* v, const float* bias,
+                                           const float* mask, const float* g, int64_t batch, int64_t nq, int64_t nk,
+                                           int64_t ldq, int64_t ldk, int64_t sq, int64_t sk, int64_t sbias,
+                                           int64_t smask, int64_t bias_div, int heads, int head_dim, float inf,
+                                           void* out_op, void* workspace, size_t workspace_bytes,
+                                           hipStream_t stream) {
+  BMX_REQUIRE(batch >= 0 && batch <= 65535, "bmx_seq_attention_x3_batched_split_fwd: batch must be in [0, 65535]");
+  BMX_REQUIRE(nq >= 0 && nq <= (1 << 20) && nk >= 1 && nk <= (1 << 20),
+              "bmx_seq_attention_x3_batched_split_fwd: need 0 <= nq <= 2^20 and 1 <= nk <= 2^20");
+  BMX_REQUIRE(head_dim == 24 || head_dim == 32 || head_dim == 48,
+              "bmx_seq_attention_x3_batched_split_fwd: head_dim must be 24, 32 or 48 (got %d)", head_dim);
+  BMX_REQUIRE(heads >= 1 && heads <= 64, "bmx_seq_attention_x3_batched_split_fwd: heads must be in [1, 64] (got %d)",
+              heads);
+  BMX_REQUIRE(ldq >= (int64_t)heads * head_dim && ldk >= (int64_t)heads * head_dim,
+              "bmx_seq_attention_x3_batched_split_fwd: row strides must be >= heads * head_dim");
+  BMX_REQUIRE(sq >= 0 && sk >= 0 && sbias >= 0 && smask >= 0 && bias_div >= 1,
+              "bmx_seq_attention_x3_batched_split_fwd: strides must be >= 0 and bias_div >= 1");
+  BMX_REQUIRE(inf > 0.f, "bmx_seq_attention_x3_batched_split_fwd: inf must be positive");
+  if (batch == 0 || nq == 0) return BMX_OK;
+  BMX_REQUIRE(q && k && v && bias && mask && g && out_op && workspace,
+              "bmx_seq_attention_x3_batched_split_fwd: null pointer");
+  BMX_REQUIRE(ldq % 4 == 0 && sq % 4 == 0 && (uintptr_t)g % 16 == 0 && (uintptr_t)out_op % 16 == 0,
+              "bmx_seq_attention_x3_batched_split_fwd: g and out_op must be 16-byte aligned, ldq and sq multiples of 4");
+  const size_t need = x3_workspace_bytes(batch, nk, heads, head_dim);
+  BMX_REQUIRE(workspace_bytes >= need && (uintptr_t)workspace % 256 == 0,
+              "bmx_seq_attention_x3_batched_split_fwd: workspace must be 256-byte aligned and hold %zu bytes (got %zu)",
+              need, workspace_bytes);
+  const SeqAttnShape sh{(int)nq, (int)nk, (int)bias_div, ldq, ldk, sq, sk, sbias, smask};
+  return launch_seq_attention_x3("bmx_seq_attention_x3_batched_split_fwd", q, k, v, bias, mask, g, batch, sh, heads,
+                                 head_dim, inf, nullptr, (bf16*)out_op, workspace, stream);
 }
 
 }  // extern "C"

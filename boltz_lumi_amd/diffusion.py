@@ -230,10 +230,15 @@ def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity, keys=N
     att = self.pair_bias_attn
     o = None
     if keys is None and to_keys is None and side.split and operand_ok(att):
-        # the AdaLN output only as the q | k | v | g GEMM's split operand
+        # the AdaLN output only as the q | k | v | g GEMM's split operand, and the
+        # attention's output only as proj_o's, where proj_o is the plain linear
+        plain_o = _untouched(att.proj_o)
         o = attention_from_operand(att, ops.adaln_split3(rows, scale_a, shift_a, self.adaln.a_norm.eps), a.shape, bias,
-                                   mask, multiplicity)
-    if o is not None:
+                                   mask, multiplicity, split_out=plain_o)
+    if o is not None and o.dtype == torch.bfloat16:
+        pl = att.proj_o
+        b = ops.mm_split(o, ops.x3_weight(pl, "x3", (pl.weight,), (pl.bias,))).view(a.shape)
+    elif o is not None:
         b = att.proj_o(o) if "forward" in vars(att.proj_o) else ops.linear_fp32(o, att.proj_o)
     elif keys is not None:
         b = ops.adaln_modulate(rows, scale_a, shift_a, self.adaln.a_norm.eps).view(a.shape)

@@ -729,7 +729,16 @@ def seq_attention(q, k, v, bias, mask, g, inf, out=None):
 X3_ATTN_MIN_KEYS = 256
 
 
-def seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=1, out=None, split=None):
+def seq_attention_split_ok(q, g, nk) -> bool:
+    """Whether ``seq_attention_batched`` takes the split-bf16 kernel by default:
+    not in exact fp32 mode, width >= ``X3_MIN_K``, >= ``X3_ATTN_MIN_KEYS`` keys,
+    and 16-byte g rows."""
+    width = q.shape[-1]
+    return (not _EXACT_FP32[0] and width >= X3_MIN_K and nk >= X3_ATTN_MIN_KEYS and g.data_ptr() % 16 == 0
+            and q.stride(1) % 4 == 0 and q.stride(0) % 4 == 0)
+
+
+def seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=1, out=None, split=None, split_out=False):
     """``seq_attention`` for a batch in one launch (``bmx_seq_attention_batched_fwd``):
     q, g [B, NQ, H * D] and k, v [B, NK, H * D] (D = 24, 32 or 48; unit column
     stride; q and g share their strides, k and v theirs), bias
@@ -737,7 +746,10 @@ def seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=1, out=None, spl
     b // bias_div), mask [B or 1, NK] with unit stride.  Returns (or writes into
     ``out``) a contiguous fp32 [B, NQ, H * D].  ``split``: True for the
     split-bf16 kernel (``bmx_seq_attention_x3_batched_fwd``, about 2^-16
-    relative per product), False for fp32 MFMA, None to choose as above."""
+    relative per product), False for fp32 MFMA, None to choose as above.
+    ``split_out``: return the output rows as the split-bf16 operand of the next
+    linear instead ([B * NQ, 3 H D + 64] bf16, ``bmx_seq_attention_x3_batched_split_fwd``;
+    split-bf16 kernel only)."""
     _cuda(q, k, v, bias, mask, g)
     _check(q.dim() == 3 and k.dim() == 3 and bias.dim() == 4 and mask.dim() == 2, "expected 3-d q/k, 4-d bias, 2-d mask")
     b, nq, width = q.shape
@@ -751,13 +763,16 @@ def seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=1, out=None, spl
            and (bias.shape[0] == 0 or bias[0].is_contiguous()), "expected fp32 [B / bias_div, H, NQ, NK] dense bias")
     _check(mask.dtype == torch.float32 and mask.shape[1] == nk and mask.shape[0] in (1, b) and mask.stride(1) == 1,
            "expected an fp32 [B or 1, NK] mask")
-    if out is None:
-        out = torch.empty((b, nq, width), device=q.device, dtype=torch.float32)
-    _check(out.shape == (b, nq, width) and out.dtype == torch.float32 and out.is_contiguous(),
-           "out must be a contiguous fp32 [B, NQ, H * D]")
     if split is None:
-        split = (not _EXACT_FP32[0] and width >= X3_MIN_K and nk >= X3_ATTN_MIN_KEYS and g.data_ptr() % 16 == 0
-                 and q.stride(1) % 4 == 0 and q.stride(0) % 4 == 0)
+        split = seq_attention_split_ok(q, g, nk)
+    if split_out:
+        _check(split and out is None, "split_out needs the split-bf16 kernel and no out")
+        out = torch.empty((b * nq, split_width(width)), device=q.device, dtype=torch.bfloat16)
+    elif out is None:
+        out = torch.empty((b, nq, width), device=q.device, dtype=torch.float32)
+    else:
+        _check(out.shape == (b, nq, width) and out.dtype == torch.float32 and out.is_contiguous(),
+               "out must be a contiguous fp32 [B, NQ, H * D]")
     if b and nq:
         args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), mask.data_ptr(), g.data_ptr(), b, nq, nk,
                 q.stride(1), k.stride(1), q.stride(0), k.stride(0), bias.stride(0),
@@ -766,7 +781,8 @@ def seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=1, out=None, spl
         if split:
             nbytes = N.lib().bmx_seq_attention_x3_workspace_bytes(b, nk, heads, width // heads)
             ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
-            N.call("bmx_seq_attention_x3_batched_fwd", *args, ws.data_ptr(), nbytes, _stream(q))
+            name = "bmx_seq_attention_x3_batched_split_fwd" if split_out else "bmx_seq_attention_x3_batched_fwd"
+            N.call(name, *args, ws.data_ptr(), nbytes, _stream(q))
         else:
             N.call("bmx_seq_attention_batched_fwd", *args, _stream(q))
     return out

@@ -114,9 +114,10 @@ def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
     return _attend(module, q, k, v, g, z, mask, multiplicity, bias)
 
 
-def _attend(module, q, k, v, g, z, mask, multiplicity, bias=None):
+def _attend(module, q, k, v, g, z, mask, multiplicity, bias=None, split_out=False):
     """The attention of ``fused_attention`` from its projections ([B, NQ / NK,
-    H * D] column slices), or None where shapes do not match."""
+    H * D] column slices), or None where shapes do not match; ``split_out``:
+    as the split-bf16 operand of ``proj_o`` (``ops.seq_attention_batched``)."""
     heads = module.num_heads
     batch, nq, nk = q.shape[0], q.shape[1], k.shape[1]
     if bias is None:
@@ -131,6 +132,9 @@ def _attend(module, q, k, v, g, z, mask, multiplicity, bias=None):
         return None
     if m.stride(1) != 1:
         m = m.contiguous()
+    if split_out:
+        return ops.seq_attention_batched(q, k, v, bias, m, g, module.inf, bias_div=multiplicity, split=True,
+                                         split_out=True)
     return ops.seq_attention_batched(q, k, v, bias, m, g, module.inf, bias_div=multiplicity)
 
 
@@ -145,17 +149,20 @@ def operand_ok(module) -> bool:
             and width % heads == 0 and width // heads in (24, 32, 48) and heads <= 64 and ops.use_split(width))
 
 
-def attention_from_operand(module, op, shape, z, mask, multiplicity=1):
+def attention_from_operand(module, op, shape, z, mask, multiplicity=1, split_out=False):
     """``fused_attention(module, s, z, mask, s, multiplicity)`` when the caller
     holds s only as its split-bf16 operand ``op`` ([B * N, 3 c_s + 64], e.g.
     the AdaLN output written by ``ops.adaln_split3``): the q | k | v | g
-    projection is one GEMM of ``op``.  ``shape`` is s's [B, N, c_s]."""
+    projection is one GEMM of ``op``.  ``shape`` is s's [B, N, c_s].  With
+    ``split_out`` the result comes as the split-bf16 operand of ``proj_o``
+    when the split-bf16 attention kernel applies (else fp32 [B, N, c_s])."""
     width = module.c_s
     lin = (module.proj_q, module.proj_k, module.proj_v, module.proj_g)
     w3 = ops.x3_weight(module, "qkvg_x3", tuple(m.weight for m in lin), tuple(m.bias for m in lin))
     proj = ops.mm_split(op, w3).view(tuple(shape[:-1]) + (4 * width,))
     q, k, v, g = proj.split(width, dim=-1)
-    return _attend(module, q, k, v, g, z, mask, multiplicity)
+    split_out = split_out and ops.seq_attention_split_ok(q, g, k.shape[1])
+    return _attend(module, q, k, v, g, z, mask, multiplicity, split_out=split_out)
 
 
 def windowed_ok(module) -> bool:

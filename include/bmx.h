@@ -292,6 +292,16 @@ int bmx_seq_attention_x3_batched_fwd(const float* q, const float* k, const float
                                      int64_t bias_div, int heads, int head_dim, float inf, float* out,
                                      void* workspace, size_t workspace_bytes, bmx_stream_t stream);
 
+/* bmx_seq_attention_x3_batched_fwd writing each output row as the split-bf16 operand of the next
+ * linear (proj_o): out_op [batch * nq][3 * heads * D + 64] bf16, rows [hi | hi | lo | 1 1 0 ...]
+ * as bmx_split3_bf16 writes them (16-byte aligned).  Saves the fp32 output and its split pass. */
+int bmx_seq_attention_x3_batched_split_fwd(const float* q, const float* k, const float* v, const float* bias,
+                                           const float* mask, const float* g, int64_t batch, int64_t nq, int64_t nk,
+                                           int64_t ldq, int64_t ldk, int64_t sq, int64_t sk, int64_t sbias,
+                                           int64_t smask, int64_t bias_div, int heads, int head_dim, float inf,
+                                           void* out_op, void* workspace, size_t workspace_bytes,
+                                           bmx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

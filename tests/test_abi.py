@@ -90,6 +90,8 @@ def test_argument_validation_needs_no_gpu(lib):
     rc = lib.bmx_seq_attention_x3_batched_fwd(*args[:17], 40, 1e6, fake, fake, 1 << 30, None)
     assert rc == N.BMX_EINVAL and b"head_dim" in lib.bmx_last_error()
     assert lib.bmx_seq_attention_x3_batched_fwd(*args[:6], 0, *args[7:], None, 0, None) == N.BMX_OK
+    rc = lib.bmx_seq_attention_x3_batched_split_fwd(*args[:19], ctypes.c_void_p(264), fake, 1 << 30, None)
+    assert rc == N.BMX_EINVAL and b"out_op must be 16-byte aligned" in lib.bmx_last_error()
     # split-bf16 operand writers and the strided modulation kernels
     assert lib.bmx_split3_bf16(None, 0, 768, 768, None, None) == N.BMX_OK
     rc = lib.bmx_split3_bf16(fake, 4, 768, 700, fake, None)

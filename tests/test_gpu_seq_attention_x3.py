@@ -81,6 +81,25 @@ def test_split_attention_matches_fp64_and_fp32_kernel(gpu, b, nq, nk, heads, d, 
     assert max_rel(got, exact) < 1e-4
 
 
+@pytest.mark.parametrize("b,nq,nk,heads,d,bias_div,mask_kind,fused", [CASES[0], CASES[2], CASES[3]])
+def test_split_attention_split_output_is_the_split_of_its_output(gpu, b, nq, nk, heads, d, bias_div, mask_kind, fused):
+    """split_out writes each output row as the split-bf16 operand of proj_o:
+    [hi | hi | lo | 1 1 0 ...] of the fp32 output of the same kernel, bit for bit."""
+    q, k, v, bias, mask, gate = inputs(11 + nq + nk + d, b, nq, nk, heads, d, bias_div, mask_kind, fused)
+    dev = [t.to(gpu) for t in (q, k, v, bias, mask, gate)]
+    with torch.inference_mode():
+        out = ops.seq_attention_batched(*dev, 1e6, bias_div=bias_div, split=True)
+        op = ops.seq_attention_batched(*dev, 1e6, bias_div=bias_div, split=True, split_out=True)
+    w = heads * d
+    rows = out.reshape(-1, w).cpu()
+    op = op.cpu()
+    hi = rows.bfloat16()
+    assert op.shape == (b * nq, 3 * w + 64)
+    assert torch.equal(op[:, :w], hi) and torch.equal(op[:, w:2 * w], hi)
+    assert torch.equal(op[:, 2 * w:3 * w], (rows - hi.float()).bfloat16())
+    assert (op[:, 3 * w:3 * w + 2] == 1).all() and (op[:, 3 * w + 2:] == 0).all()
+
+
 def test_split_attention_is_the_default_for_the_token_transformer(gpu, monkeypatch):
     """Width 768 with 1024 keys takes the split kernel, 384 (the sequence
     stack) and short key rows the fp32 kernel, and exact fp32 mode turns the
