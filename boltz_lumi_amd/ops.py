@@ -589,10 +589,11 @@ def triattn_fp32(module, x, mask, starting):
     triangle.py:38-52 accelerates it too).  LayerNorm runs on the fp32 LN128
     kernel; the q | k | v | g projection and the triangle bias are fp32 GEMMs;
     the attention, mask bias, softmax, PV product and gate run fused in
-    ``bmx_seq_attention_batched_fwd`` on fp32 MFMA (every row i is one batch
-    element attending over its N keys, all rows sharing the [4, N, N]
-    triangle bias), so the [N, 4, N, N] scores never reach HBM; ``linear_o``
-    is an fp32 GEMM.  Returns fp32 [N, N, 128]."""
+    ``bmx_seq_attention_x3_batched_fwd`` (split-bf16 products, about 2^-16
+    relative each; ``bmx_seq_attention_batched_fwd`` on fp32 MFMA in exact fp32
+    mode), every row i one batch element attending over its N keys, all rows
+    sharing the [4, N, N] triangle bias, so the [N, 4, N, N] scores never
+    reach HBM; ``linear_o`` is an fp32 GEMM.  Returns fp32 [N, N, 128]."""
     _cuda(x)
     _check(x.dim() == 3 and x.size(0) == x.size(1) and x.size(2) == C and x.dtype == torch.float32,
            "expected fp32 x of shape [N, N, 128]")
@@ -614,10 +615,9 @@ def triattn_fp32(module, x, mask, starting):
     tri_bias = tri_bias.permute(2, 0, 1).contiguous()  # [H, q, k], shared by every row
     m = x.new_ones(n, n) if mask is None else mask.to(torch.float32).contiguous()
     q, k, v, g = proj.split(C, dim=-1)
-    o = torch.empty((n, n, C), device=x.device, dtype=torch.float32)
-    N.call("bmx_seq_attention_batched_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), tri_bias.data_ptr(),
-           m.data_ptr(), g.data_ptr(), n, n, n, 4 * C, 4 * C, n * 4 * C, n * 4 * C, 0, n, n, heads, d,
-           float(module.inf), o.data_ptr(), _stream(x))
+    # the split-bf16 kernel (about 2^-16 relative per product; 1.8x faster at N = 1024) unless exact
+    # fp32 products are asked for
+    o = seq_attention_batched(q, k, v, tri_bias[None], m, g, module.inf, bias_div=n, split=not _EXACT_FP32[0])
     out = torch.nn.functional.linear(o, mha.linear_o.weight.float(), mha.linear_o.bias.float())
     return out if starting else out.transpose(0, 1)
 
