@@ -398,8 +398,9 @@ def mm_x3(x, w3):
 X3_MIN_K = 512
 
 # Set BMX_EXACT_FP32_LINEARS=1 (or call exact_fp32_linears(True)) to run every
-# fp32 linear of the diffusion blocks as a true fp32 GEMM, as the reference
-# does, instead of the split-bf16 form (about 2^-16 relative per product).
+# fp32 linear of the diffusion blocks and of fp32-mode triangle attention as a
+# true fp32 GEMM and fp32-mode attention on fp32 MFMA, as the reference does,
+# instead of the split-bf16 form (about 2^-16 relative per product).
 _EXACT_FP32 = [os.environ.get("BMX_EXACT_FP32_LINEARS", "0") not in ("", "0")]
 
 
@@ -583,11 +584,16 @@ def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=No
     return out
 
 
+TRIATTN_FP32_PROJ_COLS = 576
+
+
 def triattn_fp32(module, x, mask, starting):
     """TriangleAttention (starting or ending node) in fp32 for x [N, N, 128]
     fp32, the fp32 mode of the module (autocast off; reference
-    triangle.py:38-52 accelerates it too).  LayerNorm runs on the fp32 LN128
-    kernel; the q | k | v | g projection and the triangle bias are fp32 GEMMs;
+    triangle.py:38-52 accelerates it too).  The q | k | v | g projection and
+    the triangle bias are one split-bf16 GEMM of LayerNorm-without-affine(x),
+    the LayerNorm affine folded into its weights (in exact fp32 mode the fp32
+    LN128 kernel and fp32 GEMMs);
     the attention, mask bias, softmax, PV product and gate run fused in
     ``bmx_seq_attention_x3_batched_fwd`` (split-bf16 products, about 2^-16
     relative each; ``bmx_seq_attention_batched_fwd`` on fp32 MFMA in exact fp32
@@ -605,16 +611,37 @@ def triattn_fp32(module, x, mask, starting):
         mask = None if mask is None else mask.transpose(0, 1)
     x = x.contiguous()
     ln = module.layer_norm
-    xn = norm(x.view(-1, C), _f32(ln.weight), _f32(ln.bias), ln.eps, bf16_output=False)
-    w = cached_weight(module, "qkvg_f32", (mha.linear_q.weight, mha.linear_k.weight, mha.linear_v.weight,
-                                           mha.linear_g.weight), lambda *ws: torch.cat(ws, 0).float())
-    b = cached_weight(module, "qkvg_bias_f32", (mha.linear_g.bias,),
-                      lambda bg: torch.cat([bg.new_zeros(3 * C), bg]).float())
-    proj = torch.nn.functional.linear(xn, w, b).view(n, n, 4 * C)
-    tri_bias = torch.nn.functional.linear(xn, module.linear.weight.float()).view(n, n, heads)
-    tri_bias = tri_bias.permute(2, 0, 1).contiguous()  # [H, q, k], shared by every row
+    lins = (mha.linear_q, mha.linear_k, mha.linear_v, mha.linear_g, module.linear)
+    if not _EXACT_FP32[0] and ln.weight is not None:
+        # q | k | v | g and the triangle bias as one split-bf16 GEMM of LayerNorm-without-affine(x), the
+        # LayerNorm affine folded into the weights: (W diag w) LN0(x) + (bias + W b)
+        def fold(*_):
+            w = torch.cat([lin.weight.detach().float() for lin in lins])
+            b = torch.cat([lin.bias.detach().float() if lin.bias is not None
+                           else w.new_zeros(lin.out_features) for lin in lins])
+            if ln.bias is not None:
+                b = b + w @ ln.bias.detach().float()
+            # zero rows up to 576 outputs: the GEMM runs faster than at 516 and output rows stay 128-byte aligned
+            pad = TRIATTN_FP32_PROJ_COLS - w.shape[0]
+            w = torch.cat([w * ln.weight.detach().float(), w.new_zeros(pad, C)])
+            return _x3_weight(w, torch.cat([b, b.new_zeros(pad)]))
+
+        srcs = tuple(t for m_ in (ln,) + lins for t in (m_.weight, m_.bias) if t is not None)
+        _check(4 * C + heads <= TRIATTN_FP32_PROJ_COLS, "too many heads")
+        w3 = cached_weight(module, "qkvgb_ln_x3", srcs, fold)
+        proj = mm_split(layernorm_split3(x.view(-1, C), ln.eps), w3).view(n, n, TRIATTN_FP32_PROJ_COLS)
+        tri_bias = proj[..., 4 * C:4 * C + heads].permute(2, 0, 1).contiguous()  # [H, q, k], shared by every row
+    else:
+        xn = norm(x.view(-1, C), _f32(ln.weight), _f32(ln.bias), ln.eps, bf16_output=False)
+        w = cached_weight(module, "qkvg_f32", tuple(lin.weight for lin in lins[:4]),
+                          lambda *ws: torch.cat(ws, 0).float())
+        b = cached_weight(module, "qkvg_bias_f32", (mha.linear_g.bias,),
+                          lambda bg: torch.cat([bg.new_zeros(3 * C), bg]).float())
+        proj = torch.nn.functional.linear(xn, w, b).view(n, n, 4 * C)
+        tri_bias = torch.nn.functional.linear(xn, module.linear.weight.float()).view(n, n, heads)
+        tri_bias = tri_bias.permute(2, 0, 1).contiguous()  # [H, q, k], shared by every row
     m = x.new_ones(n, n) if mask is None else mask.to(torch.float32).contiguous()
-    q, k, v, g = proj.split(C, dim=-1)
+    q, k, v, g = proj[..., :4 * C].split(C, dim=-1)
     # the split-bf16 kernel (about 2^-16 relative per product; 1.8x faster at N = 1024) unless exact
     # fp32 products are asked for
     o = seq_attention_batched(q, k, v, tri_bias[None], m, g, module.inf, bias_div=n, split=not _EXACT_FP32[0])

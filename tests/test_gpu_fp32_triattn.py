@@ -1,8 +1,9 @@
 """fp32-mode triangle attention (autocast off, fp32 x; reference
-triangle.py:38-52): the installed forward runs fp32 LayerNorm, fp32 GEMMs and
-the fused fp32-MFMA attention (ops.triattn_fp32) and must meet the north
-star's fp32-mode bar, max relative error <= 1e-4 against the fp32 CPU oracle,
-for both nodes at N = 117, 512 and 1024, with padded tokens."""
+triangle.py:38-52): the installed forward (ops.triattn_fp32: the projection as
+one split-bf16 GEMM with the LayerNorm affine folded in, the fused split-bf16
+attention, an fp32 output linear) must meet the north star's fp32-mode bar,
+max relative error <= 1e-4 against the fp32 CPU oracle, for both nodes at
+N = 117, 512 and 1024, with padded tokens."""
 
 import copy
 
@@ -21,9 +22,11 @@ def max_rel(got, want):
     return ((got - want).abs().max() / want.abs().max()).item()
 
 
-@pytest.mark.parametrize("n", [117, 512, 1024])
+@pytest.mark.parametrize("n,exact", [(117, False), (512, False), (1024, False), (117, True), (512, True)])
 @pytest.mark.parametrize("starting", [True, False])
-def test_fp32_triangle_attention_matches_oracle(gpu, n, starting):
+def test_fp32_triangle_attention_matches_oracle(gpu, n, exact, starting):
+    """``exact``: BMX_EXACT_FP32_LINEARS mode (fp32 LayerNorm, fp32 GEMMs and
+    the fp32-MFMA attention)."""
     g = torch.Generator().manual_seed(n + starting)
     cls = R.TriangleAttention if starting else R.TriangleAttentionEndingNode
     ref = R.randomize(cls(128, 32, 4), generator=g).eval()
@@ -31,22 +34,24 @@ def test_fp32_triangle_attention_matches_oracle(gpu, n, starting):
     tok = torch.ones(n)
     tok[-(n // 10):] = 0
     mask = (tok[:, None] * tok[None, :])[None]
-    print(f"fp32 triangle attention n={n} starting={starting}: CPU oracle", flush=True)
+    print(f"fp32 triangle attention n={n} exact={exact} starting={starting}: CPU oracle", flush=True)
     with torch.no_grad():
         want = ref(x, mask, chunk_size=64)
     mine = copy.deepcopy(ref).to(gpu)
     calls = []
     original = ops.triattn_fp32
+    before = ops.exact_fp32_linears(exact)
     try:
         ops.triattn_fp32 = lambda *a, **k: calls.append(1) or original(*a, **k)
         with torch.inference_mode():
             got = triangle_attention_forward(mine, x.to(gpu), mask.to(gpu))
     finally:
         ops.triattn_fp32 = original
+        ops.exact_fp32_linears(before)
     torch.cuda.synchronize()
     assert calls == [1] and got.dtype == torch.float32 and got.shape == want.shape
     err = max_rel(got, want)
-    print(f"fp32 triangle attention n={n} starting={starting}: max_rel {err:.2e}", flush=True)
+    print(f"fp32 triangle attention n={n} exact={exact} starting={starting}: max_rel {err:.2e}", flush=True)
     assert err < 1e-4
 
 
