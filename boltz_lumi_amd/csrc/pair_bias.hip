@@ -297,24 +297,25 @@ int launch_seq_attention(const char* name, const float* q, const float* k, const
 // key rows (the token transformer's).
 //
 // A pre-pass writes K as bf16 hi / lo [b][h][key][d] and V^T as hi / lo
-// [b][h][d][key'], keys padded with zeros to a multiple of the 64-key stage
-// and, in V^T, permuted inside each 32-key block into the order in which a
+// [b][h][d][key'], keys padded with zeros to a multiple of 64 and, in V^T, permuted inside each 32-key block into the order in which a
 // lane holds P: slot 8 gi + e of a block holds key 4 gi + e (e < 4) or
 // 16 + 4 gi + e - 4; and each key's additive mask term (1 - mask) * -inf as
 // fp32 [b][key'], -infinity past nk, so that a logit is (q.k / sqrt(D) +
 // bias) + term with no per-key select.  A block serves 64 queries of one head (16 per wave) and
-// walks the keys in 64-key stages that LDS DMA copies into a double-buffered
-// LDS stage shared by the four waves (K tiles dense, V^T rows of 64 slots with
-// their 16-byte chunks XOR-swizzled by d & 7), so each K / V element is read
-// from L2 once per 64 queries.  v_mfma_f32_16x16x32_bf16 (lane l, gi = l / 16:
+// walks the keys in KS-key stages (32 keys for D = 48, else 64) that LDS DMA
+// copies into a double-buffered LDS
+// stage shared by the four waves (K tiles dense, V^T rows of KS slots with
+// their 16-byte chunks XOR-swizzled by d mod KS / 8), so each K / V element is
+// read from L2 once per 64 queries.  At D = 48, 32-key stages halve the LDS of
+// a block (24 KB), so 5 blocks share a CU instead of 3.  v_mfma_f32_16x16x32_bf16 (lane l, gi = l / 16:
 // A holds A[l%16][8 gi .. 8 gi + 7], B holds B[8 gi .. 8 gi + 7][l%16], D
 // register r holds D[4 gi + r][l%16]); per stage and wave:
-//   S^T[key][q] = K Q^T         four 16-key tiles, k steps of 32 dims (a last
+//   S^T[key][q] = K Q^T         KS / 16 16-key tiles, k steps of 32 dims (a last
 //                               step of 16 dims on v_mfma_f32_16x16x16_bf16 for
 //                               D = 48; dims past D are zero), 3 terms;
-//   O^T[d][q] += V^T P^T        two 32-key k steps per 16-dim tile, 3 terms,
+//   O^T[d][q] += V^T P^T        KS / 32 32-key k steps per 16-dim tile, 3 terms,
 //                               P^T from the lane's probabilities.
-constexpr int kX3Stage = 64;  // keys per LDS stage
+constexpr int kX3Stage = 64;  // key padding of the pre-pass, and the LDS stage where 32 keys are not whole KB
 constexpr int kX3Q = 64;      // queries per block
 
 __host__ __device__ inline int64_t x3_nkp(int64_t nk) { return (nk + kX3Stage - 1) / kX3Stage * kX3Stage; }
@@ -400,7 +401,13 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
   constexpr bool T16 = D % 32 == 16;             // the last 16 dims on a K = 16 MFMA
   constexpr int DK = T16 ? D / 32 : (D + 31) / 32;  // QK^T k steps of 32 dims
   constexpr int DT = (D + 15) / 16;              // O^T d tiles
-  constexpr int kTile = kX3Stage * D * 2;        // bytes of one K (or V^T) tile, hi or lo
+  // keys per LDS stage: 32 where a double-buffered 64-key stage (2 x 4 tiles x 64 x D x 2 bytes)
+  // would exceed 40 KB, i.e. leave fewer than 4 blocks per CU (D = 48: 3 -> 5 blocks); 64 otherwise, where
+  // the shorter stages' extra barriers cost more than the occupancy gains (D = 32: 6.29 -> 6.64 ms)
+  constexpr int KS = 2 * 4 * 64 * D * 2 > 40 * 1024 ? 32 : kX3Stage;
+  static_assert(KS == kX3Stage || (32 * D * 2) % 1024 == 0, "32-key tiles must be whole KB");
+  constexpr int kSwz = KS / 8 - 1;               // V^T chunk swizzle mask
+  constexpr int kTile = KS * D * 2;              // bytes of one K (or V^T) tile, hi or lo
   constexpr int kStage = 4 * kTile;              // K hi, K lo, V^T hi, V^T lo
   constexpr int kDmaPerWave = kStage / 1024 / kAttnWaves;
   static_assert(D % 8 == 0 && kTile % 1024 == 0 && kDmaPerWave * kAttnWaves * 1024 == kStage, "stage layout");
@@ -435,8 +442,8 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
 
   // DMA job u of this wave copies stage bytes [1024 j, 1024 j + 1024), j = w + 4 u:
   // region j / (kTile / 1024) is K hi, K lo, V^T hi or V^T lo.  K tiles are
-  // the dense rows of 64 keys; a V^T row is 64 slots (128 bytes) whose chunk
-  // at position p holds the global chunk p ^ (d & 7).
+  // the dense rows of KS keys; a V^T row is KS slots (2 KS bytes) whose chunk
+  // at position p holds the global chunk p ^ (d & kSwz).
   const bf16* dma_src[kDmaPerWave];
   int dma_step[kDmaPerWave];
 #pragma unroll
@@ -445,11 +452,11 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
     const int off = (j - region * (kTile / 1024)) * 1024 + 16 * l;  // byte offset inside the tile
     if (region < 2) {
       dma_src[u] = k_src[region] + off / 2;
-      dma_step[u] = kX3Stage * D;
+      dma_step[u] = KS * D;
     } else {
-      const int d = off / 128, p = (off % 128) / 16;
-      dma_src[u] = v_src[region - 2] + (int64_t)d * nkp + 8 * (p ^ (d & 7));
-      dma_step[u] = kX3Stage;
+      const int d = off / (KS * 2), p = (off % (KS * 2)) / 16;
+      dma_src[u] = v_src[region - 2] + (int64_t)d * nkp + 8 * (p ^ (d & kSwz));
+      dma_step[u] = KS;
     }
   }
   auto dma_stage = [&](int buf) {
@@ -486,7 +493,7 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
 #pragma unroll
   for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -3.4e38f, lsum = 0.f;
-  const int nst = (int)(nkp / kX3Stage);
+  const int nst = (int)(nkp / KS);
   // the q loads must land before the first DMA: a wait the compiler places for
   // them inside the loop would be vmcnt(0), which also waits for a DMA in flight
   wait_vm0();
@@ -496,12 +503,12 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
   for (int st = 0; st < nst; ++st) {
     if (st + 1 < nst) dma_stage((st + 1) & 1);
     const char* sb = lds + (st & 1) * kStage;
-    const int key0 = st * kX3Stage;
-    const bool full = vec && key0 + kX3Stage <= nk;
-    f32x4 sc[4];
+    const int key0 = st * KS;
+    const bool full = vec && key0 + KS <= nk;
+    f32x4 sc[KS / 16];
     float tmax = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < KS / 16; ++t) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < DK; ++ks) {
@@ -542,7 +549,7 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[t] *= alpha;
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
+    for (int s2 = 0; s2 < KS / 32; ++s2) {
       // P^T of keys key0 + 32 s2 + (slots): slot 4 t' + r <-> key 16 t' + 4 gi + r of the 32-key block
       bf16x8 ph, pl;
 #pragma unroll
@@ -557,7 +564,7 @@ __global__ __launch_bounds__(256) void seq_attention_x3_kernel(const float* __re
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int d = 16 * dt + c, chunk = 4 * s2 + gi;
-        const int off = d * (kX3Stage * 2) + ((chunk ^ (d & 7)) * 16);
+        const int off = d * (KS * 2) + ((chunk ^ (d & kSwz)) * 16);
         const bf16x8 vh = d < D ? *(const bf16x8*)(sb + 2 * kTile + off) : zero8;
         const bf16x8 vl = d < D ? *(const bf16x8*)(sb + 3 * kTile + off) : zero8;
         o[dt] = mfma16bf(vh, ph, o[dt]);
