@@ -693,6 +693,37 @@ def elementwise_kernel_rates(m, d, di, g, dev, reps_min=10):
     return out
 
 
+def token_attention_launch(q, k, v, bias, mask, g, samples, inf=1e6):
+    """The token transformer's attention over `samples` elements sharing one
+    bias (bmx_seq_attention_x3_batched_fwd: the K / V split pre-pass and the
+    split-bf16 attention) as a step function launching through the C ABI on a
+    preallocated output and workspace: the Python wrapper's argument checks and
+    allocations are host time that the stacks overlap with earlier kernels.
+    Checked once, bit for bit, against the wrapper."""
+    import torch
+    from boltz_lumi_amd import _native as N, ops
+
+    b, nq, width = q.shape
+    nk, heads = k.shape[1], bias.shape[1]
+    hd = width // heads
+    out = torch.empty(b, nq, width, device=q.device)
+    nbytes = N.lib().bmx_seq_attention_x3_workspace_bytes(b, nk, heads, hd)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), mask.data_ptr(), g.data_ptr(), b, nq, nk,
+            q.stride(1), k.stride(1), q.stride(0), k.stride(0), bias.stride(0), mask.stride(0), samples, heads, hd,
+            float(inf), out.data_ptr(), ws.data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream)
+    fn = N.lib().bmx_seq_attention_x3_batched_fwd
+
+    def step(keep=(out, ws)):
+        if fn(*args) != 0:
+            raise RuntimeError(f"bmx_seq_attention_x3_batched_fwd failed: {N.last_error()}")
+
+    step()
+    if not torch.equal(out, ops.seq_attention_batched(q, k, v, bias, mask, g, inf, bias_div=samples, split=True)):
+        raise RuntimeError("C-ABI launch of the token attention differs from the wrapper's")
+    return step
+
+
 def diffusion_kernel_times(stacks, t, packed, samples, tokens):
     """Each fused kernel of one step at the step's shapes, timed alone:
     the token attention (split-bf16 MFMA, 16 x 48), the windowed atom attention
@@ -717,8 +748,7 @@ def diffusion_kernel_times(stacks, t, packed, samples, tokens):
     mask = torch.ones(samples, tokens, device=dev)
     # split-bf16 by default (the K / V split pre-pass included): 3 bf16 MFMA
     # products per fp32 product, so the executed flops against the bf16 peak
-    rate("seq_attention (token, 16 x 48, split-bf16)",
-         lambda: ops.seq_attention_batched(qq, kk, vv, bias, mask, gg, 1e6, bias_div=samples),
+    rate("seq_attention (token, 16 x 48, split-bf16)", token_attention_launch(qq, kk, vv, bias, mask, gg, samples),
          3 * 4.0 * 16 * 48 * tokens * tokens * samples, samples * tokens * d * 16 + 16 * tokens * tokens * 4, 24,
          PEAK_BF16_TFLOPS)
     # the atom transformer's attention as the installed stacks run it: q | k | v | g of the atom rows,
@@ -730,10 +760,25 @@ def diffusion_kernel_times(stacks, t, packed, samples, tokens):
     pq, pk, pv, pg = proj.split(128, dim=-1)
     ab = prepare_window_bias(torch.randn(1, nw, 32, 128, 12, generator=g).to(dev))[..., 4:8]
     am = torch.ones(samples * 8192, device=dev)
-    rate("seq_attention (atom windows, 4 x 32)",
-         lambda: ops.seq_attention_windowed(pq.view(samples * nw, 32, 128), pk, pv, ab, am,
-                                            pg.view(samples * nw, 32, 128), 1e6, windows=nw, key_offset=-48,
-                                            bias_group=samples * nw),
+    # the wrapper's one C-ABI launch (its output, the only buffer it allocates, kept alive) replayed
+    calls = []
+    real_call = N.call
+    N.call = lambda name, *a: (calls.append((name, a)), real_call(name, *a))[1]
+    try:
+        win_out = ops.seq_attention_windowed(pq.view(samples * nw, 32, 128), pk, pv, ab, am,
+                                             pg.view(samples * nw, 32, 128), 1e6, windows=nw, key_offset=-48,
+                                             bias_group=samples * nw)
+    finally:
+        N.call = real_call
+    if [c[0] for c in calls] != ["bmx_seq_attention_windowed_fwd"]:
+        raise RuntimeError(f"unexpected launches {[c[0] for c in calls]}")
+    win_fn, win_args = getattr(N.lib(), calls[0][0]), calls[0][1]
+
+    def win_step(keep=win_out):
+        if win_fn(*win_args) != 0:
+            raise RuntimeError(f"bmx_seq_attention_windowed_fwd failed: {N.last_error()}")
+
+    rate("seq_attention (atom windows, 4 x 32)", win_step,
          4.0 * 4 * 32 * 32 * 128 * samples * nw, samples * 8192 * 5 * 128 * 4 + nw * 32 * 128 * 4 * 4, 6)
     per_step = {"adaln": 48, "gated_swiglu": 24, "gate": 24}
     for name, rec in elementwise_kernel_rates(m, d, 2 * d, g, dev).items():
@@ -778,8 +823,9 @@ def token_attention(args):
     """One token-transformer AttentionPairBias forward (c_s 768, 16 heads x 48)
     over 5 samples of N tokens sharing one prepacked [1, N, N, 24 * 16] bias
     (BASELINE configs[4] shape, one of the 24 layers), through the drop-in
-    ``prepared_forward``.  The roofline covers the fused attention kernel: fp32
-    MFMA flops 4 * 16 * 48 * N^2 per sample."""
+    ``prepared_forward``.  The roofline covers the fused attention the
+    forward runs, the split-bf16 kernel with its K / V pre-pass over the 5
+    samples: 3 x 4 * 16 * 48 * N^2 bf16 MFMA flops executed per sample."""
     import torch
     from boltz_lumi_amd import layers, ops
     from boltz_lumi_amd.pair_bias import prepare_token_bias, prepared_forward
@@ -795,21 +841,20 @@ def token_attention(args):
     with torch.inference_mode():
         ms, _ = timed_loop(lambda: prepared_forward(module, s, bias, mask, s, multiplicity=samples), steps,
                            args.warmup)
-        proj = torch.randn(n, 4 * width, generator=g).to(dev)
+        proj = torch.randn(samples, n, 4 * width, generator=g).to(dev)
         q, k, v, gl = proj.split(width, dim=-1)
-        b0, m0 = bias[0].movedim(-1, 0), mask[0]
-        out = torch.empty(n, width, device=dev)
-        kms, _ = timed_loop(lambda: ops.seq_attention(q, k, v, b0, m0, gl, module.inf, out=out),
-                            max(steps, 10) * samples, 1)
-    flops = 4.0 * heads * 48 * n * n
+        kms, _ = timed_loop(token_attention_launch(q, k, v, bias.movedim(-1, 1), mask, gl, samples, module.inf),
+                            max(steps, 10), 1)
+    flops = 3 * 4.0 * heads * 48 * n * n * samples
     out_line = line("token-transformer AttentionPairBias ms @N=1024, 5 samples", ms, "ms", args, steps, "f32",
                     "synthetic (s ~ N(0,1), bias ~ N(0,1) prepacked, masks ones; weights seed 0)",
                     {"workload": f"diffusion token-transformer AttentionPairBias forward (prepared_forward), "
                                  f"c_s=768, 16 heads x 48, {samples} samples x N={n} (BASELINE configs[4] shape)",
                      "n_tokens": n, "samples": samples},
-                    roofline={"kernel": "seq_attention", **roofline_of(flops, n * n * heads * 4, kms,
-                                                                       PEAK_FP32_TFLOPS),
-                              "traffic": None, "kernel_ms_per_sample": round(kms, 4)})
+                    roofline={"kernel": "seq_attention_x3 (with its K / V split pre-pass)",
+                              **roofline_of(flops, samples * n * width * 16 + n * n * heads * 4, kms,
+                                            PEAK_BF16_TFLOPS),
+                              "traffic": None, "kernel_ms": round(kms, 4)})
     if not args.no_cpu_baseline:
         out_line["cpu_baseline"] = token_attention_cpu(n)
     print(json.dumps(out_line), flush=True)
