@@ -216,14 +216,26 @@ def _conditioning(layer, side, eps):
             torch.nn.functional.linear(side.raw(), wg, bg))
 
 
-def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity, keys=None):
+def _operand_path(layer, side, to_keys, keys=None) -> bool:
+    """Whether ``_layer_with_side`` feeds the attention from the AdaLN output's
+    split operand (``adaln_split3``), the token transformer's path."""
+    return keys is None and to_keys is None and side.split and operand_ok(layer.pair_bias_attn)
+
+
+def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity, keys=None, carry=None, nxt=None):
     """The layer with its conditioning projections on the shared operands of s
     (``side``); with ``keys`` (a ``_WindowKeys``) the attention reads its key
-    windows by address (``windowed_attention``) instead of ``to_keys``."""
+    windows by address (``windowed_attention``) instead of ``to_keys``.
+
+    ``carry`` = (attention operand, mods, gates) of this layer, computed by the
+    previous layer's last pass; with ``nxt`` (the next layer, on the operand
+    path too) this layer's last residual update also writes the next layer's
+    attention operand (``gated_residual_adaln_split3``), and the result is
+    (a, carry for ``nxt``) instead of a."""
     d = a.shape[-1]
     tr = self.transition
     eps = self.adaln.s_norm.eps
-    mods, gates = _conditioning(self, side, eps)
+    mods, gates = _conditioning(self, side, eps) if carry is None else carry[1:]
     scale_a, shift_a, scale_t, shift_t = mods.split(d, dim=-1)
     gate_a, gate_t = gates.split(d, dim=-1)
     rows = a.reshape(-1, d)
@@ -233,8 +245,8 @@ def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity, keys=N
         # the AdaLN output only as the q | k | v | g GEMM's split operand, and the
         # attention's output only as proj_o's, where proj_o is the plain linear
         plain_o = _untouched(att.proj_o)
-        o = attention_from_operand(att, ops.adaln_split3(rows, scale_a, shift_a, self.adaln.a_norm.eps), a.shape, bias,
-                                   mask, multiplicity, split_out=plain_o)
+        op = ops.adaln_split3(rows, scale_a, shift_a, self.adaln.a_norm.eps) if carry is None else carry[0]
+        o = attention_from_operand(att, op, a.shape, bias, mask, multiplicity, split_out=plain_o)
     if o is not None and o.dtype == torch.bfloat16:
         pl = att.proj_o
         b = ops.mm_split(o, ops.x3_weight(pl, "x3", (pl.weight,), (pl.bias,))).view(a.shape)
@@ -273,6 +285,11 @@ def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity, keys=N
         x = ops.adaln_modulate(rows, scale_t, shift_t, t_eps)
         y = _linear(tr.b_to_a, ops.epilogue(_linear(tr.swish_gate[0], x), _linear(tr.a_to_b, x), None,
                                             ops.GATED_SWIGLU))
+    if nxt is not None:  # the residual update and the next layer's attention operand in one pass
+        mods_n, gates_n = _conditioning(nxt, side, nxt.adaln.s_norm.eps)
+        rows, op_n = ops.gated_residual_adaln_split3(y.reshape(rows.shape), gate_t, rows, mods_n[:, :d],
+                                                     mods_n[:, d:2 * d], nxt.adaln.a_norm.eps, out=rows)
+        return rows.view(a.shape), (op_n, mods_n, gates_n)
     rows = ops.gated_residual(y.reshape(rows.shape), gate_t, rows, out=rows)
     return self.post_lnorm(rows.view(a.shape))
 
@@ -297,6 +314,12 @@ def _layer_per_linear(self, a, s, bias, mask, to_keys, multiplicity):
     else:
         a = a + block(a, s)
     return self.post_lnorm(a)
+
+
+def _with_side_ok(layer, a, s) -> bool:
+    """Whether ``_layer`` runs the layer as ``_layer_with_side``."""
+    return (eligible(layer, a, s) and a.shape == s.shape and a.shape[-1] % 4 == 0 and _plain(layer.output_projection)
+            and _side_ok(layer, a, s) and layer.transition.adaln.s_norm.eps == layer.adaln.s_norm.eps)
 
 
 def _layer(self, a, s, bias, mask, to_keys, multiplicity, side):
@@ -339,9 +362,19 @@ def stack_forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity=1
         n_b, n, m, d = bias.shape
         bias = bias.view(n_b, n, m, len(layers), d // len(layers))
     side = _Side(s)
+    # consecutive layers on the operand path chain their boundary passes: layer
+    # i's last residual update also writes layer i + 1's attention operand
+    chain = [_with_side_ok(l, a, s) and _operand_path(l, side, to_keys) for l in layers]
+    carry = None
     for i, layer in enumerate(layers):
         bias_l = bias[:, :, :, i] if getattr(self, "pair_bias_attn", True) else None
-        a = _layer(layer, a, s, bias_l, mask, to_keys, multiplicity, side)
+        if chain[i]:
+            nxt = layers[i + 1] if (i + 1 < len(layers) and chain[i + 1]
+                                    and isinstance(layer.post_lnorm, torch.nn.Identity)) else None
+            out = _layer_with_side(layer, a, s, side, bias_l, mask, to_keys, multiplicity, carry=carry, nxt=nxt)
+            a, carry = out if nxt is not None else (out, None)
+        else:
+            a, carry = _layer(layer, a, s, bias_l, mask, to_keys, multiplicity, side), None
     return a
 
 

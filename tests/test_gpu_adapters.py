@@ -13,7 +13,7 @@ import pytest
 import torch
 from torch import nn
 
-from boltz_lumi_amd import adapters, ops
+from boltz_lumi_amd import adapters, diffusion, ops
 from boltz_lumi_amd.atom_conditioning import atom_conditioning_cache
 from oracle import boltz_ref as R
 
@@ -201,7 +201,8 @@ def test_diffusion_stack_shared_conditioning_matches_upstream(gpu, width, heads,
     folded into the weights; it matches the fp32 upstream stack within 1e-4.
     Covered on the way: an s_norm with a bias (folded as W b), a layer whose
     s_scale has an instance forward (a memo: that layer calls its projections
-    one by one), and exact fp32 linears at the token width."""
+    one by one), exact fp32 linears at the token width, and at the token width
+    the chained layer boundaries (bit for bit the unchained stack)."""
     torch.manual_seed(43 + width)
     depth = 3
     ref = R.DiffusionTransformer(depth, heads, width, width)
@@ -255,4 +256,15 @@ def test_diffusion_stack_shared_conditioning_matches_upstream(gpu, width, heads,
     assert len(calls) == 1  # LayerNorm(s) once for the three layers
     assert max_rel(got, want) < 1e-4
     assert max_rel(memo, want) < 1e-4
+    if not windows:  # token layers chain their boundaries: layer i's last pass writes layer i + 1's operand
+        fused = []
+        real_f = ops.gated_residual_adaln_split3
+        with torch.inference_mode(), pytest.MonkeyPatch.context() as mp:
+            mp.setattr(ops, "gated_residual_adaln_split3", lambda *args, **kw: fused.append(1) or real_f(*args, **kw))
+            chained = stack(a, s, bias, mask, to_keys)
+            n_chained = len(fused)
+            mp.setattr(diffusion, "_operand_path", lambda *args, **kw: False)
+            unchained = stack(a, s, bias, mask, to_keys)
+        assert n_chained == 2 * depth - 1 and len(fused) - n_chained == depth
+        assert torch.equal(chained, unchained) and torch.equal(chained, got)
     adapters.uninstall(host)
