@@ -324,8 +324,14 @@ __device__ __forceinline__ int x3_slot(int key_in_block) {
   return ((key_in_block & 15) >> 2) * 8 + (key_in_block >> 4) * 4 + (key_in_block & 3);
 }
 
-// Thread (channel c, 32-key block kb, element b) splits K[b][kb*32 + e][c] and
-// V[b][kb*32 + e][c] for the block's 32 keys (zeros past nk).
+// Block (channels 256 bx .., 32-key block kb, element b).  V: thread c splits
+// V[b][kb*32 + e][c] of the block's 32 keys into one V^T row segment (four
+// 16-byte stores).  K: each thread takes 8 consecutive channels of 4 of the
+// block's keys (32 keys x 256 channels = 1024 such chunks), so a K row is read
+// and its hi / lo rows written 16 bytes at a time (8 | D keeps a chunk inside
+// one head).  VEC: K rows 16-byte aligned (element loads otherwise).  Keys
+// past nk are zeros.
+template <bool VEC>
 __global__ __launch_bounds__(256) void seq_attn_split_kernel(const float* __restrict__ k, const float* __restrict__ v,
                                                              int nk, int64_t ldk, int64_t sk, int heads, int d,
                                                              const float* __restrict__ mask, int64_t smask, float inf,
@@ -340,24 +346,46 @@ __global__ __launch_bounds__(256) void seq_attn_split_kernel(const float* __rest
     const int key = kb * 32 + threadIdx.x;
     mterm[b * nkp + key] = key < nk ? (1.f - mask[b * smask + key]) * -inf : -INFINITY;
   }
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int chunk = threadIdx.x + 256 * it, key = kb * 32 + chunk / 32;
+    const int c0 = blockIdx.x * 256 + 8 * (chunk % 32);
+    if (c0 < hd) {
+      f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = x0;
+      if (key < nk) {
+        const float* src = k + b * sk + (int64_t)key * ldk + c0;
+        if (VEC) {
+          x0 = *(const f32x4*)src;
+          x1 = *(const f32x4*)(src + 4);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x0[e] = src[e];
+            x1[e] = src[4 + e];
+          }
+        }
+      }
+      bf16x8 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hi[e] = (bf16)x0[e];
+        lo[e] = (bf16)(x0[e] - (float)hi[e]);
+        hi[4 + e] = (bf16)x1[e];
+        lo[4 + e] = (bf16)(x1[e] - (float)hi[4 + e]);
+      }
+      const int64_t dst = ((b * heads + c0 / d) * nkp + key) * d + c0 % d;
+      *(bf16x8*)(kh + dst) = hi;
+      *(bf16x8*)(kl + dst) = lo;
+    }
+  }
   if (c >= hd) return;
   const int hh = c / d, dd = c % d;
-  const float* kb_src = k + b * sk + c;
   const float* vb_src = v + b * sk + c;
-  bf16* kh_dst = kh + ((b * heads + hh) * nkp) * d + dd;
-  bf16* kl_dst = kl + ((b * heads + hh) * nkp) * d + dd;
   bf16x8 vh[4], vlo[4];
 #pragma unroll
   for (int e = 0; e < 32; ++e) {
     const int key = kb * 32 + e;
-    float kv = 0.f, vv = 0.f;
-    if (key < nk) {
-      kv = kb_src[(int64_t)key * ldk];
-      vv = vb_src[(int64_t)key * ldk];
-    }
-    const bf16 khi = (bf16)kv;
-    kh_dst[(int64_t)key * d] = khi;
-    kl_dst[(int64_t)key * d] = (bf16)(kv - (float)khi);
+    const float vv = key < nk ? vb_src[(int64_t)key * ldk] : 0.f;
     const int slot = x3_slot(e);
     const bf16 vhi = (bf16)vv;
     vh[slot >> 3][slot & 7] = vhi;
@@ -632,8 +660,13 @@ int launch_seq_attention_x3(const char* name, const float* q, const float* k, co
   bf16* vtl = (bf16*)((char*)ws + 3 * tile);
   float* mterm = (float*)((char*)ws + 4 * tile);
   const dim3 sgrid((unsigned)((hd + 255) / 256), (unsigned)(nkp / 32), (unsigned)batch);
-  seq_attn_split_kernel<<<sgrid, 256, 0, stream>>>(k, v, sh.nk, sh.ldk, sh.sk, heads, head_dim, mask, sh.smask, inf,
-                                                    kh, kl, vth, vtl, mterm);
+  const bool kvec = (uintptr_t)k % 16 == 0 && sh.ldk % 4 == 0 && sh.sk % 4 == 0;  // 16-byte K rows
+  if (kvec)
+    seq_attn_split_kernel<true><<<sgrid, 256, 0, stream>>>(k, v, sh.nk, sh.ldk, sh.sk, heads, head_dim, mask, sh.smask,
+                                                           inf, kh, kl, vth, vtl, mterm);
+  else
+    seq_attn_split_kernel<false><<<sgrid, 256, 0, stream>>>(k, v, sh.nk, sh.ldk, sh.sk, heads, head_dim, mask,
+                                                            sh.smask, inf, kh, kl, vth, vtl, mterm);
   if (int rc = check_launch(name)) return rc;
   const bool vec = sh.nk % 4 == 0 && sh.sbias % 4 == 0 && (uintptr_t)bias % 16 == 0;  // 16-byte bias rows
   const int64_t items = (batch + sh.bdiv - 1) / sh.bdiv * sh.bdiv * heads * ((sh.nq + kX3Q - 1) / kX3Q);
