@@ -163,17 +163,29 @@ __device__ __forceinline__ void lds_dma16(const void* src, unsigned lds_addr) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
 }
 
-// s_waitcnt vmcnt(n) with the other counters left open (n < 16).
+// s_waitcnt vmcnt(n) with the other counters left open (n < 64: the count's
+// low 4 bits in [3:0], its high 2 bits in [15:14]).
 template <int N>
 __device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
+// Persistent: block b takes the tiles b, b + G, b + 2G, ... (G = gridDim.x, a
+// multiple of 8; tile T is what block T of a one-tile-per-block grid would
+// do).  Blocks are dispatched round-robin over the 8 XCDs, so every block
+// stays on one XCD, and tile T gives XCD T % 8 whole channels: a channel's
+// operand planes stay in that XCD's L2.  Two stage buffers of BK-deep A / B
+// tiles are filled by LDS DMA, one stage ahead.  After a tile's last stage
+// the next tile's first stage goes to buffer 0 while the output is staged
+// through the LDS past buffer 0 in two halves of BM / 2 rows; the next tile's
+// first wait then leaves the epilogue's stores in flight (vmcnt counts stores
+// too), so they drain under its stages.
 template <int BM, int BN, int BK, int WM, int WN, int NS>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_kernel(
     const bf16* __restrict__ A, const bf16* __restrict__ B, bf16* __restrict__ O, int np, int tiles_n,
-    int tiles_per_ch) {
+    int tiles_per_ch, int tiles) {
+  static_assert(NS == 2, "two stage buffers");
   constexpr int kWavesN = BN / WN;
   constexpr int kWaves = (BM / WM) * kWavesN;
   constexpr int kMi = WM / 32, kNi = WN / 32;
@@ -185,30 +197,35 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
   constexpr int kDmaA = kTileA / 1024 / kWaves, kDmaB = kTileB / 1024 / kWaves;  // wave instructions per stage
   constexpr int kDma = kDmaA + kDmaB;
   static_assert(kDmaA * kWaves * 1024 == kTileA && kDmaB * kWaves * 1024 == kTileB, "tile/wave mismatch");
-  static_assert(kDma * (NS - 2) < 16, "vmcnt immediate");
   constexpr int kORow = BN * 2 + 16;              // output staging row (bytes)
-  constexpr int kSmem = NS * kStage > BM * kORow ? NS * kStage : BM * kORow;
+  constexpr int kHalf = BM / 2;                   // output rows staged at a time
+  constexpr int kChunksRow = BN * 2 / 16;
+  constexpr int kThreads = kWaves * 64;
+  constexpr int kStoresHalf = kHalf * kChunksRow / kThreads;  // 16-byte stores per thread and half
+  static_assert(kStoresHalf * kThreads == kHalf * kChunksRow && 2 * kStoresHalf < 64, "uniform epilogue stores");
+  static_assert((BM / WM) % 2 == 0, "each half of the rows belongs to whole waves");
+  constexpr int kStageOut = kStage;               // output staging: right after stage buffer 0
+  constexpr int kSmem = NS * kStage > kStageOut + kHalf * kORow ? NS * kStage : kStageOut + kHalf * kORow;
   __shared__ __attribute__((aligned(16))) char smem[kSmem];
 
-  // Blocks are dispatched round-robin over the 8 XCDs; give every XCD whole
-  // channels so the channel's operand planes stay in that XCD's L2.
-  const int b = blockIdx.x;
-  const int xcd = b & 7, idx = b >> 3;
-  const int c = xcd + 8 * (idx / tiles_per_ch);
-  const int tile = idx % tiles_per_ch;
-  const int tm = tile / tiles_n, tn = tile % tiles_n;
   const int64_t plane = (int64_t)np * np;
-  const bf16* Ac = A + c * plane + (int64_t)tm * BM * np;
-  const bf16* Bc = B + c * plane + (int64_t)tn * BN * np;
-
   const int t = threadIdx.x, l = lane_id(), wv = t >> 6;
   const int wm0 = (wv / kWavesN) * WM, wn0 = (wv % kWavesN) * WN;
   const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
+  auto operands = [&](int T, const bf16*& Ac, const bf16*& Bc, bf16*& Oc) {
+    const int xcd = T & 7, idx = T >> 3;
+    const int c = xcd + 8 * (idx / tiles_per_ch);
+    const int tile = idx % tiles_per_ch;
+    const int tm = tile / tiles_n, tn = tile % tiles_n;
+    Ac = A + c * plane + (int64_t)tm * BM * np;
+    Bc = B + c * plane + (int64_t)tn * BN * np;
+    Oc = O + c * plane + (int64_t)(tm * BM) * np + tn * BN;
+  };
 
   // DMA instruction u of this wave copies tile rows kRpi q .. kRpi q + kRpi - 1
   // (q = wave + kWaves u): lane l -> row kRpi q + l / kCpr, stored chunk
   // l % kCpr holding k-chunk (l % kCpr) ^ ((row / kSwz) % kCpr).
-  auto dma_stage = [&](int k0, int buf) {
+  auto dma_stage = [&](const bf16* Ac, const bf16* Bc, int k0, int buf) {
     const unsigned base = lds0 + buf * kStage;
 #pragma unroll
     for (int u = 0; u < kDma; ++u) {
@@ -225,61 +242,82 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
     return *(const bf16x8*)(sb + tile_off + row * (BK * 2) + ((chunk ^ ((row / kSwz) % kCpr)) * 16));
   };
 
-  f32x16 acc[kMi][kNi];
+  const int kt_count = np / BK;  // >= 1: np is a multiple of 256
+  const int G = gridDim.x;
+  int T = blockIdx.x;
+  bool prefetched = false;  // this tile's first stage is in buffer 0, requested before the last epilogue's stores
+  while (T < tiles) {  // uniform over the block
+    const bf16 *Ac, *Bc;
+    bf16* Oc;
+    operands(T, Ac, Bc, Oc);
+    f32x16 acc[kMi][kNi];
 #pragma unroll
-  for (int i = 0; i < kMi; ++i)
+    for (int i = 0; i < kMi; ++i)
 #pragma unroll
-    for (int j = 0; j < kNi; ++j) acc[i][j] = zero16();
+      for (int j = 0; j < kNi; ++j) acc[i][j] = zero16();
 
-  const int kt_count = np / BK;  // >= NS - 1: np is a multiple of 256
+    if (!prefetched) dma_stage(Ac, Bc, 0, 0);
+    for (int kt = 0; kt < kt_count; ++kt) {
+      // Stage kt is this wave's oldest outstanding memory operation except
+      // for the previous epilogue's stores (first stage of a prefetched
+      // tile); the barrier publishes every wave's copy and frees buffer
+      // (kt + 1) % 2, read in stage kt - 1.
+      if (kt == 0 && prefetched) wait_vm<2 * kStoresHalf>();
+      else wait_vm<0>();
+      __syncthreads();
+      if (kt + 1 < kt_count) dma_stage(Ac, Bc, (kt + 1) * BK, (kt + 1) & 1);
+      const char* sb = smem + (kt & 1) * kStage;
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s) dma_stage(s * BK, s);
-  for (int kt = 0; kt < kt_count; ++kt) {
-    // Stage kt has landed once at most (stages issued after it) x kDma of
-    // this wave's DMAs are outstanding; the barrier publishes every wave's.
-    const int after = kt_count - 1 - kt < NS - 2 ? kt_count - 1 - kt : NS - 2;
-    if (NS >= 3 && after == 1) wait_vm<(NS >= 3 ? kDma : 0)>();
-    else if (NS >= 4 && after == 2) wait_vm<(NS >= 4 ? 2 * kDma : 0)>();
-    else if (NS >= 5 && after == 3) wait_vm<(NS >= 5 ? 3 * kDma : 0)>();
-    else if (after == 0) wait_vm<0>();
-    __syncthreads();  // stage kt visible; stage kt - 1's buffer is free
-    if (kt + NS - 1 < kt_count) dma_stage((kt + NS - 1) * BK, (kt + NS - 1) % NS);
-    const char* sb = smem + (kt % NS) * kStage;
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        bf16x8 af[kMi], bfr[kNi];
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 af[kMi], bfr[kNi];
+        for (int i = 0; i < kMi; ++i) af[i] = sfrag(sb, 0, wm0 + 32 * i, ks);
 #pragma unroll
-      for (int i = 0; i < kMi; ++i) af[i] = sfrag(sb, 0, wm0 + 32 * i, ks);
+        for (int j = 0; j < kNi; ++j) bfr[j] = sfrag(sb, kTileA, wn0 + 32 * j, ks);
 #pragma unroll
-      for (int j = 0; j < kNi; ++j) bfr[j] = sfrag(sb, kTileA, wn0 + 32 * j, ks);
+        for (int i = 0; i < kMi; ++i)
 #pragma unroll
-      for (int i = 0; i < kMi; ++i)
-#pragma unroll
-        for (int j = 0; j < kNi; ++j) acc[i][j] = mfma32(bfr[j], af[i], acc[i][j]);
-    }
-  }
-  __syncthreads();  // every wave is done with the stage buffers
-
-  // acc[i][j] = D[n][m]: lane -> m = wm0 + 32 i + l%32, registers 4q'..4q'+3 ->
-  // n = wn0 + 32 j + 8q' + 4(l/32) + 0..3, written as one 8-byte LDS store.
-#pragma unroll
-  for (int i = 0; i < kMi; ++i)
-#pragma unroll
-    for (int j = 0; j < kNi; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = wm0 + 32 * i + (l & 31), nn = wn0 + 32 * j + 8 * q + 4 * (l >> 5);
-        const bf16x4 v = {(bf16)acc[i][j][4 * q], (bf16)acc[i][j][4 * q + 1], (bf16)acc[i][j][4 * q + 2],
-                          (bf16)acc[i][j][4 * q + 3]};
-        *(bf16x4*)(smem + m * kORow + nn * 2) = v;
+          for (int j = 0; j < kNi; ++j) acc[i][j] = mfma32(bfr[j], af[i], acc[i][j]);
       }
-  __syncthreads();
-  bf16* Oc = O + c * plane + (int64_t)(tm * BM) * np + tn * BN;
-  constexpr int kChunksRow = BN * 2 / 16;
-#pragma unroll 4
-  for (int e = t; e < BM * kChunksRow; e += kWaves * 64) {
-    const int m = e / kChunksRow, ch = e % kChunksRow;
-    *(bf16x8*)(Oc + (int64_t)m * np + 8 * ch) = *(const bf16x8*)(smem + m * kORow + 16 * ch);
+    }
+    __syncthreads();  // every wave is done with the stage buffers
+
+    int next = T + G;
+    prefetched = next < tiles;
+    if (prefetched) {  // the next tile's first stage, into buffer 0, ahead of this tile's stores
+      const bf16 *An, *Bn;
+      bf16* On;
+      operands(next, An, Bn, On);
+      dma_stage(An, Bn, 0, 0);
+    }
+    // acc[i][j] = D[n][m]: lane -> m = wm0 + 32 i + l%32, registers 4q'..4q'+3 ->
+    // n = wn0 + 32 j + 8q' + 4(l/32) + 0..3, written as one 8-byte LDS store.
+    // Rows [h kHalf, (h + 1) kHalf) belong to the waves with wm0 in that range.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (wm0 / kHalf == h) {  // wave-uniform
+#pragma unroll
+        for (int i = 0; i < kMi; ++i)
+#pragma unroll
+          for (int j = 0; j < kNi; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int m = wm0 - h * kHalf + 32 * i + (l & 31), nn = wn0 + 32 * j + 8 * q + 4 * (l >> 5);
+              const bf16x4 v = {(bf16)acc[i][j][4 * q], (bf16)acc[i][j][4 * q + 1], (bf16)acc[i][j][4 * q + 2],
+                                (bf16)acc[i][j][4 * q + 3]};
+              *(bf16x4*)(smem + kStageOut + m * kORow + nn * 2) = v;
+            }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int e0 = 0; e0 < kStoresHalf; ++e0) {
+        const int e = t + kThreads * e0;
+        const int m = e / kChunksRow, ch = e % kChunksRow;
+        *(bf16x8*)(Oc + (int64_t)(h * kHalf + m) * np + 8 * ch) = *(const bf16x8*)(smem + kStageOut + m * kORow + 16 * ch);
+      }
+      __syncthreads();  // the staging rows are free again (and, after the second half, stage buffer 1)
+    }
+    T = next;
   }
 }
 
@@ -462,9 +500,11 @@ int launch(const float* x, const float* mask, int ni, int outgoing, const float*
     // slower (more barriers per k), as did register staging of the operands.
     constexpr int BM = 256, BN = 256, BK = 64, WM = 64, WN = 128, NS = 2;
     const int tiles_n = np / BN, tiles_per_ch = (np / BM) * tiles_n;
+    // persistent, one block per CU (its LDS holds two stages), a multiple of 8 so each block keeps one XCD
+    const int tiles = kC * tiles_per_ch;
+    const int grid = std::min(tiles, 8 * ((device_cu_count() + 7) / 8));
     trimul_contract_kernel<BM, BN, BK, WM, WN, NS>
-        <<<dim3(kC * tiles_per_ch), (BM / WM) * (BN / WN) * 64, 0, stream>>>(a_pl, b_pl, o_pl, np, tiles_n,
-                                                                             tiles_per_ch);
+        <<<dim3(grid), (BM / WM) * (BN / WN) * 64, 0, stream>>>(a_pl, b_pl, o_pl, np, tiles_n, tiles_per_ch, tiles);
     if (int rc = check_launch("trimul_contract")) return rc;
   }
   if (stages & 4) {
