@@ -730,7 +730,7 @@ def diffusion_kernel_times(stacks, t, packed, samples, tokens):
     (4 x 32), AdaLN and the conditioned-transition epilogues at the token
     shape; launches per step count every layer."""
     import torch
-    from boltz_lumi_amd import ops
+    from boltz_lumi_amd import _native as N, ops
     from boltz_lumi_amd.pair_bias import prepare_window_bias
 
     dev = t["a"].device
