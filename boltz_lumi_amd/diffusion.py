@@ -146,7 +146,7 @@ class _Side:
 
     def __init__(self, s):
         self.s = s.reshape(-1, s.shape[-1])
-        self.split = ops.use_split(s.shape[-1])
+        self.split = ops.use_split(s.shape[-1], s.numel() // max(s.shape[-1], 1))
         self._norm = {}
         self._raw = None
 

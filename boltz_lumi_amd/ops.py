@@ -392,10 +392,14 @@ def mm_x3(x, w3):
     return mm_split(split3(x.float()), w3)
 
 
-# Narrower fp32 linears (the atom transformer's 128 / 256) measured faster on
-# hipBLASLt's fp32 GEMM than as split-bf16 GEMMs; from 512 up (the token
-# transformer's 768 / 1536) the split form is ~1.5x faster per block.
+# fp32 linears run as split-bf16 GEMMs from 512 input channels up (the token
+# transformer's 768 / 1536: ~1.5x faster per block), and from 128 up when
+# they are tall (the atom transformer's 5 x 8192 rows at 128 / 256 channels:
+# 46.5 against 65.3 us at N = 512, 53 against 89 us at N = 768, 0.23 ms per
+# configs[4] step).  Short narrow ones (the Pairformer sequence stack's 1024
+# rows of 384) stay on hipBLASLt's fp32 GEMM.
 X3_MIN_K = 512
+X3_TALL_MIN_K, X3_TALL_MIN_ROWS = 128, 16384
 
 # Set BMX_EXACT_FP32_LINEARS=1 (or call exact_fp32_linears(True)) to run every
 # fp32 linear of the diffusion blocks and of fp32-mode triangle attention as a
@@ -413,16 +417,18 @@ def exact_fp32_linears(enabled: bool = True) -> bool:
     return before
 
 
-def use_split(k: int) -> bool:
-    """Whether fp32 linears of ``k`` input channels run as split-bf16 GEMMs."""
-    return not _EXACT_FP32[0] and k >= X3_MIN_K and k % 4 == 0
+def use_split(k: int, rows: int = 0) -> bool:
+    """Whether fp32 linears of ``k`` input channels over ``rows`` rows run as
+    split-bf16 GEMMs (never in exact fp32 mode)."""
+    if _EXACT_FP32[0] or k % 4:
+        return False
+    return k >= X3_MIN_K or (k >= X3_TALL_MIN_K and rows >= X3_TALL_MIN_ROWS)
 
 
 def linear_fp32(x, linear):
-    """``linear(x)`` for fp32 x: ``linear_x3`` for input widths >= X3_MIN_K
-    (multiples of 4) unless exact fp32 linears are switched on, else the fp32
-    GEMM."""
-    if use_split(x.shape[-1]):
+    """``linear(x)`` for fp32 x: ``linear_x3`` where ``use_split`` says so
+    (never with exact fp32 linears switched on), else the fp32 GEMM."""
+    if use_split(x.shape[-1], x.numel() // max(x.shape[-1], 1)):
         return linear_x3(x, linear)
     return torch.nn.functional.linear(x, linear.weight, linear.bias)
 
