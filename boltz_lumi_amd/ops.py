@@ -397,9 +397,11 @@ def mm_x3(x, w3):
 # they are tall (the atom transformer's 5 x 8192 rows at 128 / 256 channels:
 # 46.5 against 65.3 us at N = 512, 53 against 89 us at N = 768, 0.23 ms per
 # configs[4] step).  Short narrow ones (the Pairformer sequence stack's 1024
-# rows of 384) stay on hipBLASLt's fp32 GEMM.
+# rows of 384) stay on hipBLASLt's fp32 GEMM, and so do tall narrow ones with
+# fewer than 512 outputs whose operand needs a split pass of its own (40 960 x
+# 128: 12 us for the pass + 27 us against 29 us in fp32 at N = 128).
 X3_MIN_K = 512
-X3_TALL_MIN_K, X3_TALL_MIN_ROWS = 128, 16384
+X3_TALL_MIN_K, X3_TALL_MIN_ROWS, X3_TALL_MIN_N = 128, 16384, 512
 
 # Set BMX_EXACT_FP32_LINEARS=1 (or call exact_fp32_linears(True)) to run every
 # fp32 linear of the diffusion blocks and of fp32-mode triangle attention as a
@@ -417,18 +419,19 @@ def exact_fp32_linears(enabled: bool = True) -> bool:
     return before
 
 
-def use_split(k: int, rows: int = 0) -> bool:
+def use_split(k: int, rows: int = 0, n: int | None = None) -> bool:
     """Whether fp32 linears of ``k`` input channels over ``rows`` rows run as
-    split-bf16 GEMMs (never in exact fp32 mode)."""
+    split-bf16 GEMMs (never in exact fp32 mode).  ``n``: the GEMM's outputs
+    when its operand is split for it alone (None: a shared split operand)."""
     if _EXACT_FP32[0] or k % 4:
         return False
-    return k >= X3_MIN_K or (k >= X3_TALL_MIN_K and rows >= X3_TALL_MIN_ROWS)
+    return k >= X3_MIN_K or (k >= X3_TALL_MIN_K and rows >= X3_TALL_MIN_ROWS and (n is None or n >= X3_TALL_MIN_N))
 
 
 def linear_fp32(x, linear):
     """``linear(x)`` for fp32 x: ``linear_x3`` where ``use_split`` says so
     (never with exact fp32 linears switched on), else the fp32 GEMM."""
-    if use_split(x.shape[-1], x.numel() // max(x.shape[-1], 1)):
+    if use_split(x.shape[-1], x.numel() // max(x.shape[-1], 1), linear.weight.shape[0]):
         return linear_x3(x, linear)
     return torch.nn.functional.linear(x, linear.weight, linear.bias)
 

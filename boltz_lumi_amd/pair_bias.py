@@ -63,7 +63,8 @@ def _joint_projection(module, name, x, linears):
     autocast, else fp32 (split-bf16 where ``ops.use_split`` says so)."""
     weights = tuple(lin.weight for lin in linears)
     biases = [lin.bias for lin in linears]
-    if not torch.is_autocast_enabled() and ops.use_split(x.shape[-1], x.numel() // max(x.shape[-1], 1)):
+    if not torch.is_autocast_enabled() and ops.use_split(x.shape[-1], x.numel() // max(x.shape[-1], 1),
+                                                         sum(lin.weight.shape[0] for lin in linears)):
         y = ops.mm_x3(x.reshape(-1, x.shape[-1]), ops.x3_weight(module, name + "_x3", weights, biases))
         return y.view(x.shape[:-1] + (y.shape[-1],))
     bias = None
@@ -97,7 +98,7 @@ def fused_attention(module, s, z, mask, k_in, multiplicity=1, bias=None):
     batch, nq, nk = s.shape[0], s.shape[1], k_in.shape[1]
     if k_in is s:
         weights = (module.proj_q.weight, module.proj_k.weight, module.proj_v.weight, module.proj_g.weight)
-        if not torch.is_autocast_enabled() and ops.use_split(width, s.numel() // width):
+        if not torch.is_autocast_enabled() and ops.use_split(width, s.numel() // width, 4 * width):
             # fp32 at the token transformer's width or rows: one split-bf16 GEMM with fp32 accumulation
             biases = (module.proj_q.bias, module.proj_k.bias, module.proj_v.bias, module.proj_g.bias)
             proj = ops.mm_x3(s.reshape(-1, width), ops.x3_weight(module, "qkvg_x3", weights, biases))

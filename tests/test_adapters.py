@@ -229,12 +229,14 @@ def test_window_probe_on_cpu():
 def test_split_bf16_threshold_follows_width_and_rows():
     """fp32 linears run split-bf16 from 512 input channels (the token
     transformer), or from 128 with at least 16384 rows (the atom transformer's
-    5 x 8192 atoms); never for widths that are not multiples of 4 or in exact
-    fp32 mode; the Pairformer sequence stack's 1024 rows of 384 stay fp32."""
+    5 x 8192 atoms) when their operand is shared or they have 512+ outputs;
+    never for widths that are not multiples of 4 or in exact fp32 mode; the
+    Pairformer sequence stack's 1024 rows of 384 stay fp32."""
     from boltz_lumi_amd import ops
 
     assert ops.use_split(768) and ops.use_split(768, 10) and ops.use_split(1536, 5120)
-    assert ops.use_split(128, 40960) and ops.use_split(256, 16384)
+    assert ops.use_split(128, 40960) and ops.use_split(256, 16384) and ops.use_split(128, 40960, 512)
+    assert not ops.use_split(128, 40960, 128) and not ops.use_split(256, 40960, 256) and ops.use_split(768, 64, 128)
     assert not ops.use_split(384, 1024) and not ops.use_split(128, 512) and not ops.use_split(128)
     assert not ops.use_split(64, 10 ** 6) and not ops.use_split(770, 5120)
     before = ops.exact_fp32_linears(True)
