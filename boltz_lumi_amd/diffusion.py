@@ -228,10 +228,11 @@ def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity, keys=N
     windows by address (``windowed_attention``) instead of ``to_keys``.
 
     ``carry`` = (attention operand, mods, gates) of this layer, computed by the
-    previous layer's last pass; with ``nxt`` (the next layer, on the operand
-    path too) this layer's last residual update also writes the next layer's
-    attention operand (``gated_residual_adaln_split3``), and the result is
-    (a, carry for ``nxt``) instead of a."""
+    previous layer's last pass; with ``nxt`` (the next layer, whose attention
+    also starts from the AdaLN's split operand: the token path, or windows
+    with split linears) this layer's last residual update also writes the next
+    layer's attention operand (``gated_residual_adaln_split3``), and the
+    result is (a, carry for ``nxt``) instead of a."""
     d = a.shape[-1]
     tr = self.transition
     eps = self.adaln.s_norm.eps
@@ -251,6 +252,10 @@ def _layer_with_side(self, a, s, side, bias, mask, to_keys, multiplicity, keys=N
         pl = att.proj_o
         b = ops.mm_split(o, ops.x3_weight(pl, "x3", (pl.weight,), (pl.bias,))).view(a.shape)
     elif o is not None:
+        b = att.proj_o(o) if "forward" in vars(att.proj_o) else ops.linear_fp32(o, att.proj_o)
+    elif keys is not None and side.split:  # the AdaLN output only as the projection's split operand
+        op = ops.adaln_split3(rows, scale_a, shift_a, self.adaln.a_norm.eps) if carry is None else carry[0]
+        o = windowed_attention(att, None, bias, keys, op=op, shape=a.shape)
         b = att.proj_o(o) if "forward" in vars(att.proj_o) else ops.linear_fp32(o, att.proj_o)
     elif keys is not None:
         b = ops.adaln_modulate(rows, scale_a, shift_a, self.adaln.a_norm.eps).view(a.shape)
@@ -461,6 +466,12 @@ def atom_transformer_forward(self, q, c, bias, to_keys, mask, multiplicity=1, *a
     heads = bias.shape[4] // len(layers)
     side = _Side(cw)
     a = qw
+    carry = None
     for i, layer in enumerate(layers):
-        a = _layer_with_side(layer, a, cw, side, bias[..., i * heads:(i + 1) * heads], None, None, 1, keys)
+        # with split linears, consecutive layers chain their boundary pass as the token transformer's do
+        nxt = (layers[i + 1] if side.split and i + 1 < len(layers) and isinstance(layer.post_lnorm, torch.nn.Identity)
+               else None)
+        out = _layer_with_side(layer, a, cw, side, bias[..., i * heads:(i + 1) * heads], None, None, 1, keys,
+                               carry=carry, nxt=nxt)
+        a, carry = out if nxt is not None else (out, None)
     return a.view(b, n, d)

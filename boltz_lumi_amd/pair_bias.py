@@ -178,7 +178,7 @@ def windowed_ok(module) -> bool:
             and module.proj_k.bias is None and module.proj_v.bias is None)
 
 
-def windowed_attention(module, s, bias, keys):
+def windowed_attention(module, s, bias, keys, op=None, shape=None):
     """``sigmoid(proj_g(s)) * attention`` of AttentionPairBias ``module`` (before
     ``proj_o``) for query windows s [E, W, c_s] whose keys are the window gather
     of the same rows (upstream ``to_keys``): q | k | v | g are one projection of
@@ -186,10 +186,16 @@ def windowed_attention(module, s, bias, keys):
     (``ops.seq_attention_windowed``), so neither the gathered rows nor their
     projection is materialised.  ``keys`` carries the gather (``windows``,
     ``offset``, ``bias_group``, the atom ``mask``); ``bias`` is this layer's
-    [Eb, ..., W, NK, heads] view of the atom bias."""
-    e, w, width = s.shape
+    [Eb, ..., W, NK, heads] view of the atom bias.  With ``op`` the rows come
+    as their split-bf16 operand ([E W, 3 c_s + 64], e.g. written by
+    ``ops.adaln_split3``; s is then None and ``shape`` its [E, W, c_s])."""
+    e, w, width = s.shape if op is None else shape
     lin = (module.proj_q, module.proj_k, module.proj_v, module.proj_g)
-    proj = _joint_projection(module, "qkvg", s.reshape(e * w, width), lin)
+    if op is None:
+        proj = _joint_projection(module, "qkvg", s.reshape(e * w, width), lin)
+    else:  # the weights _joint_projection caches for its split form
+        proj = ops.mm_split(op, ops.x3_weight(module, "qkvg_x3", tuple(m.weight for m in lin),
+                                              tuple(m.bias for m in lin)))
     q, k, v, g = proj.split(width, dim=-1)
     return ops.seq_attention_windowed(q.view(e, w, width), k, v, bias.float(), keys.mask, g.view(e, w, width),
                                       module.inf, windows=keys.windows, key_offset=keys.offset,
