@@ -411,8 +411,13 @@ __device__ __forceinline__ f32x4 mfma16bf(bf16x8 a, bf16x8 b, f32x4 c) {
 // One LDS DMA: 64 lanes x 16 bytes from per-lane global addresses to
 // lds_addr + 16 * lane; waited for explicitly (s_waitcnt vmcnt(0)) before the
 // barrier that publishes the stage.
+// The DMA reads M0, which the compiler writes with an SALU instruction right
+// before the asm; gfx9 needs one wait state between the two (s_nop 0), which
+// the compiler's hazard recognizer inserts for its own LDS DMA but cannot see
+// inside inline asm: without it the DMA may use the previous M0 and write its
+// 1 KB over another stage region.
 __device__ __forceinline__ void lds_dma16(const void* src, unsigned lds_addr) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
 }
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 

@@ -294,8 +294,13 @@ constexpr int kStageBytes = kOffMb + kRows * kKT * 4;
 // lds_addr + 16 * lane.  Issued as inline asm so that the compiler does not
 // wait for it before unrelated LDS reads: the kernel waits for its DMAs
 // explicitly (s_waitcnt vmcnt) before the barrier that publishes them.
+// The DMA reads M0, which the compiler writes with an SALU instruction right
+// before the asm; gfx9 needs one wait state between the two (s_nop 0), which
+// the compiler's hazard recognizer inserts for its own LDS DMA but cannot see
+// inside inline asm: without it the DMA may use the previous M0 and write its
+// 1 KB over another stage region.
 __device__ __forceinline__ void lds_dma16(const void* src, unsigned lds_addr) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
 }
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 __device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }

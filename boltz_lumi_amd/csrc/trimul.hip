@@ -159,8 +159,13 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
 // and no staging registers are needed.  The MFMA computes D[n][m] (B as the
 // A operand), so a lane holds 4 consecutive n of one row m: the result goes
 // through LDS with 8-byte writes and leaves as 16-byte row stores.
+// The DMA reads M0, which the compiler writes with an SALU instruction right
+// before the asm; gfx9 needs one wait state between the two (s_nop 0), which
+// the compiler's hazard recognizer inserts for its own LDS DMA but cannot see
+// inside inline asm: without it the DMA may use the previous M0 and write its
+// 1 KB over another stage region.
 __device__ __forceinline__ void lds_dma16(const void* src, unsigned lds_addr) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
 }
 
 // s_waitcnt vmcnt(n) with the other counters left open (n < 64: the count's
