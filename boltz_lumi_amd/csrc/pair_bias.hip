@@ -324,32 +324,34 @@ __device__ __forceinline__ int x3_slot(int key_in_block) {
   return ((key_in_block & 15) >> 2) * 8 + (key_in_block >> 4) * 4 + (key_in_block & 3);
 }
 
-// Block (channels 256 bx .., 32-key block kb, element b).  V: thread c splits
-// V[b][kb*32 + e][c] of the block's 32 keys into one V^T row segment (four
-// 16-byte stores).  K: each thread takes 8 consecutive channels of 4 of the
-// block's keys (32 keys x 256 channels = 1024 such chunks), so a K row is read
-// and its hi / lo rows written 16 bytes at a time (8 | D keeps a chunk inside
-// one head).  VEC: K rows 16-byte aligned (element loads otherwise).  Keys
-// past nk are zeros.
-template <bool VEC>
+// Block (channels span bx .., KG 32-key blocks from KG by, element b), span =
+// 256 / KG: KG = 2 where the row has at most 128 channels, so that every
+// thread has work.  V: thread t splits V[b][key][c] of the 32 keys of key
+// block KG by + t / span, channel c = span bx + t % span, into one V^T row
+// segment (four 16-byte stores).  K: each thread takes 8 consecutive channels
+// of 4 of the block's keys (KG x 32 keys x span channels = 1024 such chunks),
+// so a K row is read and its hi / lo rows written 16 bytes at a time (8 | D
+// keeps a chunk inside one head).  VEC: K rows 16-byte aligned (element loads
+// otherwise).  Keys past nk are zeros.
+template <bool VEC, int KG>
 __global__ __launch_bounds__(256) void seq_attn_split_kernel(const float* __restrict__ k, const float* __restrict__ v,
                                                              int nk, int64_t ldk, int64_t sk, int heads, int d,
                                                              const float* __restrict__ mask, int64_t smask, float inf,
                                                              bf16* __restrict__ kh, bf16* __restrict__ kl,
                                                              bf16* __restrict__ vth, bf16* __restrict__ vtl,
                                                              float* __restrict__ mterm) {
+  constexpr int span = 256 / KG, c8 = span / 8;
   const int hd = heads * d;
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  const int kb = blockIdx.y;
   const int64_t b = blockIdx.z, nkp = x3_nkp(nk);
-  if (blockIdx.x == 0 && threadIdx.x < 32) {  // the additive mask term of key kb * 32 + lane; -inf past nk
-    const int key = kb * 32 + threadIdx.x;
+  if (blockIdx.x == 0 && threadIdx.x < 32 * KG) {  // the additive mask term of each key; -inf past nk
+    const int key = blockIdx.y * 32 * KG + threadIdx.x;
     mterm[b * nkp + key] = key < nk ? (1.f - mask[b * smask + key]) * -inf : -INFINITY;
   }
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
-    const int chunk = threadIdx.x + 256 * it, key = kb * 32 + chunk / 32;
-    const int c0 = blockIdx.x * 256 + 8 * (chunk % 32);
+    const int chunk = threadIdx.x + 256 * it, sub = chunk / (32 * c8), rem = chunk % (32 * c8);
+    const int key = (blockIdx.y * KG + sub) * 32 + rem / c8;
+    const int c0 = blockIdx.x * span + 8 * (rem % c8);
     if (c0 < hd) {
       f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = x0;
       if (key < nk) {
@@ -378,6 +380,7 @@ __global__ __launch_bounds__(256) void seq_attn_split_kernel(const float* __rest
       *(bf16x8*)(kl + dst) = lo;
     }
   }
+  const int c = blockIdx.x * span + threadIdx.x % span, kb = blockIdx.y * KG + threadIdx.x / span;
   if (c >= hd) return;
   const int hh = c / d, dd = c % d;
   const float* vb_src = v + b * sk + c;
@@ -664,14 +667,18 @@ int launch_seq_attention_x3(const char* name, const float* q, const float* k, co
   bf16* vth = (bf16*)((char*)ws + 2 * tile);
   bf16* vtl = (bf16*)((char*)ws + 3 * tile);
   float* mterm = (float*)((char*)ws + 4 * tile);
-  const dim3 sgrid((unsigned)((hd + 255) / 256), (unsigned)(nkp / 32), (unsigned)batch);
   const bool kvec = (uintptr_t)k % 16 == 0 && sh.ldk % 4 == 0 && sh.sk % 4 == 0;  // 16-byte K rows
-  if (kvec)
-    seq_attn_split_kernel<true><<<sgrid, 256, 0, stream>>>(k, v, sh.nk, sh.ldk, sh.sk, heads, head_dim, mask, sh.smask,
-                                                           inf, kh, kl, vth, vtl, mterm);
-  else
-    seq_attn_split_kernel<false><<<sgrid, 256, 0, stream>>>(k, v, sh.nk, sh.ldk, sh.sk, heads, head_dim, mask,
-                                                            sh.smask, inf, kh, kl, vth, vtl, mterm);
+  // rows of at most 128 channels: 64 keys per block (nkp is a multiple of 64)
+  const int kg = hd <= 128 ? 2 : 1, span = 256 / kg;
+  const dim3 sgrid((unsigned)((hd + span - 1) / span), (unsigned)(nkp / (32 * kg)), (unsigned)batch);
+#define SEQ_ATTN_SPLIT(VEC, KG)                                                                                \
+  seq_attn_split_kernel<VEC, KG><<<sgrid, 256, 0, stream>>>(k, v, sh.nk, sh.ldk, sh.sk, heads, head_dim, mask, \
+                                                            sh.smask, inf, kh, kl, vth, vtl, mterm)
+  if (kvec && kg == 2) SEQ_ATTN_SPLIT(true, 2);
+  else if (kvec) SEQ_ATTN_SPLIT(true, 1);
+  else if (kg == 2) SEQ_ATTN_SPLIT(false, 2);
+  else SEQ_ATTN_SPLIT(false, 1);
+#undef SEQ_ATTN_SPLIT
   if (int rc = check_launch(name)) return rc;
   const bool vec = sh.nk % 4 == 0 && sh.sbias % 4 == 0 && (uintptr_t)bias % 16 == 0;  // 16-byte bias rows
   const int64_t items = (batch + sh.bdiv - 1) / sh.bdiv * sh.bdiv * heads * ((sh.nq + kX3Q - 1) / kX3Q);
