@@ -35,6 +35,7 @@ SIGNATURES = {
     "bmx_silu_mul": (c_int, [_P, _P, _P, c_int64, _P]),
     "bmx_split3_bf16": (c_int, [_P, c_int64, c_int64, c_int64, _P, _P]),
     "bmx_layernorm_split3_bf16": (c_int, [_P, c_int64, c_int, c_int64, c_float, _P, _P]),
+    "bmx_layernorm_split3_t_bf16": (c_int, [_P, c_int64, c_int, c_int64, c_float, _P, _P]),
     "bmx_adaln_split3_bf16": (c_int, [_P, _P, _P, c_int64, c_int64, c_int, c_float, _P, _P]),
     "bmx_swiglu_split3_bf16": (c_int, [_P, c_int64, c_int64, c_int64, _P, _P]),
     "bmx_gated_residual_adaln_split3_bf16": (c_int, [_P, _P, c_int64, _P, _P, _P, _P, c_int64, c_int64, c_int, c_float,

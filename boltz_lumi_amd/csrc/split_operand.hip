@@ -17,6 +17,7 @@
 //
 //  bmx_split3_bf16            x                                -> operand
 //  bmx_layernorm_split3_bf16  LayerNorm without affine of x    -> operand
+//  bmx_layernorm_split3_t_bf16  the same over the transposed pairs of a square frame
 //  bmx_adaln_split3_bf16      sigmoid(scale) * LN(a) + shift    -> operand
 //  bmx_swiglu_split3_bf16     silu(g) * x * b of one projection -> operand
 //  bmx_gated_residual_adaln_split3_bf16  c + sigmoid(g) * a -> out, and the AdaLN
@@ -89,14 +90,16 @@ __device__ __forceinline__ RowNorm row_norm(const f32x4 (&v)[kRowChunks], int la
   return RowNorm{mean, rsqrtf(wave_sum_full(q) / d + eps)};
 }
 
+// tn > 0: the rows of x are the pairs of a tn x tn frame read transposed
+// (operand row i tn + j is x row j tn + i).
 __global__ __launch_bounds__(256) void layernorm_split3_kernel(const float* __restrict__ x, int64_t ldx,
                                                                bf16* __restrict__ out, int64_t rows, int d,
-                                                               float eps) {
+                                                               float eps, int64_t tn) {
 #pragma clang fp contract(off)
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63, chunks = d >> 2;
-  const float* xr = x + row * ldx;
+  const float* xr = x + (tn ? (row % tn) * tn + row / tn : row) * ldx;
   f32x4 v[kRowChunks];
 #pragma unroll
   for (int u = 0; u < kRowChunks; ++u) v[u] = load4(xr + 4 * min(lane + kWave * u, chunks - 1));
@@ -242,8 +245,22 @@ int bmx_layernorm_split3_bf16(const float* x, int64_t rows, int dim, int64_t ldx
   BMX_REQUIRE(x && out, "bmx_layernorm_split3_bf16: null pointer");
   BMX_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)out % 8 == 0,
               "bmx_layernorm_split3_bf16: x must be 16-byte and out 8-byte aligned");
-  layernorm_split3_kernel<<<row_blocks(rows), 256, 0, stream>>>(x, ldx, (bf16*)out, rows, dim, eps);
+  layernorm_split3_kernel<<<row_blocks(rows), 256, 0, stream>>>(x, ldx, (bf16*)out, rows, dim, eps, 0);
   return check_launch("bmx_layernorm_split3_bf16");
+}
+
+int bmx_layernorm_split3_t_bf16(const float* x, int64_t n, int dim, int64_t ldx, float eps, void* out,
+                                hipStream_t stream) {
+  BMX_REQUIRE(n >= 0 && dim > 0 && dim % 4 == 0 && dim <= 4 * kWave * kRowChunks && ldx >= dim && ldx % 4 == 0,
+              "bmx_layernorm_split3_t_bf16: need 0 < dim <= 1024, dim %% 4 == 0, ldx >= dim, ldx %% 4 == 0");
+  BMX_REQUIRE(eps > 0.f, "bmx_layernorm_split3_t_bf16: eps must be positive");
+  BMX_REQUIRE(n < (int64_t)1 << 16, "bmx_layernorm_split3_t_bf16: n must be < 65536");
+  if (n == 0) return BMX_OK;
+  BMX_REQUIRE(x && out, "bmx_layernorm_split3_t_bf16: null pointer");
+  BMX_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)out % 8 == 0,
+              "bmx_layernorm_split3_t_bf16: x must be 16-byte and out 8-byte aligned");
+  layernorm_split3_kernel<<<row_blocks(n * n), 256, 0, stream>>>(x, ldx, (bf16*)out, n * n, dim, eps, n);
+  return check_launch("bmx_layernorm_split3_t_bf16");
 }
 
 int bmx_adaln_split3_bf16(const float* a, const float* scale, const float* shift, int64_t ld_mod, int64_t rows,

@@ -261,6 +261,21 @@ def layernorm_split3(x, eps):
     return out
 
 
+def layernorm_split3_t(x, eps):
+    """``layernorm_split3`` of the rows of ``x.transpose(0, 1)`` for a square
+    pair frame x [N, N, k] with dense rows, without the transposed copy
+    (``bmx_layernorm_split3_t_bf16``); bf16 [N, N, 3 k + 64]."""
+    _cuda(x)
+    _check(x.dim() == 3 and x.shape[0] == x.shape[1] and x.dtype == torch.float32 and x.is_contiguous()
+           and 0 < x.shape[-1] <= 1024 and x.shape[-1] % 4 == 0,
+           "expected contiguous fp32 x [N, N, k] with a multiple of 4 columns, at most 1024")
+    n, k = x.shape[0], x.shape[-1]
+    out = _split_out(x, k)
+    if n:
+        N.call("bmx_layernorm_split3_t_bf16", x.data_ptr(), n, k, k, float(eps), out.data_ptr(), _stream(x))
+    return out
+
+
 def _same_rows(a, *mods):
     """Row stride shared by ``mods`` (column slices of one projection, or dense
     tensors of a's shape)."""
@@ -616,12 +631,14 @@ def triattn_fp32(module, x, mask, starting):
     mha, heads, d = module.mha, module.no_heads, module.c_hidden
     _check(heads * d == C, "expected heads x head dim = 128")
     if not starting:
-        x = x.transpose(0, 1)
         mask = None if mask is None else mask.transpose(0, 1)
-    x = x.contiguous()
     ln = module.layer_norm
     lins = (mha.linear_q, mha.linear_k, mha.linear_v, mha.linear_g, module.linear)
-    if not _EXACT_FP32[0] and ln.weight is not None:
+    split = not _EXACT_FP32[0] and ln.weight is not None
+    # the ending node works on x transposed: the split path's LayerNorm reads the transposed rows in
+    # place, the exact path transposes x once
+    x = x.contiguous() if starting or split else x.transpose(0, 1).contiguous()
+    if split:
         # q | k | v | g and the triangle bias as one split-bf16 GEMM of LayerNorm-without-affine(x), the
         # LayerNorm affine folded into the weights: (W diag w) LN0(x) + (bias + W b)
         def fold(*_):
@@ -638,7 +655,9 @@ def triattn_fp32(module, x, mask, starting):
         srcs = tuple(t for m_ in (ln,) + lins for t in (m_.weight, m_.bias) if t is not None)
         _check(4 * C + heads <= TRIATTN_FP32_PROJ_COLS, "too many heads")
         w3 = cached_weight(module, "qkvgb_ln_x3", srcs, fold)
-        proj = mm_split(layernorm_split3(x.view(-1, C), ln.eps), w3).view(n, n, TRIATTN_FP32_PROJ_COLS)
+        op = (layernorm_split3(x.view(-1, C), ln.eps) if starting
+              else layernorm_split3_t(x, ln.eps).view(-1, split_width(C)))
+        proj = mm_split(op, w3).view(n, n, TRIATTN_FP32_PROJ_COLS)
         tri_bias = proj[..., 4 * C:4 * C + heads].permute(2, 0, 1).contiguous()  # [H, q, k], shared by every row
     else:
         xn = norm(x.view(-1, C), _f32(ln.weight), _f32(ln.bias), ln.eps, bf16_output=False)

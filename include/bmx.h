@@ -107,6 +107,13 @@ int bmx_split3_bf16(const float* x, int64_t rows, int64_t k, int64_t ldx, void* 
 int bmx_layernorm_split3_bf16(const float* x, int64_t rows, int dim, int64_t ldx, float eps, void* out,
                               bmx_stream_t stream);
 
+/* bmx_layernorm_split3_bf16 over the pairs of an n x n frame read transposed: operand row i n + j
+ * is x row j n + i.  The ending-node triangle attention's fp32-mode projection operand
+ * (reference triangle.py:38-52 runs TriangleAttentionEndingNode on x.transpose(-2, -3)), without a
+ * transposed copy of x. */
+int bmx_layernorm_split3_t_bf16(const float* x, int64_t n, int dim, int64_t ldx, float eps, void* out,
+                                bmx_stream_t stream);
+
 /* Operand rows of sigmoid(scale) * LN_noaffine(a) + shift (rounded as bmx_adaln), a dense
  * [rows][dim], scale / shift rows at stride ld_mod: the AdaLN output that feeds the
  * attention's q|k|v|g and the transition's swish_gate|a_to_b projections (diffusion.py:52-68). */

@@ -98,6 +98,9 @@ def test_argument_validation_needs_no_gpu(lib):
     assert rc == N.BMX_EINVAL and b"ldx >= k" in lib.bmx_last_error()
     rc = lib.bmx_layernorm_split3_bf16(fake, 4, 1028, 1028, ctypes.c_float(1e-5), fake, None)
     assert rc == N.BMX_EINVAL and b"dim <= 1024" in lib.bmx_last_error()
+    assert lib.bmx_layernorm_split3_t_bf16(None, 0, 128, 128, ctypes.c_float(1e-5), None, None) == N.BMX_OK
+    rc = lib.bmx_layernorm_split3_t_bf16(fake, 1 << 16, 128, 128, ctypes.c_float(1e-5), fake, None)
+    assert rc == N.BMX_EINVAL and b"n must be < 65536" in lib.bmx_last_error()
     rc = lib.bmx_adaln_split3_bf16(fake, fake, fake, 512, 4, 768, ctypes.c_float(1e-5), fake, None)
     assert rc == N.BMX_EINVAL and b"ld_mod >= dim" in lib.bmx_last_error()
     rc = lib.bmx_adaln_split3_bf16(fake, ctypes.c_void_p(260), fake, 768, 4, 768, ctypes.c_float(1e-5), fake, None)

@@ -71,6 +71,19 @@ def test_layernorm_split3_matches_fp64(gpu, rows, dim):
     assert (op[:, 3 * dim:3 * dim + 2] == 1).all() and (op[:, 3 * dim + 2:] == 0).all()
 
 
+@pytest.mark.parametrize("n,dim", [(1, 128), (37, 128), (130, 128), (9, 768)])
+def test_layernorm_split3_t_is_the_operand_of_the_transposed_frame(gpu, n, dim):
+    """The ending-node fp32 projection operand: rows of x.transpose(0, 1) read in
+    place, bit for bit the operand of the transposed copy."""
+    g = torch.Generator().manual_seed(n + dim)
+    x = (torch.randn(n, n, dim, generator=g) * 2 - 1).to(gpu)
+    with torch.inference_mode():
+        got = ops.layernorm_split3_t(x, 1e-5)
+        want = ops.layernorm_split3(x.transpose(0, 1).contiguous().view(-1, dim), 1e-5)
+    assert got.shape == (n, n, 3 * dim + 64)
+    assert torch.equal(got.view(-1, 3 * dim + 64), want)
+
+
 @pytest.mark.parametrize("rows,cols", [(37, 1536), (5, 4), (3, 260)])
 def test_swiglu_split3_matches_gated_swiglu(gpu, rows, cols):
     g = torch.Generator().manual_seed(cols)
