@@ -9,7 +9,12 @@ gfx950 kernels, then the fp32 sequence stack.  Inputs (z [1,N,N,128],
 s [1,N,384], masks all ones) and random-init weights (seed 0, N(0, 0.08),
 norm weights N(1, 0.08)) are resident in HBM before timing.
 
+The default line also carries ``dropin``: the same layer (weights, inputs)
+timed through ``install()`` as a Boltz user runs it (guards, dropout draws,
+per-call allocation), with its ratio to the headline.
+
 Other workloads (--workload), each on one BASELINE config:
+  dropin           configs[3]: the installed PairformerLayer alone (its own line)
   trimul           configs[2]: TriangleMultiplication out and in, N=768, 5% of tokens masked
   triattn          configs[1]: TriangleAttention start and end, N=512, last 51 tokens masked
   trunk            configs[3]: the 64-block PairformerModule at N=1024
@@ -44,7 +49,7 @@ PEAK_HBM_GBS = 8000.0
 # (probe on the box), 256 CUs x 4 SIMDs at 2.4 GHz.
 EXP_PER_SIMD_CYCLE, SIMDS, CLOCK_HZ = 64 / 8, 1024, 2.4e9
 ROOT = os.path.dirname(os.path.abspath(__file__))
-WORKLOADS = ("pairformer", "trunk", "trimul", "triattn", "diffusion-step", "token-attention", "diffusion")
+WORKLOADS = ("pairformer", "dropin", "trunk", "trimul", "triattn", "diffusion-step", "token-attention", "diffusion")
 
 
 def parse():
@@ -326,6 +331,9 @@ def pairformer(args):
     with torch.inference_mode():
         ms, wall = timed_loop(lambda: layer(s, z, mask, pair_mask, z_out=z_out, workspace=ws), steps, args.warmup)
         kt, modules_ms = per_kernel_times(layer, s, z, mask, pair_mask, z_out, ws, args.kernel_reps)
+    del ws, z_out
+    dropin = dropin_layer_ms(layer, s, z, mask, pair_mask, steps, args.warmup)
+    dropin["vs_headline"] = round(dropin["ms"] / ms, 4)
     table = kernel_table(n)
     breakdown = {}
     for name, (avg_ms, launches) in kt.items():
@@ -354,7 +362,63 @@ def pairformer(args):
                {"workload": f"PairformerLayer forward, N={n}, c_z=128, c_s=384, tri-att 4x32, tri-mult 128, "
                             f"transition x4, single attention 16 heads (BASELINE configs[3], one of 64 blocks)",
                 "n_tokens": n, "batch": 1},
-               wall_s=round(wall, 3), roofline=roofline, modules=modules, breakdown=breakdown)
+               wall_s=round(wall, 3), roofline=roofline, modules=modules, breakdown=breakdown, dropin=dropin)
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_pairformer(n)
+    print(json.dumps(out), flush=True)
+
+
+def dropin_layer_ms(layer, s, z, mask, pair_mask, steps, warmup):
+    """The same layer as a Boltz user runs it: ``install`` on a model holding a
+    PairformerLayer (Boltz's class and module names), called as upstream's
+    PairformerModule calls it under bf16 autocast, with upstream's chunk size
+    (128 above 384 tokens).  The patched forward checks its guards, draws the
+    four dropout masks as upstream does, allocates its output z and workspace
+    from torch's caching allocator, and runs the fused composition."""
+    import copy
+
+    import torch
+    from boltz_lumi_amd import adapters
+
+    host = torch.nn.Module()
+    host.pairformer_module = torch.nn.Module()
+    host.pairformer_module.layers = torch.nn.ModuleList([copy.deepcopy(layer)])
+    patched = adapters.install(host, require_boltz2=False)
+    installed = host.pairformer_module.layers[0]
+    if "forward" not in vars(installed):
+        raise RuntimeError("install() did not patch the PairformerLayer")
+    chunk = 128 if z.shape[1] > 384 else 512
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        ms, wall = timed_loop(lambda: installed(s, z, mask, pair_mask, chunk), steps, warmup)
+    adapters.uninstall(host)
+    return {"ms": round(ms, 4), "wall_s": round(wall, 3), "patched_modules": patched,
+            "path": "install(model) -> pairformer.pairformer_layer_forward under bf16 autocast"}
+
+
+def dropin(args):
+    """``--workload dropin``: the installed PairformerLayer alone (the headline
+    layer's weights and inputs), one JSON line."""
+    import torch
+    from boltz_lumi_amd import layers
+
+    dev = torch.device("cuda:0")
+    n = args.n or 1024
+    steps = args.steps or 10
+    layer = init_weights(layers.PairformerLayer(), 0).to(dev).eval()
+    g = torch.Generator().manual_seed(0)
+    z = torch.randn(1, n, n, 128, generator=g).to(dev)
+    s = torch.randn(1, n, 384, generator=g).to(dev)
+    mask = torch.ones(1, n, device=dev)
+    pair_mask = torch.ones(1, n, n, device=dev)
+    d = dropin_layer_ms(layer, s, z, mask, pair_mask, steps, args.warmup)
+    layer_f = 2.831e12 * (n / 1024) ** 3
+    out = line("Pairformer layer ms @N=1024 bf16 (installed drop-in path)", d["ms"], "ms", args, steps, "bf16",
+               "synthetic (z, s ~ N(0,1); masks ones; random-init weights seed 0)",
+               {"workload": f"PairformerLayer forward through install() under bf16 autocast, N={n} (BASELINE "
+                            f"configs[3], one of 64 blocks)", "n_tokens": n, "batch": 1},
+               wall_s=d["wall_s"], path=d["path"], patched_modules=d["patched_modules"],
+               modules={"layer": {"ms": d["ms"], "t_star_ms": round(t_star_ms(layer_f, 0), 4),
+                                  "frac": round(t_star_ms(layer_f, 0) / d["ms"], 4)}})
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_pairformer(n)
     print(json.dumps(out), flush=True)
@@ -960,7 +1024,7 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding of the pair stack is a design note, not built)"}))
         sys.exit(2)
-    {"pairformer": pairformer, "trunk": trunk, "trimul": lambda a: isolated_module(a, "trimul"),
+    {"pairformer": pairformer, "dropin": dropin, "trunk": trunk, "trimul": lambda a: isolated_module(a, "trimul"),
      "triattn": lambda a: isolated_module(a, "triattn"), "diffusion-step": diffusion_step,
      "token-attention": token_attention, "diffusion": diffusion}[args.workload](args)
 

@@ -46,13 +46,13 @@ SIGNATURES = {
     "bmx_bias_softmax": (c_int, [_P, _P, _P, _P, c_int, _I64P, _I64P, _I64P, _I64P, _P]),
     "bmx_trimul_workspace_bytes": (c_size_t, [c_int64]),
     "bmx_trimul_fwd": (c_int, [_P, _P, c_int64, c_int, _P, _P, c_float, _P, _P, _P, c_float, _P, _P, _P, c_int, _P,
-                               c_size_t, c_int, _P]),
+                               _P, c_size_t, c_int, _P]),
     "bmx_trimul_fwd_noalloc": (c_int, [_P, _P, c_int64, c_int, _P, _P, c_float, _P, _P, _P, c_float, _P, _P, _P,
                                        c_int, _P]),
     "bmx_triattn_workspace_bytes": (c_size_t, [c_int64]),
     "bmx_triattn_proj_rows": (c_int, []),
     "bmx_triattn_fwd": (c_int, [_P, c_int, _P, c_int64, c_int, c_float, _P, _P, c_float, _P, _P, _P, _P, _P, _P, c_int,
-                                _P, c_size_t, c_int, _P]),
+                                _P, _P, c_size_t, c_int, _P]),
     "bmx_pack_mfma_weights": (c_int, [_P, c_int64, c_int64, _P, _P]),
     "bmx_pair_transition_fwd": (c_int, [_P, c_int, c_int64, _P, _P, c_float, _P, _P, _P, c_int, _P]),
     "bmx_pair_bias_fwd": (c_int, [_P, c_int, c_int64, _P, _P, c_float, _P, c_int, _P, _P]),

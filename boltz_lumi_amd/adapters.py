@@ -12,6 +12,12 @@ Patched (class name, path rule -> replacement):
       ._chunk (ending node)                        -> triangle.contiguous_mask_chunk
   TriangleMultiplication{Outgoing,Incoming}        -> multiplication.normalized_forward
   Transition named "*.transition_z"                -> pair_transition.transition_forward
+  PairformerLayer (trunk, confidence)              -> pairformer.pairformer_layer_forward (the
+      five pair kernels adding into the fp32 stream in place, the dropout masks
+      as row scales, the sequence stack fused with its pair bias written by the
+      pair transition; beyond the reference, which leaves the layer upstream)
+  PairformerNoSeqLayer (MSA, template)             -> pairformer.pairformer_noseq_forward
+      (the template stack's 64-channel layers fall back to the class forward)
   AdaLN / ConditionedTransitionBlock under
       "structure_module.score_model."              -> diffusion.adaln_forward / transition_forward
   AttentionPairBias under
@@ -68,6 +74,7 @@ def install(model, *, require_boltz2: bool = True, require_device: bool = True):
     from .multiplication import normalized_forward
     from .pair_bias import prepared_forward
     from .pair_transition import transition_forward as pair_transition_forward
+    from .pairformer import pairformer_layer_forward, pairformer_noseq_forward
     from .triangle import contiguous_mask_chunk, normalization_forward, triangle_attention_forward
 
     patched = 0
@@ -84,6 +91,12 @@ def install(model, *, require_boltz2: bool = True, require_device: bool = True):
             patched += 1
         elif cls == "Transition" and name.endswith(".transition_z"):
             module.forward = MethodType(pair_transition_forward, module)
+            patched += 1
+        elif cls == "PairformerLayer":
+            module.forward = MethodType(pairformer_layer_forward, module)
+            patched += 1
+        elif cls == "PairformerNoSeqLayer":
+            module.forward = MethodType(pairformer_noseq_forward, module)
             patched += 1
         elif name.startswith(SCORE_MODEL) and cls == "AdaLN":
             module.forward = MethodType(adaln_forward, module)

@@ -43,6 +43,6 @@ extern "C" {
 
 const char* bmx_last_error(void) { return g_last_error; }
 
-int bmx_abi_version(void) { return 1; }
+int bmx_abi_version(void) { return 2; }
 
 }  // extern "C"

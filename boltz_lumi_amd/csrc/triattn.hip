@@ -652,16 +652,21 @@ __global__ __launch_bounds__(kCoreThreads) __attribute__((amdgpu_waves_per_eu(4)
 // (ybuf), where the residual is added.  Tile k's rows are stored from ybuf in
 // iteration k+1, before the next prefetch: vmcnt counts stores in issue
 // order, so the wait for that prefetch does not wait for fresh stores.
+// kScaled: the module output of frame row i is multiplied by row_scale[i]
+// before it is written or added (PairformerLayer's row / column dropout mask:
+// frame row i is z's row i for the starting node and z's column i for the
+// ending node).
 constexpr int kP3 = 64;
 
-template <typename TIn>
+template <typename TIn, bool kScaled>
 __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const float* __restrict__ ln_w,
                                                              const float* __restrict__ ln_b, float eps,
                                                              const bf16* __restrict__ w_g,
                                                              const float* __restrict__ b_g,
                                                              const bf16* __restrict__ w_o,
                                                              const float* __restrict__ b_o, int starting, void* out,
-                                                             int out_mode, Layout L) {
+                                                             int out_mode, const float* __restrict__ row_scale,
+                                                             Layout L) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kP3 * kLdsRow];
   __shared__ __attribute__((aligned(16))) float ybuf[kP3 * kYRow];  // fp32 result rows
   bf16* xg = smem;                   // LN(x'), pairs x channels
@@ -685,8 +690,10 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
   constexpr int kRowsPer = kP3 / 8;
   f32x4 px[kRowsPer];
   bf16x4 po[kRowsPer];
+  float prs = 1.f;
   auto fetch = [&](int tile) {
     const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
+    if constexpr (kScaled) prs = row_scale[i];
 #pragma unroll
     for (int u = 0; u < kRowsPer; ++u) {
       const int j = min(j0 + hw + 8 * u, n - 1);
@@ -715,6 +722,7 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
   int tile = blockIdx.x, prev = -1;
   if (tile < total) fetch(tile);
   for (; tile < total; tile += gridDim.x) {
+    const float rs = prs;
     f32x4 xc[kRowsPer];
 #pragma unroll
     for (int u = 0; u < kRowsPer; ++u) {
@@ -748,7 +756,11 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) acc = mfma32(frag(xo, kLdsRow, nt * 32, ks), wo[ks], acc);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ybuf[(nt * 32 + drow(r, l)) * kYRow + ch] = rbf(acc[r] + bo);
+      for (int r = 0; r < 16; ++r) {
+        float y = rbf(acc[r] + bo);
+        if constexpr (kScaled) y *= rs;
+        ybuf[(nt * 32 + drow(r, l)) * kYRow + ch] = y;
+      }
     }
     __syncthreads();
     if (out_mode == kOutResidual || (out_mode == kOutAccumulate && x_in_regs)) {
@@ -790,7 +802,7 @@ Layout make_layout(void* ws, int n) {
 template <typename TIn>
 int run(const TIn* x, const float* mask, int n, int starting, float inf, const float* ln_w, const float* ln_b,
         float eps, const bf16* w_proj, const bf16* w_g, const float* b_g, const bf16* w_o, const float* b_o,
-        void* out, int out_mode, void* ws, int stages, hipStream_t st) {
+        void* out, int out_mode, const float* row_scale, void* ws, int stages, hipStream_t st) {
   Layout L = make_layout(ws, n);
   if (stages & 1) {
     const int total = L.np * (L.np / kP1);
@@ -805,8 +817,12 @@ int run(const TIn* x, const float* mask, int n, int starting, float inf, const f
   if (stages & 4) {
     const int total = n * ((n + kP3 - 1) / kP3);
     const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
-    triattn_out_kernel<TIn><<<dim3(grid), 256, 0, st>>>(x, ln_w, ln_b, eps, w_g, b_g, w_o, b_o, starting, out,
-                                                        out_mode, L);
+    if (row_scale)
+      triattn_out_kernel<TIn, true><<<dim3(grid), 256, 0, st>>>(x, ln_w, ln_b, eps, w_g, b_g, w_o, b_o, starting, out,
+                                                                out_mode, row_scale, L);
+    else
+      triattn_out_kernel<TIn, false><<<dim3(grid), 256, 0, st>>>(x, ln_w, ln_b, eps, w_g, b_g, w_o, b_o, starting,
+                                                                 out, out_mode, nullptr, L);
     if (int rc = check_launch("triattn_out")) return rc;
   }
   return BMX_OK;
@@ -825,8 +841,8 @@ size_t bmx_triattn_workspace_bytes(int64_t n) {
 
 int bmx_triattn_fwd(const void* x, int x_dtype, const float* mask, int64_t n, int starting, float inf,
                     const float* ln_w, const float* ln_b, float eps, const void* w_proj, const void* w_g,
-                    const float* b_g, const void* w_o, const float* b_o, void* out, int out_mode, void* workspace,
-                    size_t workspace_bytes, int stages, hipStream_t stream) {
+                    const float* b_g, const void* w_o, const float* b_o, void* out, int out_mode,
+                    const float* row_scale, void* workspace, size_t workspace_bytes, int stages, hipStream_t stream) {
   BMX_REQUIRE(n >= 0 && n <= 8192, "bmx_triattn_fwd: n must be in [0, 8192] (got %lld)", (long long)n);
   BMX_REQUIRE(x_dtype == kF32 || x_dtype == kBF16, "bmx_triattn_fwd: x dtype must be fp32 or bf16");
   BMX_REQUIRE(out_mode >= 0 && out_mode <= 3,
@@ -844,9 +860,10 @@ int bmx_triattn_fwd(const void* x, int x_dtype, const float* mask, int64_t n, in
               "bmx_triattn_fwd: x and weights must be 16-byte aligned, workspace 256-byte aligned");
   if (x_dtype == kF32)
     return run<float>((const float*)x, mask, (int)n, starting, inf, ln_w, ln_b, eps, (const bf16*)w_proj,
-                      (const bf16*)w_g, b_g, (const bf16*)w_o, b_o, out, out_mode, workspace, stages, stream);
+                      (const bf16*)w_g, b_g, (const bf16*)w_o, b_o, out, out_mode, row_scale, workspace, stages,
+                      stream);
   return run<bf16>((const bf16*)x, mask, (int)n, starting, inf, ln_w, ln_b, eps, (const bf16*)w_proj,
-                   (const bf16*)w_g, b_g, (const bf16*)w_o, b_o, out, out_mode, workspace, stages, stream);
+                   (const bf16*)w_g, b_g, (const bf16*)w_o, b_o, out, out_mode, row_scale, workspace, stages, stream);
 }
 
 int bmx_triattn_proj_rows(void) { return kProjRows; }

@@ -334,8 +334,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void trimul_contract_ke
 // where the residual is added.  Tile k's rows are stored from ybuf in
 // iteration k+1, before the next prefetch is issued: vmcnt counts stores in
 // issue order, so the wait for that prefetch does not wait for fresh stores.
+// kScaled: the module output of frame row i is multiplied by row_scale[i]
+// before it is written or added (PairformerLayer's row dropout mask).
 constexpr int kP3 = 64;
 
+template <bool kScaled>
 __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, const bf16* __restrict__ o_pl,
                                                             const float* __restrict__ in_w,
                                                             const float* __restrict__ in_b, float eps_in,
@@ -343,7 +346,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
                                                             const float* __restrict__ out_b, float eps_out,
                                                             const bf16* __restrict__ w_pout,
                                                             const bf16* __restrict__ w_gout, void* out, int out_mode,
-                                                            int n, int np) {
+                                                            const float* __restrict__ row_scale, int n, int np) {
   // xo: LN_out(O) and xg: LN_in(x), pairs x channels; ybuf: the tile's fp32 output rows.
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kP3 * kLdsRow];
   __shared__ __attribute__((aligned(16))) float ybuf[kP3 * kYRow];
@@ -376,8 +379,10 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
   }
   f32x4 px[kRowsPer];
   bf16x8 po[kOChunks];
+  float prs = 1.f;
   auto fetch = [&](int tile) {
     const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
+    if constexpr (kScaled) prs = row_scale[i];
 #pragma unroll
     for (int u = 0; u < kRowsPer; ++u) {
       const int j = j0 + hw + 8 * u;
@@ -415,6 +420,7 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
   if (tile < total) fetch(tile);
   for (; tile < total; tile += gridDim.x) {
     const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
+    const float rs = prs;
     f32x4 xc[kRowsPer];
 #pragma unroll
     for (int u = 0; u < kRowsPer; ++u) {
@@ -461,7 +467,10 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
         ag = mfma32(frag(xg, kLdsRow, nt * 32, ks), wg[ks], ag);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) res[nt][r] = rbf(ay[r] * sigmoid_f(ag[r]));  // the bf16 module output
+      for (int r = 0; r < 16; ++r) {
+        res[nt][r] = rbf(ay[r] * sigmoid_f(ag[r]));  // the bf16 module output
+        if constexpr (kScaled) res[nt][r] *= rs;
+      }
     }
 #pragma unroll
     for (int nt = 0; nt < kP3 / 32; ++nt)
@@ -485,8 +494,8 @@ inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 // The three kernels of one module on `workspace` (3 planes of 128 x np x np bf16).
 int launch(const float* x, const float* mask, int ni, int outgoing, const float* norm_in_w, const float* norm_in_b,
            float eps_in, const bf16* w_in, const float* norm_out_w, const float* norm_out_b, float eps_out,
-           const bf16* w_pout, const bf16* w_gout, void* out, int out_mode, void* workspace, int stages,
-           hipStream_t stream) {
+           const bf16* w_pout, const bf16* w_gout, void* out, int out_mode, const float* row_scale, void* workspace,
+           int stages, hipStream_t stream) {
   const int np = (int)round_up(ni, kPlaneTile);
   const int64_t plane = (int64_t)np * np * kC;
   bf16* a_pl = (bf16*)workspace;
@@ -515,8 +524,14 @@ int launch(const float* x, const float* mask, int ni, int outgoing, const float*
   if (stages & 4) {
     const int total = ni * ((ni + kP3 - 1) / kP3);
     const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
-    trimul_out_kernel<<<dim3(grid), 256, 0, stream>>>(x, o_pl, norm_in_w, norm_in_b, eps_in, norm_out_w, norm_out_b,
-                                                      eps_out, w_pout, w_gout, out, out_mode, ni, np);
+    if (row_scale)
+      trimul_out_kernel<true><<<dim3(grid), 256, 0, stream>>>(x, o_pl, norm_in_w, norm_in_b, eps_in, norm_out_w,
+                                                              norm_out_b, eps_out, w_pout, w_gout, out, out_mode,
+                                                              row_scale, ni, np);
+    else
+      trimul_out_kernel<false><<<dim3(grid), 256, 0, stream>>>(x, o_pl, norm_in_w, norm_in_b, eps_in, norm_out_w,
+                                                               norm_out_b, eps_out, w_pout, w_gout, out, out_mode,
+                                                               nullptr, ni, np);
     if (int rc = check_launch("trimul_out")) return rc;
   }
   return BMX_OK;
@@ -595,7 +610,8 @@ size_t bmx_trimul_workspace_bytes(int64_t n) {
 int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, const float* norm_in_w,
                    const float* norm_in_b, float eps_in, const void* w_in, const float* norm_out_w,
                    const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
-                   int out_mode, void* workspace, size_t workspace_bytes, int stages, hipStream_t stream) {
+                   int out_mode, const float* row_scale, void* workspace, size_t workspace_bytes, int stages,
+                   hipStream_t stream) {
   const char* fn = "bmx_trimul_fwd";
   BMX_REQUIRE(stages >= 1 && stages <= 7, "bmx_trimul_fwd: stages must be a non-empty subset of 1|2|4");
   if (int rc = check_args(fn, x, mask, n, 16384, norm_in_w, norm_in_b, eps_in, w_in, norm_out_w, norm_out_b, eps_out,
@@ -607,7 +623,8 @@ int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, c
               bmx_trimul_workspace_bytes(n));
   BMX_REQUIRE((uintptr_t)workspace % 16 == 0, "bmx_trimul_fwd: workspace must be 16-byte aligned");
   return launch(x, mask, (int)n, outgoing, norm_in_w, norm_in_b, eps_in, (const bf16*)w_in, norm_out_w, norm_out_b,
-                eps_out, (const bf16*)w_pout, (const bf16*)w_gout, out, out_mode, workspace, stages, stream);
+                eps_out, (const bf16*)w_pout, (const bf16*)w_gout, out, out_mode, row_scale, workspace, stages,
+                stream);
 }
 
 int bmx_trimul_fwd_noalloc(const float* x, const float* mask, int64_t n, int outgoing, const float* norm_in_w,
@@ -626,7 +643,7 @@ int bmx_trimul_fwd_noalloc(const float* x, const float* mask, int64_t n, int out
   // zeros) and the contraction every element of O, so nothing left in the
   // scratch by an earlier call is read: no clearing is needed.
   return launch(x, mask, (int)n, outgoing, norm_in_w, norm_in_b, eps_in, (const bf16*)w_in, norm_out_w, norm_out_b,
-                eps_out, (const bf16*)w_pout, (const bf16*)w_gout, out, out_mode, ws, 7, stream);
+                eps_out, (const bf16*)w_pout, (const bf16*)w_gout, out, out_mode, nullptr, ws, 7, stream);
 }
 
 }  // extern "C"

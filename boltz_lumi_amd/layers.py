@@ -20,7 +20,7 @@ import torch
 from torch import nn
 import torch.nn.functional as F
 
-from . import ops
+from . import ops, pairformer
 from .pair_bias import fused_attention
 
 
@@ -147,16 +147,9 @@ class Transition(nn.Module):
         """``x + self(x)`` for the unfused sizes: fc1 | fc2 as one GEMM and the
         residual add in the fc3 GEMM's epilogue (fp32 x; written into x when
         ``inplace`` and x is contiguous)."""
-        if self.fused or x.dtype != torch.float32 or self.fc3.weight.dtype != x.dtype or torch.is_grad_enabled():
+        if self.fused:
             return x + self(x)
-        w12 = ops.cached_weight(self, "w12", (self.fc1.weight, self.fc2.weight), lambda a, b: torch.cat([a, b], 0))
-        h = F.linear(self.norm(x), w12)
-        h = F.silu(h[..., :self.hidden]).mul_(h[..., self.hidden:])
-        x2 = x.reshape(-1, x.shape[-1])
-        if inplace and x.is_contiguous():
-            x2.addmm_(h.reshape(-1, self.hidden), self.fc3.weight.t())
-            return x
-        return torch.addmm(x2, h.reshape(-1, self.hidden), self.fc3.weight.t()).view(x.shape)
+        return pairformer.transition_residual(self, x, inplace)
 
 
 class _HeadsFirst(nn.Module):
@@ -180,7 +173,7 @@ class AttentionPairBias(nn.Module):
         self.proj_g = nn.Linear(c_s, c_s, bias=False)
         self.compute_pair_bias = compute_pair_bias
         if compute_pair_bias:
-            self.proj_z = nn.Sequential(nn.LayerNorm(c_z), nn.Linear(c_z, num_heads, bias=False))
+            self.proj_z = nn.Sequential(nn.LayerNorm(c_z), nn.Linear(c_z, num_heads, bias=False), _HeadsFirst())
         else:
             self.proj_z = _HeadsFirst()
         self.proj_o = nn.Linear(c_s, c_s, bias=False)
@@ -196,7 +189,7 @@ class AttentionPairBias(nn.Module):
             for b in range(z.shape[0]):
                 ops.pair_bias(norm, lin, z[b].contiguous(), out=out[b])
             return out
-        return self.proj_z(z).movedim(-1, 1)
+        return self.proj_z(z)
 
     def fused_bias_ok(self, z):
         """Whether ``pair_bias(z)`` is the fused 128 -> 16 kernel's (so a
@@ -235,11 +228,12 @@ class AttentionPairBias(nn.Module):
 class PairformerLayer(nn.Module):
     """Boltz-2 ``PairformerLayer`` (v2, eval) with the fused pair stack."""
 
-    def __init__(self, token_s=384, token_z=128, num_heads=16, pairwise_head_width=32, pairwise_num_heads=4,
-                 post_layer_norm=False):
+    def __init__(self, token_s=384, token_z=128, num_heads=16, dropout=0.25, pairwise_head_width=32,
+                 pairwise_num_heads=4, post_layer_norm=False):
         super().__init__()
         self.token_z = token_z
         self.num_heads = num_heads
+        self.dropout = dropout  # upstream's rate; this module's own forward runs eval only (no masks)
         self.pre_norm_s = nn.LayerNorm(token_s)
         self.attention = AttentionPairBias(token_s, token_z, num_heads)
         self.tri_mul_out = TriangleMultiplicationOutgoing(token_z)
@@ -252,43 +246,21 @@ class PairformerLayer(nn.Module):
 
     def pair_stack(self, z, pair_mask, z_out=None, workspace=None, bias_out=None):
         """z_out = z + tri_mul_out + tri_mul_in + tri_att_start + tri_att_end + transition_z,
-        each added in order into the fp32 stream (eval dropout is identity).
-        z is read once and never written; z_out may be preallocated.  With
-        ``bias_out`` [B, 16, N, N] the transition's epilogue also writes the
-        sequence stack's pair bias of z_out (``attention.pair_bias(z_out)``)."""
+        each added in order into the fp32 stream (``pairformer.pair_stack``; no
+        dropout masks).  z is read once and never written; z_out may be
+        preallocated.  With ``bias_out`` [B, 16, N, N] the transition's
+        epilogue also writes the sequence stack's pair bias of z_out
+        (``attention.pair_bias(z_out)``)."""
         _require_cuda(z, "PairformerLayer")
-        if z.dtype != torch.float32:
-            raise RuntimeError("the pair stream is fp32")
-        z = z.contiguous()
-        z_out = torch.empty_like(z) if z_out is None else z_out
-        n = z.shape[1]
-        ws = ops.new_workspace(n, z.device) if workspace is None else workspace
-        for b in range(z.shape[0]):
-            zi, zo = z[b], z_out[b]
-            mb = pair_mask[b].float().contiguous()
-            ops.trimul(self.tri_mul_out, zi, mb, True, ops.OUT_RESIDUAL, zo, ws)
-            ops.trimul(self.tri_mul_in, zo, mb, False, ops.OUT_ACCUMULATE, zo, ws)
-            ops.triattn(self.tri_att_start, zo, mb, True, ops.OUT_ACCUMULATE, zo, ws)
-            ops.triattn(self.tri_att_end, zo, mb, False, ops.OUT_ACCUMULATE, zo, ws)
-            pb = None if bias_out is None else (self.attention.proj_z[0], self.attention.proj_z[1], bias_out[b])
-            ops.pair_transition(self.transition_z, zo, ops.OUT_ACCUMULATE, zo, pair_bias=pb)
-        return z_out
+        mods = None if bias_out is None else (self.attention.proj_z[0], self.attention.proj_z[1])
+        return pairformer.pair_stack(self, z, pair_mask, z_out, workspace, bias_out, mods)
 
     def sequence_stack(self, s, z, mask, pair_bias=None):
         """s + attention, then + transition_s (upstream order, fp32); on the
-        fused path each residual add rides in the epilogue of its output GEMM.
-        ``pair_bias``: ``attention.pair_bias(z)`` if already computed."""
-        with torch.autocast("cuda", enabled=False):
-            s = s.float()
-            s_normed = self.pre_norm_s(s)
-            o = self.attention.attend(s_normed, z, mask.float(), s_normed, bias=pair_bias)
-            if o is None:
-                s = s + self.attention(s=s_normed, z=z, mask=mask.float(), k_in=s_normed)
-            else:
-                s = torch.addmm(s.reshape(-1, s.shape[-1]), o.reshape(-1, o.shape[-1]),
-                                self.attention.proj_o.weight.float().t()).view(s.shape)
-            s = self.transition_s.residual(s, inplace=o is not None)
-            return self.s_post_norm(s)
+        fused path each residual add rides in the epilogue of its output GEMM
+        (``pairformer.sequence_stack``).  ``pair_bias``:
+        ``attention.pair_bias(z)`` if already computed."""
+        return pairformer.sequence_stack(self, s, z, mask, pair_bias)
 
     def forward(self, s, z, mask, pair_mask, chunk_size_tri_attn=None, use_kernels=False, z_out=None,
                 workspace=None):
@@ -308,7 +280,8 @@ class PairformerModule(nn.Module):
         super().__init__()
         self.token_z = token_z
         self.layers = nn.ModuleList([
-            PairformerLayer(token_s, token_z, num_heads, pairwise_head_width, pairwise_num_heads, post_layer_norm)
+            PairformerLayer(token_s, token_z, num_heads, 0.25, pairwise_head_width, pairwise_num_heads,
+                            post_layer_norm)
             for _ in range(num_blocks)])
 
     def forward(self, s, z, mask, pair_mask, use_kernels=False):

@@ -56,18 +56,20 @@ def _inference_only() -> None:
     _check(not torch.is_grad_enabled(), "Inference only")
 
 
-def _version(p):
-    return -1 if p.is_inference() else p._version
-
-
 def cached_weight(module, name: str, sources, build):
     """Derived weight (e.g. a bf16 concatenation) cached on ``module``.
 
-    Reused only while every source parameter keeps its identity, version,
-    device and dtype (the rule of the reference's joint projection cache,
-    multiplication.py:29-40).  Inference tensors carry no version counter;
-    for them only identity, device and dtype are checked."""
-    key = tuple((id(p), _version(p), p.device, p.dtype) for p in sources)
+    Reused only while every source parameter keeps its identity, version
+    counter, storage, device and dtype (the rule of the reference's joint
+    projection cache, multiplication.py:29-40, plus the storage address, which
+    a ``param.data = ...`` swap changes).  Inference tensors (parameters made
+    or loaded under ``torch.inference_mode``) carry no version counter, so an
+    in-place update of one cannot be seen: with such a source the weight is
+    rebuilt on every call and never cached."""
+    if any(p.is_inference() for p in sources):
+        with torch.no_grad():
+            return build(*sources).contiguous()
+    key = tuple((id(p), p._version, p.data_ptr(), p.device, p.dtype) for p in sources)
     cache = module.__dict__.setdefault("_bmx_weight_cache", {})
     hit = cache.get(name)
     if hit is None or hit[0] != key:
@@ -528,11 +530,24 @@ def _out_tensor(x, out, out_mode):
     return out
 
 
-def trimul(module, x, mask, outgoing, out_mode=OUT_BF16, out=None, workspace=None, stages=ALL_STAGES):
+def _row_scale(row_scale, x, n):
+    """Checked fp32 [n] row scale (or None) for the fused modules' output kernels."""
+    if row_scale is None:
+        return None
+    _cuda(x, row_scale)
+    _check(row_scale.dtype == torch.float32 and row_scale.numel() == n and row_scale.is_contiguous(),
+           "expected a contiguous fp32 row scale of n values")
+    return row_scale
+
+
+def trimul(module, x, mask, outgoing, out_mode=OUT_BF16, out=None, workspace=None, stages=ALL_STAGES,
+           row_scale=None):
     """Fused TriangleMultiplication{Outgoing,Incoming} for x [N, N, 128] fp32.
 
     ``stages`` selects the kernels (1 projection, 2 contraction, 4 output);
-    separate calls must share ``workspace``."""
+    separate calls must share ``workspace``.  ``row_scale`` (fp32 [N] or None)
+    multiplies output row i (before the residual add): PairformerLayer's
+    row-wise dropout mask."""
     _cuda(x, mask)
     _check(x.dim() == 3 and x.size(0) == x.size(1) and x.size(2) == C, "expected x of shape [N, N, 128]")
     _check(x.dtype == torch.float32 and x.is_contiguous(), "expected contiguous fp32 x")
@@ -546,13 +561,14 @@ def trimul(module, x, mask, outgoing, out_mode=OUT_BF16, out=None, workspace=Non
     niw, nib = cached_weight(module, "ni_w", (ni.weight,), _f32), cached_weight(module, "ni_b", (ni.bias,), _f32)
     now, nob = cached_weight(module, "no_w", (no.weight,), _f32), cached_weight(module, "no_b", (no.bias,), _f32)
     out = _out_tensor(x, out, out_mode)
+    rs = _row_scale(row_scale, x, n)
     nbytes = N.lib().bmx_trimul_workspace_bytes(n)
     ws = workspace if workspace is not None and workspace.numel() >= nbytes else _workspace(nbytes, x.device)
     if n:
         N.call("bmx_trimul_fwd", x.data_ptr(), mask.data_ptr(), n, int(bool(outgoing)), niw.data_ptr(),
                nib.data_ptr(), float(ni.eps), w_in.data_ptr(), now.data_ptr(), nob.data_ptr(), float(no.eps),
-               w_pout.data_ptr(), w_gout.data_ptr(), out.data_ptr(), out_mode, ws.data_ptr(), ws.numel(), stages,
-               _stream(x))
+               w_pout.data_ptr(), w_gout.data_ptr(), out.data_ptr(), out_mode, None if rs is None else rs.data_ptr(),
+               ws.data_ptr(), ws.numel(), stages, _stream(x))
     return out
 
 
@@ -574,12 +590,16 @@ def _triattn_proj_weight(wq, wk, wv, wb):
     return w
 
 
-def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=None, stages=ALL_STAGES):
+def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=None, stages=ALL_STAGES,
+            row_scale=None):
     """Fused TriangleAttention (starting or ending node) for x [N, N, 128].
 
     ``module`` carries Boltz's TriangleAttention parameters: ``layer_norm``,
     ``linear`` (triangle bias), ``mha.linear_{q,k,v,g,o}``, ``inf``.
-    ``stages`` selects the kernels (1 projection, 2 attention core, 4 output)."""
+    ``stages`` selects the kernels (1 projection, 2 attention core, 4 output).
+    ``row_scale`` (fp32 [N] or None) multiplies the output of x's row i
+    (starting) or column i (ending) before the residual add:
+    PairformerLayer's dropout mask (row-wise / column-wise)."""
     _cuda(x)
     _check(x.dim() == 3 and x.size(0) == x.size(1) and x.size(2) == C, "expected x of shape [N, N, 128]")
     _check(x.dtype in (torch.float32, torch.bfloat16) and x.is_contiguous(), "expected contiguous fp32/bf16 x")
@@ -598,13 +618,14 @@ def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=No
     ln = module.layer_norm
     lnw, lnb = cached_weight(module, "ln_w", (ln.weight,), _f32), cached_weight(module, "ln_b", (ln.bias,), _f32)
     out = _out_tensor(x, out, out_mode)
+    rs = _row_scale(row_scale, x, n)
     nbytes = N.lib().bmx_triattn_workspace_bytes(n)
     ws = workspace if workspace is not None and workspace.numel() >= nbytes else _workspace(nbytes, x.device)
     if n:
         N.call("bmx_triattn_fwd", x.data_ptr(), _code(x.dtype), None if mask is None else mask.data_ptr(), n,
                int(bool(starting)), float(module.inf), lnw.data_ptr(), lnb.data_ptr(), float(ln.eps),
                w_proj.data_ptr(), w_g.data_ptr(), b_g.data_ptr(), w_o.data_ptr(), b_o.data_ptr(), out.data_ptr(),
-               out_mode, ws.data_ptr(), ws.numel(), stages, _stream(x))
+               out_mode, None if rs is None else rs.data_ptr(), ws.data_ptr(), ws.numel(), stages, _stream(x))
     return out
 
 

@@ -148,6 +148,12 @@ int bmx_bias_softmax(const void* scores, const void* bias, const float* mask, vo
 /* out_mode for the fused modules: 0 = write bf16 [n,n,128], 1 = write fp32,
  * 2 = add into fp32 `out` (residual stream; out may alias x),
  * 3 = write fp32 out = x + y (out-of-place residual; out must not alias x).
+ * row_scale (trimul / triattn): NULL, or fp32 [n]: the module output of frame row r is
+ * multiplied by row_scale[r] before it is written or added.  The frame row is z's row for the
+ * multiplications and the starting node, z's column for the ending node: PairformerLayer's
+ * eval-mode dropout masks (upstream get_dropout_mask draws them even in eval, row-wise for
+ * tri_mul_out / tri_mul_in / tri_att_start and column-wise for tri_att_end; the reference keeps
+ * that composition, src/boltz_lumi/adapters.py:24-46 patches only the modules inside it).
  * stages (trimul / triattn): bitmask of the kernels to launch, 1 = projection,
  * 2 = contraction / attention core, 4 = output; 7 runs the whole module.  The
  * workspace carries the intermediates between separately launched stages. */
@@ -161,7 +167,8 @@ size_t bmx_trimul_workspace_bytes(int64_t n);
 int bmx_trimul_fwd(const float* x, const float* mask, int64_t n, int outgoing, const float* norm_in_w,
                    const float* norm_in_b, float eps_in, const void* w_in, const float* norm_out_w,
                    const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
-                   int out_mode, void* workspace, size_t workspace_bytes, int stages, bmx_stream_t stream);
+                   int out_mode, const float* row_scale, void* workspace, size_t workspace_bytes, int stages,
+                   bmx_stream_t stream);
 
 /* bmx_trimul_fwd (all three stages) with no workspace argument and no allocation: the operand
  * planes live in a static device array of the library (48 MiB = 3 planes of 128 x 256 x 256 bf16,
@@ -190,8 +197,8 @@ int bmx_triattn_proj_rows(void);
  * mha.forward (src/boltz_lumi/triangle.py:18-22,32-104,107-146). */
 int bmx_triattn_fwd(const void* x, int x_dtype, const float* mask, int64_t n, int starting, float inf,
                     const float* ln_w, const float* ln_b, float eps, const void* w_proj, const void* w_g,
-                    const float* b_g, const void* w_o, const float* b_o, void* out, int out_mode, void* workspace,
-                    size_t workspace_bytes, int stages, bmx_stream_t stream);
+                    const float* b_g, const void* w_o, const float* b_o, void* out, int out_mode,
+                    const float* row_scale, void* workspace, size_t workspace_bytes, int stages, bmx_stream_t stream);
 
 /* Pack a row-major bf16 matrix W[rows][cols] (rows % 32 == 0, cols % 16 == 0) into MFMA
  * A-operand order: element (r, c) goes to ((r/32 * cols/16 + c/16) * 64 + lane) * 8 + c%8

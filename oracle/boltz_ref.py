@@ -383,11 +383,39 @@ class AttentionPairBias(nn.Module):
 # --------------------------------------------------------------------------
 
 
+def get_dropout_mask(dropout: float, z: torch.Tensor, training: bool, columnwise: bool = False) -> torch.Tensor:
+    """Upstream ``layers.dropout.get_dropout_mask``: one uniform draw per row
+    ([B, N, 1, 1]) or per column ([B, 1, N, 1]) of z, kept where it exceeds
+    ``dropout * training`` and scaled by ``1 / (1 - dropout * training)``.  The
+    draw happens in eval too (rate 0): the mask is then 1 except where a draw
+    is exactly 0, and the generator advances."""
+    dropout = dropout * training
+    v = z[:, 0:1, :, 0:1] if columnwise else z[:, :, 0:1, 0:1]
+    d = torch.rand_like(v) > dropout
+    return d * 1.0 / (1.0 - dropout)
+
+
+def _pair_stack(layer, z, pair_mask, chunk_size_tri_attn=None):
+    """The pair stack of upstream ``PairformerLayer`` / ``PairformerNoSeqLayer``:
+    each of the four triangle updates added through its dropout mask (the
+    ending node's column-wise), then the transition."""
+    d = get_dropout_mask(layer.dropout, z, layer.training)
+    z = z + d * layer.tri_mul_out(z, mask=pair_mask)
+    d = get_dropout_mask(layer.dropout, z, layer.training)
+    z = z + d * layer.tri_mul_in(z, mask=pair_mask)
+    d = get_dropout_mask(layer.dropout, z, layer.training)
+    z = z + d * layer.tri_att_start(z, mask=pair_mask, chunk_size=chunk_size_tri_attn)
+    d = get_dropout_mask(layer.dropout, z, layer.training, columnwise=True)
+    z = z + d * layer.tri_att_end(z, mask=pair_mask, chunk_size=chunk_size_tri_attn)
+    return z + layer.transition_z(z)
+
+
 class PairformerLayer(nn.Module):
     """Upstream ``layers.pairformer.PairformerLayer`` (v2, eval mode).
 
-    Pair stack: ``z += tri_mul_out``, ``tri_mul_in``, ``tri_att_start``,
-    ``tri_att_end``, ``transition_z`` (the eval dropout mask is ones).  Then
+    Pair stack: ``z += d * tri_mul_out``, ``tri_mul_in``, ``tri_att_start``,
+    ``tri_att_end`` (``d`` the ``get_dropout_mask`` draw of each: ones in eval
+    except where a draw is exactly 0), then ``z += transition_z``.  Then
     the fp32 sequence stack with autocast disabled: ``s += attention(
     pre_norm_s(s), z)``, ``s += transition_s(s)``, ``s_post_norm`` (Identity in
     the trunk).  Pinned by branch isolation (every branch but one zeroed gives
@@ -398,11 +426,12 @@ class PairformerLayer(nn.Module):
     ``triangle.py:113``) and an unpatched s-stack (``adapters.py:39-45``).
     """
 
-    def __init__(self, token_s=384, token_z=128, num_heads=16, pairwise_head_width=32,
+    def __init__(self, token_s=384, token_z=128, num_heads=16, dropout=0.25, pairwise_head_width=32,
                  pairwise_num_heads=4, post_layer_norm=False):
         super().__init__()
         self.token_z = token_z
         self.num_heads = num_heads
+        self.dropout = dropout
         self.pre_norm_s = nn.LayerNorm(token_s)
         self.attention = AttentionPairBias(token_s, token_z, num_heads)
         self.tri_mul_out = TriangleMultiplicationOutgoing(token_z)
@@ -413,12 +442,9 @@ class PairformerLayer(nn.Module):
         self.transition_z = Transition(token_z, token_z * 4)
         self.s_post_norm = nn.LayerNorm(token_s) if post_layer_norm else nn.Identity()
 
-    def forward(self, s, z, mask, pair_mask, chunk_size_tri_attn=None, use_kernels=False):
-        z = z + self.tri_mul_out(z, mask=pair_mask)
-        z = z + self.tri_mul_in(z, mask=pair_mask)
-        z = z + self.tri_att_start(z, mask=pair_mask, chunk_size=chunk_size_tri_attn)
-        z = z + self.tri_att_end(z, mask=pair_mask, chunk_size=chunk_size_tri_attn)
-        z = z + self.transition_z(z)
+    def forward(self, s, z, mask, pair_mask, chunk_size_tri_attn=None, use_kernels=False, use_cuequiv_mul=False,
+                use_cuequiv_attn=False):
+        z = _pair_stack(self, z, pair_mask, chunk_size_tri_attn)
         # Upstream runs the sequence stack in fp32 with autocast disabled, on
         # the updated z (the reference leaves it unpatched, adapters.py:39-45).
         f = _at_least_f32
@@ -440,21 +466,19 @@ class PairformerNoSeqLayer(nn.Module):
     against the pair stack of ``PairformerLayer`` (pinned there).
     """
 
-    def __init__(self, token_z=128, pairwise_head_width=32, pairwise_num_heads=4):
+    def __init__(self, token_z=128, dropout=0.25, pairwise_head_width=32, pairwise_num_heads=4):
         super().__init__()
         self.token_z = token_z
+        self.dropout = dropout
         self.tri_mul_out = TriangleMultiplicationOutgoing(token_z)
         self.tri_mul_in = TriangleMultiplicationIncoming(token_z)
         self.tri_att_start = TriangleAttention(token_z, pairwise_head_width, pairwise_num_heads, inf=1e9)
         self.tri_att_end = TriangleAttentionEndingNode(token_z, pairwise_head_width, pairwise_num_heads, inf=1e9)
         self.transition_z = Transition(token_z, token_z * 4)
 
-    def forward(self, z, pair_mask, chunk_size_tri_attn=None, use_kernels=False):
-        z = z + self.tri_mul_out(z, mask=pair_mask)
-        z = z + self.tri_mul_in(z, mask=pair_mask)
-        z = z + self.tri_att_start(z, mask=pair_mask, chunk_size=chunk_size_tri_attn)
-        z = z + self.tri_att_end(z, mask=pair_mask, chunk_size=chunk_size_tri_attn)
-        return z + self.transition_z(z)
+    def forward(self, z, pair_mask, chunk_size_tri_attn=None, use_kernels=False, use_cuequiv_mul=False,
+                use_cuequiv_attn=False):
+        return _pair_stack(self, z, pair_mask, chunk_size_tri_attn)
 
 
 # --------------------------------------------------------------------------

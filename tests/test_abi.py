@@ -32,7 +32,7 @@ def lib():
 def test_library_exports_every_declared_symbol(lib):
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.bmx_abi_version() == 1
+    assert lib.bmx_abi_version() == 2
 
 
 def test_workspace_queries(lib):
@@ -52,20 +52,20 @@ def test_argument_validation_needs_no_gpu(lib):
     # Rejected before any launch: bad dtype code, bad out_mode, empty input.
     rc = lib.bmx_layernorm128(None, 7, 0, None, None, 1e-5, None, 0, 4, None)
     assert rc == N.BMX_EINVAL and b"dtypes" in lib.bmx_last_error()
-    rc = lib.bmx_trimul_fwd(None, None, 4, 1, None, None, 1e-5, None, None, None, 1e-5, None, None, None, 9, None, 0,
-                            7, None)
+    rc = lib.bmx_trimul_fwd(None, None, 4, 1, None, None, 1e-5, None, None, None, 1e-5, None, None, None, 9, None, None,
+                            0, 7, None)
     assert rc == N.BMX_EINVAL and b"out_mode" in lib.bmx_last_error()
-    rc = lib.bmx_trimul_fwd(None, None, 4, 1, None, None, 1e-5, None, None, None, 1e-5, None, None, None, 0, None, 0,
-                            7, None)
+    rc = lib.bmx_trimul_fwd(None, None, 4, 1, None, None, 1e-5, None, None, None, 1e-5, None, None, None, 0, None, None,
+                            0, 7, None)
     assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
-    rc = lib.bmx_trimul_fwd(None, None, 4, 1, None, None, 1e-5, None, None, None, 1e-5, None, None, None, 0, None, 0,
-                            8, None)
+    rc = lib.bmx_trimul_fwd(None, None, 4, 1, None, None, 1e-5, None, None, None, 1e-5, None, None, None, 0, None, None,
+                            0, 8, None)
     assert rc == N.BMX_EINVAL and b"stages" in lib.bmx_last_error()
     assert lib.bmx_gate(None, None, None, 0, None) == N.BMX_OK
     rc = lib.bmx_diffusion_epilogue(2, None, None, None, None, 0, 1, 4, None)
     assert rc == N.BMX_EINVAL and b"kind" in lib.bmx_last_error()
     rc = lib.bmx_triattn_fwd(None, 0, None, 8, 1, 1e9, None, None, 1e-5, None, None, None, None, None, None, 0,
-                             None, 0, 7, None)
+                             None, None, 0, 7, None)
     assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
     rc = lib.bmx_pair_transition_fwd(None, 1, 8, None, None, 1e-5, None, None, None, 2, None)
     assert rc == N.BMX_EINVAL and b"residual" in lib.bmx_last_error()

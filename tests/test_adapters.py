@@ -56,11 +56,12 @@ def test_install_requires_boltz2_and_gfx950():
 def test_install_patches_by_class_and_path_and_is_idempotent():
     model = Boltz2()
     n = adapters.install(model, require_device=False)
-    # tri_mul_out, tri_mul_in, tri_att_start, tri_att_end, transition_z; score model: block (CTB) and its
-    # AdaLN, the token-transformer layer itself, its AdaLN, AttentionPairBias, CTB and its AdaLN;
-    # structure_module.sample
-    assert n == 13
+    # the Pairformer layer and its tri_mul_out, tri_mul_in, tri_att_start, tri_att_end, transition_z; score
+    # model: block (CTB) and its AdaLN, the token-transformer layer itself, its AdaLN, AttentionPairBias, CTB
+    # and its AdaLN; structure_module.sample
+    assert n == 14
     layer = model.pairformer_module.layers[0]
+    assert "forward" in vars(layer)  # the fused composition (pairformer.pairformer_layer_forward)
     assert "forward" in vars(layer.tri_att_start) and "forward" in vars(layer.tri_att_start.layer_norm)
     assert "forward" in vars(layer.transition_z) and "forward" not in vars(layer.transition_s)
     assert "forward" not in vars(layer.attention)  # the trunk's AttentionPairBias stays upstream
@@ -68,8 +69,9 @@ def test_install_patches_by_class_and_path_and_is_idempotent():
     assert "forward" in vars(token_layer.pair_bias_attn) and "sample" in vars(model.structure_module)
     assert "forward" in vars(token_layer)
     assert adapters.install(model, require_device=False) == 0
-    assert adapters.uninstall(model) >= 13
+    assert adapters.uninstall(model) >= 14
     assert "forward" not in vars(layer.tri_att_start) and "sample" not in vars(model.structure_module)
+    assert "forward" not in vars(layer)
 
 
 def test_prepare_token_bias_keeps_values_and_packs_each_layer_densely():
@@ -111,12 +113,16 @@ def test_cpu_tensors_fall_back_to_upstream_exactly():
     mask = torch.ones(1, n)
     mask[:, -1] = 0
     pm = mask[:, :, None] * mask[:, None, :]
-    with torch.no_grad():
-        want = layer(s, z, mask, pm)
-    adapters.install(model, require_device=False)
-    with torch.no_grad():
-        got = layer(s, z, mask, pm)
-    assert all(torch.equal(a, b) for a, b in zip(got, want))
+    for training in (False, True):  # in training the dropout masks are live: same seed, same draws
+        model.train(training)
+        adapters.uninstall(model)
+        with torch.no_grad():
+            torch.manual_seed(7)
+            want = layer(s, z, mask, pm)
+            adapters.install(model, require_device=False)
+            torch.manual_seed(7)
+            got = layer(s, z, mask, pm)
+        assert all(torch.equal(a, b) for a, b in zip(got, want))
 
 
 def test_grad_mode_falls_back_with_equal_gradients():
@@ -201,7 +207,9 @@ def test_msa_template_and_confidence_stacks_are_patched_by_class_and_suffix():
     template = model.template_module.pairformer.layers[0]
     with torch.inference_mode():
         want = template(z, pm)
-    assert adapters.install(model, require_boltz2=False, require_device=False) == 15
+    # 15 pair modules and the three layers (MSA and template PairformerNoSeqLayer, confidence PairformerLayer)
+    assert adapters.install(model, require_boltz2=False, require_device=False) == 18
+    assert "forward" in vars(msa_layer.pairformer_layer) and "forward" in vars(template)
     assert "forward" in vars(msa_layer.pairformer_layer.transition_z)
     assert "forward" not in vars(msa_layer.msa_transition)
     with torch.inference_mode():

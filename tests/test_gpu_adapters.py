@@ -46,7 +46,7 @@ def model(gpu):
 
 
 def test_install_on_gfx950(model):
-    assert adapters.install(model) == 8  # 5 pair modules, AdaLN, CTB and the AdaLN inside it
+    assert adapters.install(model) == 9  # the Pairformer layer, its 5 pair modules, AdaLN, CTB and its AdaLN
 
 
 @pytest.mark.parametrize("n", [64, 117])
@@ -65,7 +65,7 @@ def test_patched_pair_modules_match_upstream(model, gpu, n):
     }
     with torch.inference_mode():
         want = {k: f(getattr(layer, k)) for k, f in calls.items()}  # upstream fp32
-    assert adapters.install(model) == 8  # 5 pair modules, AdaLN, CTB and the AdaLN inside it
+    assert adapters.install(model) == 9  # the Pairformer layer, its 5 pair modules, AdaLN, CTB and its AdaLN
     with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
         for k, f in calls.items():
             got = f(getattr(layer, k))

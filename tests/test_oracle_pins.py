@@ -373,7 +373,7 @@ def test_pairformer_layer_runs_and_is_residual():
     final projections leave z and s unchanged (the layer is residual)."""
     g = _gen(18)
     layer = R.randomize(R.PairformerLayer(token_s=32, token_z=16, num_heads=4, pairwise_head_width=8,
-                                          pairwise_num_heads=2), generator=g)
+                                          pairwise_num_heads=2), generator=g).eval()
     with torch.no_grad():
         for mod in (layer.tri_mul_out.p_out, layer.tri_mul_in.p_out, layer.tri_att_start.mha.linear_o,
                     layer.tri_att_end.mha.linear_o, layer.transition_z.fc3, layer.attention.proj_o,
@@ -395,8 +395,8 @@ def test_pairformer_no_seq_layer_is_the_trunk_pair_stack(token_z):
     trunk's width and at a template-like narrower one."""
     g = _gen(19)
     layer = R.randomize(R.PairformerLayer(token_s=32, token_z=token_z, num_heads=4, pairwise_head_width=8,
-                                          pairwise_num_heads=2), generator=g)
-    noseq = R.PairformerNoSeqLayer(token_z, pairwise_head_width=8, pairwise_num_heads=2)
+                                          pairwise_num_heads=2), generator=g).eval()
+    noseq = R.PairformerNoSeqLayer(token_z, pairwise_head_width=8, pairwise_num_heads=2).eval()
     own = noseq.state_dict()
     noseq.load_state_dict({k: v for k, v in layer.state_dict().items() if k in own})
     with torch.no_grad():
@@ -424,7 +424,7 @@ _BRANCHES = ("tri_mul_out", "tri_mul_in", "tri_att_start", "tri_att_end", "trans
 
 
 def _small_layer(seed):
-    return R.randomize(R.PairformerLayer(**_SMALL), generator=_gen(seed)).double()
+    return R.randomize(R.PairformerLayer(**_SMALL), generator=_gen(seed)).double().eval()
 
 
 def _silence(layer, names):
@@ -517,7 +517,7 @@ def test_pairformer_sequence_stack_is_fp32_under_autocast():
     runs with autocast disabled: s_out equals the fp32 sequence stack applied
     to the (bf16-path) z_out, far inside the bf16 rounding it would show
     otherwise."""
-    layer = R.randomize(R.PairformerLayer(**_SMALL), generator=_gen(26))
+    layer = R.randomize(R.PairformerLayer(**_SMALL), generator=_gen(26)).eval()
     g = _gen(27)
     n = 6
     s = torch.randn(1, n, 16, generator=g)
@@ -711,3 +711,52 @@ def test_atom_transformer_windows_and_multiplicity(multiplicity):
                 x = nxt
             want[bi] = x
     assert _rel(got, want) < 1e-12
+
+
+@pytest.mark.parametrize("branch,columnwise", [("tri_mul_out", False), ("tri_att_start", False),
+                                               ("tri_att_end", True)])
+def test_pairformer_dropout_masks_rows_or_columns(branch, columnwise):
+    """The dropout masks (upstream ``get_dropout_mask``): in training with rate
+    1/2 and only ``branch`` left on, z_out - z is, per row (per column for the
+    ending node), either zero or twice the branch output on the same z, and
+    both kinds occur; in eval the layer equals the unmasked sum, and it draws
+    from the generator exactly what the four masks' shapes draw (3 x [B, N]
+    and 1 x [B, N]), so a caller's later draws are those of the upstream layer."""
+    layer = _small_layer(30)
+    layer.dropout = 0.5
+    _silence(layer, [b for b in _BRANCHES if b != branch])
+    g = _gen(31)
+    n = 12
+    s = torch.randn(1, n, 16, generator=g, dtype=torch.float64)
+    z = torch.randn(1, n, n, 8, generator=g, dtype=torch.float64)
+    mask = torch.ones(1, n, dtype=torch.float64)
+    pm = mask[:, :, None] * mask[:, None, :]
+    mod = getattr(layer, branch)
+    with torch.no_grad():
+        y = mod(z, mask=pm)
+        layer.train()
+        torch.manual_seed(5)
+        _, z2 = layer(s, z, mask, pm)
+        layer.eval()
+        torch.manual_seed(6)
+        _, z_eval = layer(s, z, mask, pm)
+        after = torch.rand(3)
+        torch.manual_seed(6)
+        for _ in range(4):
+            torch.rand(1, n, dtype=torch.float64)
+        expected_after = torch.rand(3)
+    d = (z2 - z)[0]
+    y = y[0]
+    if columnwise:
+        d, y = d.transpose(0, 1), y.transpose(0, 1)
+    kinds = set()
+    for r in range(n):
+        if torch.equal(d[r], torch.zeros_like(d[r])):
+            kinds.add(0)
+        else:
+            assert torch.allclose(d[r], 2 * y[r], rtol=1e-12, atol=1e-12)
+            kinds.add(1)
+    assert kinds == {0, 1}
+    assert torch.allclose(z_eval, z + y[None] if not columnwise else z + y.transpose(0, 1)[None], rtol=1e-12,
+                          atol=1e-12)
+    assert torch.equal(after, expected_after)
