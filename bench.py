@@ -702,6 +702,11 @@ def diffusion_step(args):
                             f"transformer + atom decoder, {samples} samples, {tokens} tokens x 768 (16 heads), "
                             f"{atoms} atoms x 128 (4 heads, windows 32 x 128), fp32 as the reference runs them "
                             f"(BASELINE configs[4])",
+                "host_model": "stand-in for Boltz's score model: oracle/boltz_ref.py DiffusionStacks (the three "
+                              "stacks' upstream module structure, restated) with install() applied; every "
+                              "transformer layer, stack and attention runs the patched native forwards, while the "
+                              "container's glue (r_to_q and pos_update linears, the stack calls) is the stand-in's "
+                              "own torch code and is inside the timed region",
                 "samples": samples, "n_tokens": tokens, "n_atoms": atoms, "patched_modules": patched,
                 "ms_for_all_steps": round(ms * steps, 2),
                 "stack_ms": {k: round(v, 4) for k, v in block_ms.items()}},

@@ -679,6 +679,7 @@ def triattn_fp32(module, x, mask, starting):
         op = (layernorm_split3(x.view(-1, C), ln.eps) if starting
               else layernorm_split3_t(x, ln.eps).view(-1, split_width(C)))
         proj = mm_split(op, w3).view(n, n, TRIATTN_FP32_PROJ_COLS)
+        del op  # 0.9 KB per pair, not needed by the attention
         tri_bias = proj[..., 4 * C:4 * C + heads].permute(2, 0, 1).contiguous()  # [H, q, k], shared by every row
     else:
         xn = norm(x.view(-1, C), _f32(ln.weight), _f32(ln.bias), ln.eps, bf16_output=False)
@@ -694,6 +695,7 @@ def triattn_fp32(module, x, mask, starting):
     # the split-bf16 kernel (about 2^-16 relative per product; 1.8x faster at N = 1024) unless exact
     # fp32 products are asked for
     o = seq_attention_batched(q, k, v, tri_bias[None], m, g, module.inf, bias_div=n, split=not _EXACT_FP32[0])
+    del q, k, v, g, proj, tri_bias  # 2.3 KB per pair, before linear_o's output is allocated
     out = torch.nn.functional.linear(o, mha.linear_o.weight.float(), mha.linear_o.bias.float())
     return out if starting else out.transpose(0, 1)
 

@@ -29,13 +29,36 @@ def _native_shape_ok(module, x) -> bool:
     )
 
 
+# fp32 mode holds about this many bytes per pair at its peak (``ops.triattn_fp32``:
+# the [N^2, 576] fp32 projection, the split-bf16 attention's K / V workspace,
+# the attention output and the linear_o result), all N rows at once.
+FP32_BYTES_PER_PAIR = 4608
+# ... and runs natively while that fits in this share of the device memory
+# (N up to about 5300 on a 288 GB MI355X); larger N run upstream's chunked
+# fp32 forward.
+FP32_MEMORY_SHARE = 0.45
+
+
+def fp32_native_fits(n: int, device_bytes: int) -> bool:
+    """Whether fp32-mode triangle attention at size ``n`` runs natively on a
+    device of ``device_bytes`` (its working set within ``FP32_MEMORY_SHARE``)."""
+    return FP32_BYTES_PER_PAIR * n * n <= FP32_MEMORY_SHARE * device_bytes
+
+
 def triangle_attention_forward(self, x, mask=None, chunk_size=None, use_kernels=False):
     """Drop-in for ``TriangleAttention{,EndingNode}.forward(x, mask, chunk_size, use_kernels)``.
 
     Native in inference under bf16 autocast (or for bf16 x), with a bf16
     result like the upstream autocast path; and in fp32 mode (autocast off,
-    fp32 x; reference triangle.py:38-52), with an fp32 result from fp32
-    LayerNorm, fp32 GEMMs and the fused fp32-MFMA attention (``ops.triattn_fp32``)."""
+    fp32 x; reference triangle.py:38-52), with an fp32 result
+    (``ops.triattn_fp32``): by default one split-bf16 GEMM of
+    LayerNorm-without-affine(x) for q | k | v | g and the triangle bias (the
+    LayerNorm affine folded into the weights) and the fused split-bf16
+    attention, about 2^-16 relative per product; with
+    ``BMX_EXACT_FP32_LINEARS=1`` the fp32 LN128 kernel, fp32 GEMMs and the
+    fp32-MFMA attention.  fp32 mode holds all N rows at once, so it runs
+    natively only while its working set fits (``fp32_native_fits``); larger N
+    take the class forward, which chunks the rows."""
     base = (
         not use_kernels
         and inference(self)
@@ -45,6 +68,8 @@ def triangle_attention_forward(self, x, mask=None, chunk_size=None, use_kernels=
     )
     starting = getattr(self, "starting", True)
     if base and autocast_off() and x.dtype == torch.float32 and self.layer_norm.weight.dtype == torch.float32:
+        if not fp32_native_fits(x.shape[1], torch.cuda.get_device_properties(x.device).total_memory):
+            return type(self).forward(self, x, mask, chunk_size=chunk_size, use_kernels=use_kernels)
         outs = [ops.triattn_fp32(self, x[b], None if mask is None else mask[b], starting) for b in range(x.shape[0])]
         return torch.stack(outs)
     supported = base and (bf16_autocast() or x.dtype == torch.bfloat16) and x.dtype in (torch.float32, torch.bfloat16)

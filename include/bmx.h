@@ -42,7 +42,7 @@ int bmx_layernorm128(const void* x, int x_dtype, int channel_first, const float*
                      void* out, int out_dtype, int64_t rows, bmx_stream_t stream);
 
 /* General LN over dim <= 1024 (dim % 4 == 0) with optional weight/bias (NULL = none).
- * Serves AdaLN.a_norm / s_norm, which the reference leaves to torch (diffusion.py:83-84). */
+ * Serves AdaLN.a_norm / s_norm, which the reference leaves to torch (diffusion.py:55-56). */
 int bmx_layernorm(const void* x, const float* weight, const float* bias, float eps, void* out, int dtype, int64_t rows,
                   int dim, bmx_stream_t stream);
 

@@ -252,3 +252,16 @@ def test_split_bf16_threshold_follows_width_and_rows():
         assert not ops.use_split(768, 5120) and not ops.use_split(128, 40960)
     finally:
         ops.exact_fp32_linears(before)
+
+
+def test_fp32_triangle_attention_native_only_while_its_working_set_fits():
+    """fp32-mode triangle attention holds ~4.6 KB per pair for all N rows at
+    once: natively up to about N = 5300 on a 288 GB MI355X, the class forward
+    (upstream's chunked rows) above, e.g. at the kernels' N = 8192 limit."""
+    from boltz_lumi_amd.triangle import FP32_BYTES_PER_PAIR, fp32_native_fits
+
+    mi355x = 288 * 1024 ** 3
+    assert fp32_native_fits(1024, mi355x) and fp32_native_fits(4096, mi355x) and fp32_native_fits(5300, mi355x)
+    assert not fp32_native_fits(6500, mi355x) and not fp32_native_fits(8192, mi355x)
+    assert not fp32_native_fits(4096, 64 * 1024 ** 3)  # a smaller device caps earlier
+    assert FP32_BYTES_PER_PAIR * 8192 ** 2 > 288e9  # all rows at once would not fit at N = 8192
