@@ -172,6 +172,59 @@ __device__ __forceinline__ f32x4 ln128_half(f32x4 v, const LnAffine& a, float ep
   return d * inv * a.w + a.b;
 }
 
+// K independent half-wave sums, each step issued for all K before the next:
+// the K DPP chains and the K ds_swizzle round trips overlap instead of
+// waiting one after another.  Each sum is the same bits as half_sum.
+template <int K>
+__device__ __forceinline__ void half_sums(float (&v)[K]) {
+#pragma unroll
+  for (int u = 0; u < K; ++u) v[u] += dpp<0xB1>(v[u]);
+#pragma unroll
+  for (int u = 0; u < K; ++u) v[u] += dpp<0x4E>(v[u]);
+#pragma unroll
+  for (int u = 0; u < K; ++u) v[u] += dpp<0x141>(v[u]);
+#pragma unroll
+  for (int u = 0; u < K; ++u) v[u] += dpp<0x140>(v[u]);
+  float x[K];
+#pragma unroll
+  for (int u = 0; u < K; ++u) x[u] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v[u]), 0x401F));
+#pragma unroll
+  for (int u = 0; u < K; ++u) v[u] += x[u];
+}
+
+// ln128_half of K rows (one per element of v, all held by this half-wave),
+// with the reductions of the K rows interleaved; row u is zeroed where
+// keep[u] is false.  Bit for bit ln128_half per row.
+template <int K>
+__device__ __forceinline__ void ln128_half_rows(f32x4 (&v)[K], const bool (&keep)[K], const LnAffine& a, float eps) {
+  float s[K];
+#pragma unroll
+  for (int u = 0; u < K; ++u) s[u] = v[u][0] + v[u][1] + v[u][2] + v[u][3];
+  half_sums(s);
+  float q[K];
+#pragma unroll
+  for (int u = 0; u < K; ++u) {
+    v[u] = v[u] - s[u] * (1.f / kC);
+    q[u] = v[u][0] * v[u][0] + v[u][1] * v[u][1] + v[u][2] * v[u][2] + v[u][3] * v[u][3];
+  }
+  half_sums(q);
+#pragma unroll
+  for (int u = 0; u < K; ++u) {
+    const float inv = rsqrtf(q[u] * (1.f / kC) + eps);
+    const f32x4 y = v[u] * inv * a.w + a.b;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[u][c] = keep[u] ? y[c] : 0.f;
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void ln128_half_rows(f32x4 (&v)[K], const LnAffine& a, float eps) {
+  bool keep[K];
+#pragma unroll
+  for (int u = 0; u < K; ++u) keep[u] = true;
+  ln128_half_rows(v, keep, a, eps);
+}
+
 // Normalise TP rows of 128 channels into an LDS tile lds[TP][kLdsRow] (bf16).
 // row_ptr(p) returns the row's base pointer or nullptr for padding rows,
 // which are written as zeros.  Padding rows read the valid row `safe`

@@ -100,11 +100,11 @@ constexpr int kP1 = 64;
 constexpr int kQRow = kD + 8;   // staged q / k row of one pair (bf16, 80 bytes)
 constexpr int kVRow = kP1 + 8;  // staged v^T row of one head dim (bf16, 144 bytes)
 
-template <typename TIn>
+template <typename TIn, bool starting>
 __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restrict__ x, const float* __restrict__ mask,
                                                               const float* __restrict__ ln_w,
                                                               const float* __restrict__ ln_b, float eps,
-                                                              const bf16* __restrict__ w_proj, float inf, int starting,
+                                                              const bf16* __restrict__ w_proj, float inf,
                                                               Layout L) {
   __shared__ __attribute__((aligned(16))) bf16 xt[kP1 * kLdsRow];
   __shared__ __attribute__((aligned(16))) bf16 sq[kH * kP1 * kQRow];
@@ -166,11 +166,13 @@ __global__ __launch_bounds__(256, 2) void triattn_proj_kernel(const TIn* __restr
   if (tile < total) fetch(tile);
   for (; tile < total; tile += gridDim.x) {
     const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP1;
+    bool keep[kRowsPer];
+#pragma unroll
+    for (int u = 0; u < kRowsPer; ++u) keep[u] = i < n && j0 + hw + 8 * u < n;
+    ln128_half_rows(px, keep, aff, eps);  // px is fetched again after the barrier
 #pragma unroll
     for (int u = 0; u < kRowsPer; ++u) {
-      f32x4 y = ln128_half(px[u], aff, eps);
-      if (i >= n || j0 + hw + 8 * u >= n) y = f32x4{0.f, 0.f, 0.f, 0.f};
-      const bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+      const bf16x4 o = {(bf16)px[u][0], (bf16)px[u][1], (bf16)px[u][2], (bf16)px[u][3]};
       *(bf16x4*)(xt + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
     }
     if (t < kP1) {
@@ -658,13 +660,13 @@ __global__ __launch_bounds__(kCoreThreads) __attribute__((amdgpu_waves_per_eu(4)
 // ending node).
 constexpr int kP3 = 64;
 
-template <typename TIn, bool kScaled>
+template <typename TIn, bool kScaled, bool starting>
 __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const float* __restrict__ ln_w,
                                                              const float* __restrict__ ln_b, float eps,
                                                              const bf16* __restrict__ w_g,
                                                              const float* __restrict__ b_g,
                                                              const bf16* __restrict__ w_o,
-                                                             const float* __restrict__ b_o, int starting, void* out,
+                                                             const float* __restrict__ b_o, void* out,
                                                              int out_mode, const float* __restrict__ row_scale,
                                                              Layout L) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kP3 * kLdsRow];
@@ -725,10 +727,11 @@ __global__ __launch_bounds__(256, 2) void triattn_out_kernel(const TIn* x, const
     const float rs = prs;
     f32x4 xc[kRowsPer];
 #pragma unroll
+    for (int u = 0; u < kRowsPer; ++u) xc[u] = px[u];
+    ln128_half_rows(px, aff, eps);  // px is fetched again after the barrier
+#pragma unroll
     for (int u = 0; u < kRowsPer; ++u) {
-      xc[u] = px[u];
-      f32x4 y = ln128_half(px[u], aff, eps);
-      bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+      bf16x4 o = {(bf16)px[u][0], (bf16)px[u][1], (bf16)px[u][2], (bf16)px[u][3]};
       *(bf16x4*)(xg + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
       *(bf16x4*)(xo + (hw + 8 * u) * kLdsRow + 4 * hl) = po[u];
     }
@@ -807,7 +810,10 @@ int run(const TIn* x, const float* mask, int n, int starting, float inf, const f
   if (stages & 1) {
     const int total = L.np * (L.np / kP1);
     const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
-    triattn_proj_kernel<TIn><<<dim3(grid), 256, 0, st>>>(x, mask, ln_w, ln_b, eps, w_proj, inf, starting, L);
+    if (starting)
+      triattn_proj_kernel<TIn, true><<<dim3(grid), 256, 0, st>>>(x, mask, ln_w, ln_b, eps, w_proj, inf, L);
+    else
+      triattn_proj_kernel<TIn, false><<<dim3(grid), 256, 0, st>>>(x, mask, ln_w, ln_b, eps, w_proj, inf, L);
     if (int rc = check_launch("triattn_proj")) return rc;
   }
   if (stages & 2) {
@@ -817,12 +823,16 @@ int run(const TIn* x, const float* mask, int n, int starting, float inf, const f
   if (stages & 4) {
     const int total = n * ((n + kP3 - 1) / kP3);
     const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
+    auto launch_out = [&](auto scaled, auto start) {
+      triattn_out_kernel<TIn, decltype(scaled)::value, decltype(start)::value>
+          <<<dim3(grid), 256, 0, st>>>(x, ln_w, ln_b, eps, w_g, b_g, w_o, b_o, out, out_mode, row_scale, L);
+    };
+    using T = std::true_type;
+    using F = std::false_type;
     if (row_scale)
-      triattn_out_kernel<TIn, true><<<dim3(grid), 256, 0, st>>>(x, ln_w, ln_b, eps, w_g, b_g, w_o, b_o, starting, out,
-                                                                out_mode, row_scale, L);
+      starting ? launch_out(T{}, T{}) : launch_out(T{}, F{});
     else
-      triattn_out_kernel<TIn, false><<<dim3(grid), 256, 0, st>>>(x, ln_w, ln_b, eps, w_g, b_g, w_o, b_o, starting,
-                                                                 out, out_mode, nullptr, L);
+      starting ? launch_out(F{}, T{}) : launch_out(F{}, F{});
     if (int rc = check_launch("triattn_out")) return rc;
   }
   return BMX_OK;

@@ -38,14 +38,16 @@ constexpr int kPlaneTile = 256;        // plane padding granularity (the contrac
 constexpr int kP1 = 64;                // pairs per K1 tile (one plane row segment)
 constexpr int kStage1 = kP1 + 8;       // staged plane rows (bf16)
 
+template <bool kOutgoing>
 __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __restrict__ x,
                                                              const float* __restrict__ mask,
                                                              const float* __restrict__ ln_w,
                                                              const float* __restrict__ ln_b, float eps,
                                                              const bf16* __restrict__ w_in, bf16* __restrict__ a_pl,
-                                                             bf16* __restrict__ b_pl, int n, int np, int outgoing) {
+                                                             bf16* __restrict__ b_pl, int n, int np) {
   __shared__ __attribute__((aligned(16))) bf16 xt[kP1 * kLdsRow];
   __shared__ __attribute__((aligned(16))) bf16 stage[2 * kC * kStage1];
+  __shared__ __attribute__((aligned(16))) float msk[kP1];  // the tile's mask values, 0 for padding
   const int l = lane_id(), w = threadIdx.x >> 6, c0 = 32 * w;
   const int hw = threadIdx.x >> 5, hl = threadIdx.x & 31;
   const LnAffine aff = ln_affine(ln_w, ln_b, hl);
@@ -73,12 +75,12 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
 #pragma unroll
     for (int nt = 0; nt < kP1 / 32; ++nt) {  // first, so that a wait for them leaves the rows in flight
       const int tc = min(t0 + nt * 32 + (l & 31), n - 1);
-      mpre[nt] = mask[outgoing ? (int64_t)rc * n + tc : (int64_t)tc * n + rc];
+      mpre[nt] = mask[kOutgoing ? (int64_t)rc * n + tc : (int64_t)tc * n + rc];
     }
 #pragma unroll
     for (int u = 0; u < kP1 / 8; ++u) {
       const int tc = min(t0 + hw + 8 * u, n - 1);
-      const int64_t pair = outgoing ? (int64_t)rc * n + tc : (int64_t)tc * n + rc;
+      const int64_t pair = kOutgoing ? (int64_t)rc * n + tc : (int64_t)tc * n + rc;
       pre[u] = load4(x + pair * kC + 4 * hl);
     }
   };
@@ -104,41 +106,46 @@ __global__ __launch_bounds__(256, 2) void trimul_proj_kernel(const float* __rest
   if (tile < total) fetch(tile);
   for (; tile < total; tile += gridDim.x) {
     const int rp = tile / tiles_x, t0 = (tile % tiles_x) * kP1;
+    bool keep[kP1 / 8];
+#pragma unroll
+    for (int u = 0; u < kP1 / 8; ++u) keep[u] = rp < n && t0 + hw + 8 * u < n;
+    ln128_half_rows(pre, keep, aff, eps);
 #pragma unroll
     for (int u = 0; u < kP1 / 8; ++u) {
-      const int tt = t0 + hw + 8 * u;
-      f32x4 y = ln128_half(pre[u], aff, eps);
-      if (rp >= n || tt >= n) y = f32x4{0.f, 0.f, 0.f, 0.f};
-      bf16x4 o = {(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+      bf16x4 o = {(bf16)pre[u][0], (bf16)pre[u][1], (bf16)pre[u][2], (bf16)pre[u][3]};
       *(bf16x4*)(xt + (hw + 8 * u) * kLdsRow + 4 * hl) = o;
     }
-    float mcur[kP1 / 32];
-#pragma unroll
-    for (int nt = 0; nt < kP1 / 32; ++nt) mcur[nt] = mpre[nt];
+    // rows / columns past n (plane padding) are written as zeros
+    const float mt = (rp < n && t0 + l < n) ? mpre[l >> 5] : 0.f;
+    if (w == 0) msk[l] = mt;
     if (prev >= 0) store_planes(prev);
     __syncthreads();  // xt written; the stage has been read
     if (tile + (int)gridDim.x < total) fetch(tile + gridDim.x);
 
-    // D[ch][pair]: A = weight rows, B = normalised pairs; lane l holds pair l%32.
+    // D[pair][ch]: A = normalised pairs, B = weight rows; lane l holds channel
+    // c0 + l%32, and its registers 4q..4q+3 hold 4 consecutive pairs, which
+    // leave as one 8-byte write into the channel's stage row.
 #pragma unroll
     for (int nt = 0; nt < kP1 / 32; ++nt) {
-      const int tt = t0 + nt * 32 + (l & 31);
-      // rows / columns past n (plane padding) are written as zeros
-      const float m = (rp < n && tt < n) ? mcur[nt] : 0.f;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         f32x16 ap = zero16(), ag = zero16();
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
           bf16x8 xf = frag(xt, kLdsRow, nt * 32, ks);
-          ap = mfma32(wf[2 * half][ks], xf, ap);
-          ag = mfma32(wf[2 * half + 1][ks], xf, ag);
+          ap = mfma32(xf, wf[2 * half][ks], ap);
+          ag = mfma32(xf, wf[2 * half + 1][ks], ag);
         }
+        bf16* srow = stage + (half * kC + c0 + (l & 31)) * kStage1;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
+        for (int q = 0; q < 4; ++q) {
+          const int p0 = nt * 32 + drow(4 * q, l);
+          const f32x4 m = *(const f32x4*)(msk + p0);
           // p * sigmoid(g) * mask, rounded once to the bf16 operand
-          const float v = ap[r] * sigmoid_f(ag[r]) * m;
-          stage[(half * kC + c0 + drow(r, l)) * kStage1 + nt * 32 + (l & 31)] = (bf16)v;
+          bf16x4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = (bf16)(ap[4 * q + i] * sigmoid_f(ag[4 * q + i]) * m[i]);
+          *(bf16x4*)(srow + p0) = o;
         }
       }
     }
@@ -505,8 +512,12 @@ int launch(const float* x, const float* mask, int ni, int outgoing, const float*
   if (stages & 1) {
     const int total = np * (np / kP1);
     const int grid = total < 2 * device_cu_count() ? total : 2 * device_cu_count();
-    trimul_proj_kernel<<<dim3(grid), 256, 0, stream>>>(x, mask, norm_in_w, norm_in_b, eps_in, w_in, a_pl, b_pl, ni,
-                                                       np, outgoing);
+    if (outgoing)
+      trimul_proj_kernel<true><<<dim3(grid), 256, 0, stream>>>(x, mask, norm_in_w, norm_in_b, eps_in, w_in, a_pl, b_pl,
+                                                               ni, np);
+    else
+      trimul_proj_kernel<false><<<dim3(grid), 256, 0, stream>>>(x, mask, norm_in_w, norm_in_b, eps_in, w_in, a_pl,
+                                                                b_pl, ni, np);
     if (int rc = check_launch("trimul_proj")) return rc;
   }
   if (stages & 2) {
