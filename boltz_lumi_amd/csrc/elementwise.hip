@@ -63,40 +63,48 @@ __global__ __launch_bounds__(256) void split_kernel(const bf16* __restrict__ p, 
 //   outgoing: a_cm[c][i][k] = a[i,k,c],  b_cm[c][k][j] = b[j,k,c]
 //   incoming: a_cm[c][i][k] = a[k,i,c],  b_cm[c][k][j] = b[k,j,c]
 // (the reference's bmm(left, right) layout, multiplication_gate_hip.cu:52-58).
-// A block transposes a 16x16 pair tile for 32 channels through LDS.
+// Plane row r, columns t of an operand come from pairs (r, t), or (t, r) when
+// the operand is transposed (b outgoing, a incoming).  A block writes one
+// 64-column segment of one plane row for all 128 channels, as trimul_proj
+// writes its operand planes: each thread gates 8 channels of one source pair
+// from 16-byte loads into an LDS [channel][column] tile, which leaves as
+// 16-byte segment stores.
+constexpr int kPackSeg = 64;
+
 __global__ __launch_bounds__(256) void pack_kernel(const bf16* __restrict__ p, const bf16* __restrict__ g,
                                                    const float* __restrict__ mask, bf16* __restrict__ a,
                                                    bf16* __restrict__ b, int n, int stride, int outgoing) {
-  __shared__ bf16 ta[32][16][17], tb[32][16][17];
-  const int i0 = blockIdx.x * 16, j0 = blockIdx.y * 16, c0 = blockIdx.z * 32;
-  for (int idx = threadIdx.x; idx < 16 * 16 * 32; idx += 256) {
-    int c = idx & 31, j = (idx >> 5) & 15, i = idx >> 9;
-    float va = 0.f, vb = 0.f;
-    if (i0 + i < n && j0 + j < n) {
-      int64_t pair = (int64_t)(i0 + i) * n + j0 + j;
-      float m = mask[pair];
-      const bf16* pp = p + pair * stride + c0 + c;
-      const bf16* gg = g + pair * stride + c0 + c;
-      va = rbf(gated((float)pp[0], (float)gg[0])) * m;
-      vb = rbf(gated((float)pp[kC], (float)gg[kC])) * m;
+  __shared__ __attribute__((aligned(16))) bf16 tile[kC][kPackSeg + 8];
+  const int r = blockIdx.x, t0 = blockIdx.y * kPackSeg, operand = blockIdx.z;  // operand 0: a, 1: b
+  const bool transposed = (operand == 0) != (outgoing != 0);
+  const int ch0 = operand * kC;  // the operand's channels within p / g rows
+  for (int idx = threadIdx.x; idx < kPackSeg * (kC / 8); idx += 256) {
+    const int col = idx >> 4, c8 = (idx & 15) * 8, t = t0 + col;
+    bf16x8 v = {};
+    if (t < n) {
+      const int64_t pair = transposed ? (int64_t)t * n + r : (int64_t)r * n + t;
+      const float m = mask[pair];
+      const bf16x8 pv = *(const bf16x8*)(p + pair * stride + ch0 + c8);
+      const bf16x8 gv = *(const bf16x8*)(g + pair * stride + ch0 + c8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (bf16)(rbf(gated((float)pv[e], (float)gv[e])) * m);
     }
-    ta[c][i][j] = (bf16)va;
-    tb[c][i][j] = (bf16)vb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[c8 + e][col] = v[e];
   }
   __syncthreads();
   const int64_t plane = (int64_t)n * n;
-  for (int idx = threadIdx.x; idx < 16 * 16 * 32; idx += 256) {
-    int j = idx & 15, i = (idx >> 4) & 15, c = idx >> 8;
-    bf16* ap = a + (int64_t)(c0 + c) * plane;
-    bf16* bp = b + (int64_t)(c0 + c) * plane;
-    if (outgoing) {
-      // a_cm[c][i0+i][j0+j] = a[i0+i, j0+j];  b_cm[c][j0+i][i0+j] = b[i0+j, j0+i]
-      if (i0 + i < n && j0 + j < n) ap[(int64_t)(i0 + i) * n + j0 + j] = ta[c][i][j];
-      if (j0 + i < n && i0 + j < n) bp[(int64_t)(j0 + i) * n + i0 + j] = tb[c][j][i];
+  bf16* dst = (operand ? b : a) + (int64_t)r * n + t0;
+  const bool vec = n % 8 == 0;  // 16-byte aligned segment starts
+  for (int idx = threadIdx.x; idx < kC * (kPackSeg / 8); idx += 256) {
+    const int c = idx >> 3, col = (idx & 7) * 8;
+    bf16* out = dst + c * plane + col;
+    if (vec && t0 + col + 8 <= n) {
+      *(bf16x8*)out = *(const bf16x8*)&tile[c][col];
     } else {
-      // a_cm[c][j0+i][i0+j] = a[i0+j, j0+i];  b_cm[c][i0+i][j0+j] = b[i0+i, j0+j]
-      if (j0 + i < n && i0 + j < n) ap[(int64_t)(j0 + i) * n + i0 + j] = ta[c][j][i];
-      if (i0 + i < n && j0 + j < n) bp[(int64_t)(i0 + i) * n + j0 + j] = tb[c][i][j];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (t0 + col + e < n) out[e] = tile[c][col + e];
     }
   }
 }
@@ -280,7 +288,8 @@ int bmx_trimul_pack(const void* p, const void* g, const float* mask, void* a, vo
   BMX_REQUIRE(row_stride == 256 || row_stride == 512, "bmx_trimul_pack: row stride must be 256 or 512");
   if (n == 0) return BMX_OK;
   BMX_REQUIRE(p && g && mask && a && b, "bmx_trimul_pack: null pointer");
-  dim3 grid((unsigned)((n + 15) / 16), (unsigned)((n + 15) / 16), kC / 32);
+  BMX_REQUIRE(((uintptr_t)p | (uintptr_t)g) % 16 == 0, "bmx_trimul_pack: p and g must be 16-byte aligned");
+  dim3 grid((unsigned)n, (unsigned)((n + kPackSeg - 1) / kPackSeg), 2);
   pack_kernel<<<grid, 256, 0, stream>>>((const bf16*)p, (const bf16*)g, mask, (bf16*)a, (bf16*)b, (int)n,
                                         row_stride, outgoing);
   return check_launch("bmx_trimul_pack");

@@ -69,6 +69,7 @@ int bmx_trimul_split(const void* p, const void* g, const float* mask, void* a, v
                      bmx_stream_t stream);
 
 /* Channel-major bmm operands a,b[128][n][n] (outgoing: b transposed; incoming: a transposed).
+ * p and g must be 16-byte aligned.
  * Replaces multiplication_gate_pack (kernels/multiplication_gate_hip.cu:96-123, `pack`). */
 int bmx_trimul_pack(const void* p, const void* g, const float* mask, void* a, void* b, int64_t n, int row_stride,
                     int outgoing, bmx_stream_t stream);
