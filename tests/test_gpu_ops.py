@@ -84,7 +84,7 @@ def test_silu_mul_non_default_stream(gpu):
     assert bits_close(got, want)
 
 
-@pytest.mark.parametrize("n", [7, 117, 130])
+@pytest.mark.parametrize("n", [7, 117, 130, 136])  # 136: 16-byte segment stores, then a ragged tail
 @pytest.mark.parametrize("joint", [False, True])
 def test_split_and_pack(gpu, n, joint):
     g = torch.Generator().manual_seed(n)
