@@ -125,8 +125,13 @@ def dropout_mask(layer, z, columnwise=False):
     generator as upstream's does."""
     p = float(getattr(layer, "dropout", 0.0)) * layer.training
     v = z[:, 0:1, :, 0:1] if columnwise else z[:, :, 0:1, 0:1]
-    d = torch.rand_like(v) > p
-    return d * 1.0 / (1.0 - p)
+    d = torch.rand_like(v)
+    if p == 0.0:
+        # (d > 0) * 1.0 / 1.0 as one in-place comparison: the same 0 / 1
+        # values in one kernel instead of three (the fused path runs in eval,
+        # where the rate is always 0)
+        return d.gt_(0.0)
+    return (d > p) * 1.0 / (1.0 - p)
 
 
 def _row_scales(mask):

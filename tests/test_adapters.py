@@ -265,3 +265,23 @@ def test_fp32_triangle_attention_native_only_while_its_working_set_fits():
     assert not fp32_native_fits(6500, mi355x) and not fp32_native_fits(8192, mi355x)
     assert not fp32_native_fits(4096, 64 * 1024 ** 3)  # a smaller device caps earlier
     assert FP32_BYTES_PER_PAIR * 8192 ** 2 > 288e9  # all rows at once would not fit at N = 8192
+
+
+@pytest.mark.parametrize("training", [False, True])
+@pytest.mark.parametrize("columnwise", [False, True])
+def test_dropout_masks_match_upstream_draws(training, columnwise):
+    """The installed layer's dropout masks (one in-place comparison in eval)
+    are upstream's get_dropout_mask values, dtype and shape, and leave the
+    generator where upstream's leave it."""
+    from boltz_lumi_amd import pairformer
+
+    layer = SimpleNamespace(dropout=0.25, training=training)
+    z = torch.randn(2, 37, 37, 128)
+    torch.manual_seed(5)
+    got = pairformer.dropout_mask(layer, z, columnwise)
+    state_got = torch.get_rng_state()
+    torch.manual_seed(5)
+    want = R.get_dropout_mask(0.25, z, training, columnwise)
+    assert got.dtype == want.dtype and got.shape == want.shape
+    assert torch.equal(got, want)
+    assert torch.equal(state_got, torch.get_rng_state())
