@@ -312,7 +312,7 @@ def pairformer(args):
 
     dev = torch.device("cuda:0")
     n = args.n or 1024
-    steps = args.steps or 10
+    steps = args.steps or 20
     if args.calibrate_copy:
         src = torch.ones(1 << 28, device=dev)  # 1 GiB of fp32
         dst = torch.empty_like(src)
@@ -403,7 +403,7 @@ def dropin(args):
 
     dev = torch.device("cuda:0")
     n = args.n or 1024
-    steps = args.steps or 10
+    steps = args.steps or 20
     layer = init_weights(layers.PairformerLayer(), 0).to(dev).eval()
     g = torch.Generator().manual_seed(0)
     z = torch.randn(1, n, n, 128, generator=g).to(dev)
