@@ -27,9 +27,9 @@ Prints one JSON line.  ``roofline`` covers the kernel with the largest share
 of the step, timed with HIP events on the launch stream; its ``bound`` is
 whichever of flop time (at the MFMA peak) and byte time (at 8 TB/s) is larger.
 ``modules`` gives each triangle module's time against its roofline T* =
-max(F / 2.5 PFLOP/s, B / 8 TB/s) (F, B as in BASELINE.md section 2).
-``cpu_baseline`` times the CPU oracle on the host cores (a reported baseline,
-not the target), following BASELINE.md section 3.
+max(F / 2.5 PFLOP/s, B / 8 TB/s), F the module's algorithmic flops and B its
+compulsory HBM bytes (``tri_module_cost``).  ``cpu_baseline`` times the fp32
+CPU oracle on the host cores: a reported baseline, not the target.
 """
 
 from __future__ import annotations
@@ -101,8 +101,8 @@ def fan_in_weights(module, seed: int):
 
 
 def tri_module_cost(kind: str, n: int):
-    """(F flops, B compulsory bytes) of one triangle module direction
-    (BASELINE.md section 2): tri-attention F = 512 N^3 + 164864 N^2,
+    """(F flops, B compulsory bytes) of one triangle module direction:
+    tri-attention F = 512 N^3 + 164864 N^2,
     tri-multiplication F = 256 N^3 + 196608 N^2; B = N^2 (128*4 + 4 + 128*2)
     (fp32 z and mask in, bf16 out)."""
     n2, n3 = float(n) ** 2, float(n) ** 3
@@ -271,7 +271,7 @@ def _median_ms(fn, reps, warm=None):
 
 
 def cpu_pairformer(n_layer=1024, n_small=128):
-    """one PairformerLayer of the
+    """CPU baseline of configs[0] and configs[3]: one PairformerLayer of the
     fp32 oracle at N=128 (2 warm-ups, median of 10) and at N=1024 (one
     warm-up at N=256, median of 2; x64 reported as the extrapolated trunk)."""
     import torch
@@ -354,7 +354,7 @@ def pairformer(args):
         f, b = tri_module_cost("triattn" if name.startswith("triattn") else "trimul", n)
         ts = t_star_ms(f, b)
         modules[name] = {"ms": round(mod_ms, 4), "t_star_ms": round(ts, 4), "frac": round(ts / mod_ms, 4)}
-    layer_f = 2.831e12 * (n / 1024) ** 3  # BASELINE.md section 2, configs[3] (dominated by the N^3 terms)
+    layer_f = 2.831e12 * (n / 1024) ** 3  # algorithmic flops of one layer at N=1024 (dominated by the N^3 terms)
     modules["layer"] = {"ms": round(ms, 4), "t_star_ms": round(t_star_ms(layer_f, 0), 4),
                         "frac": round(t_star_ms(layer_f, 0) / ms, 4)}
     out = line("Pairformer layer ms @N=1024 bf16", ms, "ms", args, steps, "bf16",
@@ -596,7 +596,7 @@ def isolated_module(args, kind):
 
 
 def cpu_isolated(kind, n, masked):
-    """the fp32 oracle module per
+    """CPU baseline of configs[1] and configs[2]: the fp32 oracle module per
     direction, one warm-up at a quarter of N, median of 3."""
     import torch
 
@@ -857,8 +857,8 @@ def diffusion_kernel_times(stacks, t, packed, samples, tokens):
 
 
 def cpu_diffusion_step(tokens, steps):
-    """one denoiser step of the fp32
-    oracle stacks for one of the 5 samples (x5), reported x``steps`` as
+    """CPU baseline of configs[4]: one denoiser step of the fp32 oracle
+    stacks for one of the 5 samples (x5), reported x``steps`` as
     extrapolated."""
     import torch
 

@@ -117,7 +117,7 @@ class Attention(nn.Module):
 
 
 # --------------------------------------------------------------------------
-# Triangle attention  (reference: triangle.py, SURVEY rows A1-A3)
+# Triangle attention  (reference: triangle.py)
 # --------------------------------------------------------------------------
 
 
@@ -324,7 +324,7 @@ class Transition(nn.Module):
 
 
 # --------------------------------------------------------------------------
-# Attention with pair bias (v2)  (reference: pair_bias.py:15-36, SURVEY F1/F2)
+# Attention with pair bias (v2)  (reference: pair_bias.py:15-36)
 # --------------------------------------------------------------------------
 
 
@@ -379,7 +379,7 @@ class AttentionPairBias(nn.Module):
 
 
 # --------------------------------------------------------------------------
-# Pairformer layer  
+# Pairformer layer
 # --------------------------------------------------------------------------
 
 
@@ -586,7 +586,7 @@ def randomize(module: nn.Module, std: float = 0.08, generator=None):
 
 
 # --------------------------------------------------------------------------
-# Diffusion transformer stacks
+# Diffusion transformer stacks (the score model's stacks at configs[4])
 # --------------------------------------------------------------------------
 
 
