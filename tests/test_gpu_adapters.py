@@ -49,7 +49,7 @@ def test_install_on_gfx950(model):
     assert adapters.install(model) == 9  # the Pairformer layer, its 5 pair modules, AdaLN, CTB and its AdaLN
 
 
-@pytest.mark.parametrize("n", [64, 117])
+@pytest.mark.parametrize("n", [17, 64, 117, 312, 576])  # the reference test's sizes (tests/test_operator_additions.py)
 def test_patched_pair_modules_match_upstream(model, gpu, n):
     layer = model.pairformer_module.layers[0]
     x = torch.randn(1, n, n, 128, device=gpu) * 0.3
@@ -78,6 +78,31 @@ def test_patched_pair_modules_match_upstream(model, gpu, n):
                 assert got.dtype == torch.float32 and max_rel(got, want[k]) < 1e-4, k
             else:  # upstream math, bit for bit
                 assert torch.equal(got, want[k]), k
+
+
+@pytest.mark.parametrize("n", [1134, 2511])
+def test_patched_triangle_attention_at_the_reference_token_counts(model, gpu, n):
+    """The installed triangle attention, both nodes, at the token counts the
+    reference publishes (partial mask: the last 3 tokens), against upstream's
+    fp32 forward on the same GPU (chunk 32, as the reference test)."""
+    layer = model.pairformer_module.layers[0]
+    g = torch.Generator(device=gpu).manual_seed(n)
+    x = torch.randn(1, n, n, 128, device=gpu, generator=g) * 0.3
+    mask = torch.ones(1, n, n, device=gpu)
+    mask[:, -3:, :] = 0
+    mask[:, :, -3:] = 0
+    print(f"installed triangle attention n={n}", flush=True)
+    for name in ("tri_att_start", "tri_att_end"):
+        mod = getattr(layer, name)
+        with torch.inference_mode():
+            want = mod(x, mask, chunk_size=32)  # upstream fp32 (not installed yet)
+        assert adapters.install(model) == 9
+        with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+            got = mod(x, mask, chunk_size=32)
+        adapters.uninstall(model)
+        assert got.dtype == torch.bfloat16 and torch.isfinite(got).all(), name
+        assert max_rel(got, want) < 2e-2, name
+        del want, got
 
 
 def test_grad_mode_falls_back(model, gpu):
