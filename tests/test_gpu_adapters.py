@@ -80,6 +80,24 @@ def test_patched_pair_modules_match_upstream(model, gpu, n):
                 assert torch.equal(got, want[k]), k
 
 
+@pytest.mark.parametrize("n", [17, 117, 312, 576])
+def test_patched_transition_dense_and_strided_input(model, gpu, n):
+    """The installed pair transition on a dense x and on the strided view
+    x[:, ::2] (the reference test's two layouts) against upstream's fp32
+    forward on the same input."""
+    layer = model.pairformer_module.layers[0]
+    x = torch.randn(1, n, n, 128, device=gpu) * 0.3
+    for inp in (x, x[:, ::2]):
+        with torch.inference_mode():
+            want = layer.transition_z(inp)
+        assert adapters.install(model) == 9
+        with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+            got = layer.transition_z(inp)
+        adapters.uninstall(model)
+        assert got.shape == inp.shape and got.dtype == torch.bfloat16
+        assert max_rel(got, want) < 2e-2
+
+
 @pytest.mark.parametrize("n", [1134, 2511])
 def test_patched_triangle_attention_at_the_reference_token_counts(model, gpu, n):
     """The installed triangle attention, both nodes, at the token counts the
