@@ -177,6 +177,47 @@ def test_conditioning_cache_computes_once(gpu):
             assert torch.equal(g_, w_)
 
 
+def test_conditioning_cache_recomputes_per_context_and_stays_off_under_autocast_or_grad(gpu):
+    """A new cache context computes the projections again; under bf16 autocast
+    or with grad enabled the cache does not memoise (every call computes),
+    and the results equal the uncached layer's (the reference's cases,
+    tests/test_atom_conditioning.py:100-130)."""
+    torch.manual_seed(99)
+    layers = [R.randomize(R.DiffusionTransformerLayer(4, 32, 32), std=0.07).to(gpu).eval() for _ in range(2)]
+    score = SimpleNamespace(
+        atom_attention_encoder=SimpleNamespace(atom_encoder=SimpleNamespace(
+            diffusion_transformer=SimpleNamespace(layers=layers[:1]))),
+        atom_attention_decoder=SimpleNamespace(atom_decoder=SimpleNamespace(
+            diffusion_transformer=SimpleNamespace(layers=layers[1:]))),
+    )
+    s = torch.randn(1, 17, 32, device=gpu)
+    bias = torch.randn(1, 17, 17, 4, device=gpu)
+    mask = torch.ones(1, 17, device=gpu)
+    a = torch.randn(1, 17, 32, device=gpu)
+    calls = []
+    norm = layers[0].adaln.s_norm
+    original = norm.forward
+    norm.forward = lambda x: (calls.append(1), original(x))[1]
+    with torch.inference_mode():
+        want = layers[0](a, s, bias, mask)
+        for _ in range(2):  # two contexts, two calls each: one computation per context
+            with atom_conditioning_cache(score):
+                for _ in range(2):
+                    assert torch.equal(layers[0](a, s, bias, mask), want)
+    assert len(calls) == 1 + 2
+    calls.clear()
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16), atom_conditioning_cache(score):
+        for _ in range(2):
+            layers[0](a, s, bias, mask)
+    assert len(calls) == 2  # not memoised under autocast
+    calls.clear()
+    with torch.enable_grad(), atom_conditioning_cache(score):
+        for _ in range(2):
+            got = layers[0](a, s, bias, mask)
+    assert len(calls) == 2  # not memoised with grad
+    assert torch.equal(got.detach(), want)
+
+
 def test_diffusion_widths_off_the_kernels_fall_back(gpu):
     """The fused epilogues take widths that are multiples of 4: a block of
     another width runs its class forward, bit for bit, instead of raising."""
