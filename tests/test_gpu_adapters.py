@@ -49,7 +49,7 @@ def test_install_on_gfx950(model):
     assert adapters.install(model) == 9  # the Pairformer layer, its 5 pair modules, AdaLN, CTB and its AdaLN
 
 
-@pytest.mark.parametrize("n", [17, 64, 117, 312, 576])  # the reference test's sizes (tests/test_operator_additions.py)
+@pytest.mark.parametrize("n", [7, 17, 64, 117, 312, 576])  # the reference test's sizes (tests/test_operator_additions.py)
 def test_patched_pair_modules_match_upstream(model, gpu, n):
     layer = model.pairformer_module.layers[0]
     x = torch.randn(1, n, n, 128, device=gpu) * 0.3
