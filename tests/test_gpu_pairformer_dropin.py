@@ -5,7 +5,9 @@ bf16 autocast.  Checked here:
 
 * at N = 1024 (the headline shape, 24 padded tokens) against the fp32 CPU
   oracle, and bit for bit against this package's own ``layers.PairformerLayer``
-  on the same weights (the benchmarked layer: the same kernels);
+  on the same weights (the benchmarked layer: the same kernels); at the
+  reference's published N = 1134 and 2511 against the oracle layer in fp32
+  on the GPU;
 * the dropout masks: the generator ends in the state upstream's forward leaves
   it in, and masks with zeros (forced on both sides) drop the same rows and
   columns as the oracle's;
@@ -96,6 +98,33 @@ def test_installed_layer_at_n1024_matches_oracle_and_benchmarked_layer(gpu):
     with torch.no_grad():
         s_ref, z_ref = ref(s, z, mask, pm)
     err_z, err_s = rel(z_got, z_ref, z), rel(s_got, s_ref, s)
+    print(f"  z update {err_z:.2e}  s update {err_s:.2e}", flush=True)
+    assert err_z < TOL and err_s < TOL
+
+
+@pytest.mark.parametrize("n", [1134, 2511])
+def test_installed_layer_at_the_reference_token_counts(gpu, n):
+    """The installed layer at the token counts the reference publishes (3
+    padded tokens) against upstream's fp32 composition, the oracle layer,
+    evaluated on the same GPU (on the CPU it would take minutes); both calls
+    start from the same generator state, so they draw the same dropout masks."""
+    print(f"installed PairformerLayer n={n} against the fp32 oracle layer on the GPU", flush=True)
+    ref, layer = installed(7, gpu)
+    ref_gpu = copy.deepcopy(ref).to(gpu)  # not installed: upstream's forward in fp32
+    sg, zg, mg, pmg = (t.to(gpu) for t in inputs(n, 3, 2))
+    with torch.inference_mode():
+        torch.manual_seed(11)
+        s_ref, z_ref = ref_gpu(sg, zg, mg, pmg, chunk_size_tri_attn=128)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        torch.manual_seed(11)
+        s_got, z_got = layer(sg, zg, mg, pmg, 128)
+    assert z_got.dtype == torch.float32 and torch.isfinite(z_got).all() and torch.isfinite(s_got).all()
+
+    def rel_gpu(got, want, base):
+        d, w = got - base, want - base
+        return ((d - w).abs().max() / w.abs().max()).item()
+
+    err_z, err_s = rel_gpu(z_got, z_ref, zg), rel_gpu(s_got, s_ref, sg)
     print(f"  z update {err_z:.2e}  s update {err_s:.2e}", flush=True)
     assert err_z < TOL and err_s < TOL
 
