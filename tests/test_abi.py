@@ -128,6 +128,36 @@ def test_argument_validation_needs_no_gpu(lib):
     assert lib.bmx_seq_attention_windowed_fwd(*wargs, 4, 32, ctypes.c_float(1e6), fake, None) == N.BMX_OK
 
 
+def test_operator_set_entry_points_reject_bad_arguments(lib):
+    # The reference's unfused operator set (gate / split / pack / silu_mul / bias softmax) and the
+    # stand-alone pair bias: every rejection happens before a launch.
+    fake, odd = ctypes.c_void_p(256), ctypes.c_void_p(264)  # 16-byte aligned / only 8-byte aligned
+    assert lib.bmx_silu_mul(None, None, None, 0, None) == N.BMX_OK  # empty input: nothing to do
+    rc = lib.bmx_silu_mul(None, fake, fake, 64, None)
+    assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
+    rc = lib.bmx_trimul_split(fake, fake, fake, fake, fake, 4, 384, None)
+    assert rc == N.BMX_EINVAL and b"row stride must be 256 or 512" in lib.bmx_last_error()
+    rc = lib.bmx_trimul_split(fake, fake, fake, odd, fake, 4, 256, None)
+    assert rc == N.BMX_EINVAL and b"16-byte aligned" in lib.bmx_last_error()
+    rc = lib.bmx_trimul_pack(fake, fake, fake, fake, fake, -1, 256, 1, None)
+    assert rc == N.BMX_EINVAL and b"bad n" in lib.bmx_last_error()
+    rc = lib.bmx_trimul_pack(odd, fake, fake, fake, fake, 8, 512, 0, None)
+    assert rc == N.BMX_EINVAL and b"p and g must be 16-byte aligned" in lib.bmx_last_error()
+    shape = (ctypes.c_int64 * 5)(1, 1, 4, 4, 4097)
+    strides = (ctypes.c_int64 * 5)(0, 0, 0, 4097, 1)
+    rc = lib.bmx_bias_softmax(fake, fake, fake, fake, 0, shape, strides, strides, strides, None)
+    assert rc == N.BMX_EINVAL and b"at most 4096 keys" in lib.bmx_last_error()
+    rc = lib.bmx_bias_softmax(fake, fake, fake, fake, 2, shape, strides, strides, strides, None)
+    assert rc == N.BMX_EINVAL and b"dtype must be fp32 or bf16" in lib.bmx_last_error()
+    shape[4] = 64
+    rc = lib.bmx_bias_softmax(fake, None, fake, fake, 1, shape, strides, strides, strides, None)
+    assert rc == N.BMX_EINVAL and b"null pointer" in lib.bmx_last_error()
+    rc = lib.bmx_pair_bias_fwd(fake, 0, 4, fake, fake, ctypes.c_float(1e-5), fake, 8, fake, None)
+    assert rc == N.BMX_EINVAL and b"16 heads" in lib.bmx_last_error()
+    rc = lib.bmx_pair_bias_fwd(odd, 0, 4, fake, fake, ctypes.c_float(1e-5), fake, 16, fake, None)
+    assert rc == N.BMX_EINVAL and b"z must be 16-byte aligned" in lib.bmx_last_error()
+
+
 def test_call_raises_with_message(lib):
     with pytest.raises(N.BmxError, match="eps must be positive"):
         N.call("bmx_layernorm", None, None, None, 0.0, None, 0, 1, 4, None)
