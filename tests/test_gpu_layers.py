@@ -15,8 +15,11 @@ def max_rel(got, want):
     return ((got - want).abs().max() / want.abs().max()).item()
 
 
-@pytest.mark.parametrize("n,masked", [(48, False), (100, True)])
+@pytest.mark.parametrize("n,masked", [(48, None), (100, "suffix"), (160, "scattered")])
 def test_pairformer_layer_matches_oracle(gpu, n, masked):
+    """Token masks as Boltz builds them: none, padding (a suffix), or tokens
+    masked anywhere (the attention core's closed rows and its per-row masked
+    path, the multiplication's masked operand rows in the middle of a tile)."""
     g = torch.Generator().manual_seed(n)
     ref = R.randomize(R.PairformerLayer(), generator=g).eval()
     mine = layers.PairformerLayer()
@@ -25,8 +28,10 @@ def test_pairformer_layer_matches_oracle(gpu, n, masked):
     z = torch.randn(1, n, n, 128, generator=g)
     s = torch.randn(1, n, 384, generator=g)
     mask = torch.ones(1, n)
-    if masked:
+    if masked == "suffix":
         mask[:, -7:] = 0
+    elif masked == "scattered":
+        mask[0, 1 + torch.randperm(n - 1, generator=g)[:15]] = 0
     pm = mask[:, :, None] * mask[:, None, :]
     with torch.no_grad():
         s_ref, z_ref = ref(s, z, mask, pm)
