@@ -174,3 +174,38 @@ def test_batched_pair_modules_match_per_element_calls(model, gpu):
                 assert torch.equal(got[b], alone[0]), (k, b)
                 w = want[k][b].double()
                 assert ((got[b].double() - w).abs().max() / w.abs().max()).item() < TOL, (k, b)
+
+
+def test_batched_installed_layers_match_per_element_calls(model, gpu, calls):
+    """The installed whole-layer forwards on a batch of two with different
+    token masks: element b equals the call on element b alone, bit for bit
+    (one workspace shared by the batch loop, per-element masks and dropout
+    row scales), and both layers match upstream's fp32 forward."""
+    n = 80
+    m = torch.ones(2, n, device=gpu)
+    m[0, -6:] = 0
+    m[1, 10:14] = 0
+    pm = m[:, :, None] * m[:, None, :]
+    s = torch.randn(2, n, 384, device=gpu)
+    z = torch.randn(2, n, n, 128, device=gpu) * 0.5
+    conf = model.confidence_module.pairformer_stack.layers[0]
+    msa = model.msa_module.layers[0].pairformer_layer
+    with torch.inference_mode():
+        want_s, want_z = conf(s, z, m, pm)
+        want_msa = msa(z, pm)
+    adapters.install(model)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        got_s, got_z = conf(s, z, m, pm)
+        got_msa = msa(z, pm)
+        # the native pair stack ran for both elements of both layers
+        assert calls == {"trimul": 8, "triattn": 8, "pair_transition": 4}
+        for b in range(2):
+            one = slice(b, b + 1)
+            alone_s, alone_z = conf(s[one].contiguous(), z[one].contiguous(), m[one].contiguous(),
+                                    pm[one].contiguous())
+            assert torch.equal(got_z[b], alone_z[0]) and torch.equal(got_s[b], alone_s[0]), b
+            assert torch.equal(got_msa[b], msa(z[one].contiguous(), pm[one].contiguous())[0]), b
+    for b in range(2):
+        assert rel(got_z[b], want_z[b], z[b]) < TOL, b
+        assert rel(got_s[b], want_s[b], s[b]) < TOL, b
+        assert rel(got_msa[b], want_msa[b], z[b]) < TOL, b
