@@ -29,9 +29,11 @@ def _native_shape_ok(module, x) -> bool:
     )
 
 
-# fp32 mode holds about this many bytes per pair at its peak (``ops.triattn_fp32``:
+# fp32 mode holds at most this many bytes per pair at its peak (``ops.triattn_fp32``:
 # the [N^2, 576] fp32 projection, the split-bf16 attention's K / V workspace,
-# the attention output and the linear_o result), all N rows at once.
+# the attention output and the linear_o result), all N rows at once.  Measured
+# at N = 1024: 3860-3864 bytes per pair by default, 3088-3604 with exact fp32
+# linears (tests/test_gpu_fp32_triattn.py); the bound keeps a margin.
 FP32_BYTES_PER_PAIR = 4608
 # ... and runs natively while that fits in this share of the device memory
 # (N up to about 5300 on a 288 GB MI355X); larger N run upstream's chunked

@@ -62,3 +62,38 @@ def test_fp32_triangle_attention_falls_back_under_grad(gpu):
     got = triangle_attention_forward(ref, x, mask)
     want = type(ref).forward(ref, x, mask)
     assert torch.equal(got, want) and got.requires_grad
+
+
+@pytest.mark.parametrize("exact", [False, True])
+@pytest.mark.parametrize("starting", [True, False])
+def test_fp32_working_set_within_the_native_bound(gpu, starting, exact):
+    """fp32 mode holds every row at once, so it runs natively only while
+    ``FP32_BYTES_PER_PAIR`` * N^2 fits the device (``fp32_native_fits``): the
+    memory one call allocates on top of its input, output included, must stay
+    within that per-pair figure."""
+    from boltz_lumi_amd.triangle import FP32_BYTES_PER_PAIR
+
+    n = 1024
+    cls = R.TriangleAttention if starting else R.TriangleAttentionEndingNode
+    layer = R.randomize(cls(128, 32, 4), generator=torch.Generator().manual_seed(3)).to(gpu).eval()
+    x = torch.randn(1, n, n, 128, device=gpu)
+    tok = torch.ones(n, device=gpu)
+    tok[-50:] = 0
+    mask = (tok[:, None] * tok[None, :])[None]
+    before = ops.exact_fp32_linears(exact)
+    try:
+        with torch.inference_mode():
+            triangle_attention_forward(layer, x, mask)  # weight packs and library state built here
+            torch.cuda.synchronize()
+            torch.cuda.reset_peak_memory_stats(gpu)
+            base = torch.cuda.memory_allocated(gpu)
+            out = triangle_attention_forward(layer, x, mask)
+            torch.cuda.synchronize()
+            peak = torch.cuda.max_memory_allocated(gpu) - base
+    finally:
+        ops.exact_fp32_linears(before)
+    assert out.dtype == torch.float32
+    per_pair = peak / (n * n)
+    print(f"fp32 triangle attention n={n} starting={starting} exact={exact}: {per_pair:.0f} bytes per pair at peak",
+          flush=True)
+    assert per_pair <= FP32_BYTES_PER_PAIR
