@@ -94,8 +94,11 @@ __global__ __launch_bounds__(256) void pack_kernel(const bf16* __restrict__ p, c
   }
   __syncthreads();
   const int64_t plane = (int64_t)n * n;
-  bf16* dst = (operand ? b : a) + (int64_t)r * n + t0;
-  const bool vec = n % 8 == 0;  // 16-byte aligned segment starts
+  bf16* const base = operand ? b : a;
+  bf16* dst = base + (int64_t)r * n + t0;
+  // With n % 8 == 0 every segment start is as aligned as the operand itself:
+  // 16-byte stores when that is 16-byte aligned, element stores otherwise.
+  const bool vec = n % 8 == 0 && ((uintptr_t)base & 15) == 0;
   for (int idx = threadIdx.x; idx < kC * (kPackSeg / 8); idx += 256) {
     const int c = idx >> 3, col = (idx & 7) * 8;
     bf16* out = dst + c * plane + col;

@@ -69,7 +69,8 @@ int bmx_trimul_split(const void* p, const void* g, const float* mask, void* a, v
                      bmx_stream_t stream);
 
 /* Channel-major bmm operands a,b[128][n][n] (outgoing: b transposed; incoming: a transposed).
- * p and g must be 16-byte aligned.
+ * p and g must be 16-byte aligned; a and b need bf16 alignment only (16-byte aligned operands
+ * take 16-byte stores when n % 8 == 0).
  * Replaces multiplication_gate_pack (kernels/multiplication_gate_hip.cu:96-123, `pack`). */
 int bmx_trimul_pack(const void* p, const void* g, const float* mask, void* a, void* b, int64_t n, int row_stride,
                     int outgoing, bmx_stream_t stream);

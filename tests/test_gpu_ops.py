@@ -108,6 +108,31 @@ def test_split_and_pack(gpu, n, joint):
             assert torch.equal(right, want_r.reshape(128, n, n))
 
 
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_pack_into_unaligned_operands(gpu, outgoing):
+    """The ABI asks 16-byte alignment of p and g only: operands that start one
+    element into a buffer (2-byte aligned) take element stores and hold the
+    same values as 16-byte-aligned ones (n = 136 would take 16-byte segment
+    stores)."""
+    from boltz_lumi_amd import _native as N
+
+    n = 136
+    g = torch.Generator().manual_seed(11)
+    p = torch.randn(1, n, n, 256, generator=g).to(torch.bfloat16).to(gpu)
+    gt = torch.randn(1, n, n, 256, generator=g).to(torch.bfloat16).to(gpu)
+    mask = torch.rand(1, n, n, generator=g).to(gpu)
+    with torch.inference_mode():
+        want_a, want_b = ops.pack(p, gt, mask, outgoing)
+        buf = torch.full((2, 128 * n * n + 8), -7.0, device=gpu, dtype=torch.bfloat16)
+        a, b = buf[0, 1:1 + 128 * n * n], buf[1, 1:1 + 128 * n * n]
+        assert a.data_ptr() % 16 == 2 and b.data_ptr() % 16 == 2
+        N.call("bmx_trimul_pack", p.data_ptr(), gt.data_ptr(), mask.data_ptr(), a.data_ptr(), b.data_ptr(), n, 256,
+               int(outgoing), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(128, n, n), want_a) and torch.equal(b.view(128, n, n), want_b)
+    assert (buf[:, 0] == -7.0).all() and (buf[:, 1 + 128 * n * n:] == -7.0).all()  # nothing written outside
+
+
 @pytest.mark.parametrize("kind", [ops.MODULATION, ops.GATE, ops.GATED_SWIGLU])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_epilogue(gpu, kind, dtype):
