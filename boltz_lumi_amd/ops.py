@@ -632,7 +632,41 @@ def triattn(module, x, mask, starting, out_mode=OUT_BF16, out=None, workspace=No
 TRIATTN_FP32_PROJ_COLS = 576
 
 
-def triattn_fp32(module, x, mask, starting):
+def _triattn_fp32_split_weight(module):
+    """q | k | v | g and the triangle bias as one split-bf16 weight for
+    LayerNorm-without-affine(x), the LayerNorm affine folded in:
+    (W diag w) LN0(x) + (bias + W b); bf16 [576, 3 * 128 + 64] (rows 512 ..
+    512 + heads the triangle bias, zero rows up to 576)."""
+    mha, ln = module.mha, module.layer_norm
+    lins = (mha.linear_q, mha.linear_k, mha.linear_v, mha.linear_g, module.linear)
+
+    def fold(*_):
+        w = torch.cat([lin.weight.detach().float() for lin in lins])
+        b = torch.cat([lin.bias.detach().float() if lin.bias is not None
+                       else w.new_zeros(lin.out_features) for lin in lins])
+        if ln.bias is not None:
+            b = b + w @ ln.bias.detach().float()
+        # zero rows up to 576 outputs: the GEMM runs faster than at 516 and output rows stay 128-byte aligned
+        pad = TRIATTN_FP32_PROJ_COLS - w.shape[0]
+        w = torch.cat([w * ln.weight.detach().float(), w.new_zeros(pad, C)])
+        return _x3_weight(w, torch.cat([b, b.new_zeros(pad)]))
+
+    srcs = tuple(t for m_ in (ln,) + lins for t in (m_.weight, m_.bias) if t is not None)
+    _check(4 * C + module.no_heads <= TRIATTN_FP32_PROJ_COLS, "too many heads")
+    return cached_weight(module, "qkvgb_ln_x3", srcs, fold)
+
+
+def _triattn_fp32_exact_weights(module):
+    """fp32 q | k | v | g weight [512, 128] and bias (linear_g's only)."""
+    mha = module.mha
+    w = cached_weight(module, "qkvg_f32", (mha.linear_q.weight, mha.linear_k.weight, mha.linear_v.weight,
+                                           mha.linear_g.weight), lambda *ws: torch.cat(ws, 0).float())
+    b = cached_weight(module, "qkvg_bias_f32", (mha.linear_g.bias,),
+                      lambda bg: torch.cat([bg.new_zeros(3 * C), bg]).float())
+    return w, b
+
+
+def triattn_fp32(module, x, mask, starting, block_rows=None):
     """TriangleAttention (starting or ending node) in fp32 for x [N, N, 128]
     fp32, the fp32 mode of the module (autocast off; reference
     triangle.py:38-52 accelerates it too).  The q | k | v | g projection and
@@ -644,38 +678,29 @@ def triattn_fp32(module, x, mask, starting):
     relative each; ``bmx_seq_attention_batched_fwd`` on fp32 MFMA in exact fp32
     mode), every row i one batch element attending over its N keys, all rows
     sharing the [4, N, N] triangle bias, so the [N, 4, N, N] scores never
-    reach HBM; ``linear_o`` is an fp32 GEMM.  Returns fp32 [N, N, 128]."""
+    reach HBM; ``linear_o`` is an fp32 GEMM.  Returns fp32 [N, N, 128].
+
+    ``block_rows`` < N processes the rows of the frame (x's rows for the
+    starting node, its columns for the ending node) in blocks of that many
+    (``_triattn_fp32_blocked``): the same products, with the per-pair working
+    set held for one block at a time."""
     _cuda(x)
     _check(x.dim() == 3 and x.size(0) == x.size(1) and x.size(2) == C and x.dtype == torch.float32,
            "expected fp32 x of shape [N, N, 128]")
     n = x.size(0)
     mha, heads, d = module.mha, module.no_heads, module.c_hidden
     _check(heads * d == C, "expected heads x head dim = 128")
+    if block_rows is not None and 0 < block_rows < n:
+        return _triattn_fp32_blocked(module, x, mask, starting, int(block_rows))
     if not starting:
         mask = None if mask is None else mask.transpose(0, 1)
     ln = module.layer_norm
-    lins = (mha.linear_q, mha.linear_k, mha.linear_v, mha.linear_g, module.linear)
     split = not _EXACT_FP32[0] and ln.weight is not None
     # the ending node works on x transposed: the split path's LayerNorm reads the transposed rows in
     # place, the exact path transposes x once
     x = x.contiguous() if starting or split else x.transpose(0, 1).contiguous()
     if split:
-        # q | k | v | g and the triangle bias as one split-bf16 GEMM of LayerNorm-without-affine(x), the
-        # LayerNorm affine folded into the weights: (W diag w) LN0(x) + (bias + W b)
-        def fold(*_):
-            w = torch.cat([lin.weight.detach().float() for lin in lins])
-            b = torch.cat([lin.bias.detach().float() if lin.bias is not None
-                           else w.new_zeros(lin.out_features) for lin in lins])
-            if ln.bias is not None:
-                b = b + w @ ln.bias.detach().float()
-            # zero rows up to 576 outputs: the GEMM runs faster than at 516 and output rows stay 128-byte aligned
-            pad = TRIATTN_FP32_PROJ_COLS - w.shape[0]
-            w = torch.cat([w * ln.weight.detach().float(), w.new_zeros(pad, C)])
-            return _x3_weight(w, torch.cat([b, b.new_zeros(pad)]))
-
-        srcs = tuple(t for m_ in (ln,) + lins for t in (m_.weight, m_.bias) if t is not None)
-        _check(4 * C + heads <= TRIATTN_FP32_PROJ_COLS, "too many heads")
-        w3 = cached_weight(module, "qkvgb_ln_x3", srcs, fold)
+        w3 = _triattn_fp32_split_weight(module)
         op = (layernorm_split3(x.view(-1, C), ln.eps) if starting
               else layernorm_split3_t(x, ln.eps).view(-1, split_width(C)))
         proj = mm_split(op, w3).view(n, n, TRIATTN_FP32_PROJ_COLS)
@@ -683,10 +708,7 @@ def triattn_fp32(module, x, mask, starting):
         tri_bias = proj[..., 4 * C:4 * C + heads].permute(2, 0, 1).contiguous()  # [H, q, k], shared by every row
     else:
         xn = norm(x.view(-1, C), _f32(ln.weight), _f32(ln.bias), ln.eps, bf16_output=False)
-        w = cached_weight(module, "qkvg_f32", tuple(lin.weight for lin in lins[:4]),
-                          lambda *ws: torch.cat(ws, 0).float())
-        b = cached_weight(module, "qkvg_bias_f32", (mha.linear_g.bias,),
-                          lambda bg: torch.cat([bg.new_zeros(3 * C), bg]).float())
+        w, b = _triattn_fp32_exact_weights(module)
         proj = torch.nn.functional.linear(xn, w, b).view(n, n, 4 * C)
         tri_bias = torch.nn.functional.linear(xn, module.linear.weight.float()).view(n, n, heads)
         tri_bias = tri_bias.permute(2, 0, 1).contiguous()  # [H, q, k], shared by every row
@@ -697,6 +719,58 @@ def triattn_fp32(module, x, mask, starting):
     o = seq_attention_batched(q, k, v, tri_bias[None], m, g, module.inf, bias_div=n, split=not _EXACT_FP32[0])
     del q, k, v, g, proj, tri_bias  # 2.3 KB per pair, before linear_o's output is allocated
     out = torch.nn.functional.linear(o, mha.linear_o.weight.float(), mha.linear_o.bias.float())
+    return out if starting else out.transpose(0, 1)
+
+
+def _triattn_fp32_blocked(module, x, mask, starting, rows):
+    """``triattn_fp32`` over blocks of ``rows`` frame rows (x's rows for the
+    starting node, x's columns, copied transposed one block at a time, for the
+    ending node).  A first pass writes the [H, N, N] triangle bias, which every
+    row shares, from each block's LayerNorm operand and only the bias rows of
+    the projection weight; a second pass recomputes each block's operand and
+    runs its q | k | v | g projection, the fused attention over the block's
+    rows and ``linear_o`` into the output frame.  Full-frame memory: the
+    output, the bias and the mask (about 532 bytes per pair); the rest is
+    per block."""
+    n = x.size(0)
+    mha, heads, ln = module.mha, module.no_heads, module.layer_norm
+    split = not _EXACT_FP32[0] and ln.weight is not None
+    if mask is None:
+        m = x.new_ones(n, n)
+    else:
+        m = (mask if starting else mask.transpose(0, 1)).to(torch.float32).contiguous()
+
+    def frame_rows(i0, i1):  # [i1 - i0, N, 128] fp32, contiguous
+        return x[i0:i1].contiguous() if starting else x[:, i0:i1].transpose(0, 1).contiguous()
+
+    if split:
+        w3 = _triattn_fp32_split_weight(module)
+        w3_bias = w3[4 * C:]  # the bias rows and their zero padding: 64 outputs
+        features = lambda xb: layernorm_split3(xb.view(-1, C), ln.eps)
+        project_bias = lambda f: mm_split(f, w3_bias)
+        project = lambda f: mm_split(f, w3)
+    else:
+        w, b = _triattn_fp32_exact_weights(module)
+        w_bias = module.linear.weight.float()
+        features = lambda xb: norm(xb.view(-1, C), _f32(ln.weight), _f32(ln.bias), ln.eps, bf16_output=False)
+        project_bias = lambda f: torch.nn.functional.linear(f, w_bias)
+        project = lambda f: torch.nn.functional.linear(f, w, b)
+    blocks = [(i0, min(n, i0 + rows)) for i0 in range(0, n, rows)]
+    tri_bias = torch.empty(heads, n, n, device=x.device, dtype=torch.float32)  # [H, q, k]
+    for i0, i1 in blocks:
+        bias = project_bias(features(frame_rows(i0, i1)))[:, :heads]
+        tri_bias[:, i0:i1] = bias.view(i1 - i0, n, heads).permute(2, 0, 1)
+        del bias
+    out = torch.empty(n, n, C, device=x.device, dtype=torch.float32)  # the output frame
+    w_o, b_o = mha.linear_o.weight.float(), mha.linear_o.bias.float()
+    for i0, i1 in blocks:
+        proj = project(features(frame_rows(i0, i1))).view(i1 - i0, n, -1)
+        q, k, v, g = proj[..., :4 * C].split(C, dim=-1)
+        o = seq_attention_batched(q, k, v, tri_bias[None], m[i0:i1], g, module.inf, bias_div=i1 - i0,
+                                  split=not _EXACT_FP32[0])
+        del q, k, v, g, proj
+        torch.addmm(b_o, o.view(-1, C), w_o.t(), out=out[i0:i1].view(-1, C))
+        del o
     return out if starting else out.transpose(0, 1)
 
 

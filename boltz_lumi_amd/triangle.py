@@ -35,16 +35,28 @@ def _native_shape_ok(module, x) -> bool:
 # at N = 1024: 3860-3864 bytes per pair by default, 3088-3604 with exact fp32
 # linears (tests/test_gpu_fp32_triattn.py); the bound keeps a margin.
 FP32_BYTES_PER_PAIR = 4608
-# ... and runs natively while that fits in this share of the device memory
-# (N up to about 5300 on a 288 GB MI355X); larger N run upstream's chunked
-# fp32 forward.
+# ... and runs in one pass while that fits in this share of the device memory
+# (N up to about 5300 on a 288 GB MI355X).  Larger N run in blocks of frame
+# rows, which hold the output frame, the triangle bias and the mask (this many
+# bytes per pair) for the whole frame and the rest for one block at a time.
 FP32_MEMORY_SHARE = 0.45
+FP32_FRAME_BYTES_PER_PAIR = 532
 
 
 def fp32_native_fits(n: int, device_bytes: int) -> bool:
-    """Whether fp32-mode triangle attention at size ``n`` runs natively on a
-    device of ``device_bytes`` (its working set within ``FP32_MEMORY_SHARE``)."""
+    """Whether fp32-mode triangle attention at size ``n`` runs in one pass on
+    a device of ``device_bytes`` (its working set within ``FP32_MEMORY_SHARE``)."""
     return FP32_BYTES_PER_PAIR * n * n <= FP32_MEMORY_SHARE * device_bytes
+
+
+def fp32_block_rows(n: int, device_bytes: int) -> int:
+    """Frame rows per block for fp32-mode triangle attention at size ``n``:
+    ``n`` when one pass fits, otherwise the most rows whose working set fits
+    beside the full-frame output, bias and mask; 0 when not one row fits."""
+    if fp32_native_fits(n, device_bytes):
+        return n
+    budget = FP32_MEMORY_SHARE * device_bytes - FP32_FRAME_BYTES_PER_PAIR * n * n
+    return max(0, min(n, int(budget // (FP32_BYTES_PER_PAIR * n))))
 
 
 def triangle_attention_forward(self, x, mask=None, chunk_size=None, use_kernels=False):
@@ -58,9 +70,10 @@ def triangle_attention_forward(self, x, mask=None, chunk_size=None, use_kernels=
     LayerNorm affine folded into the weights) and the fused split-bf16
     attention, about 2^-16 relative per product; with
     ``BMX_EXACT_FP32_LINEARS=1`` the fp32 LN128 kernel, fp32 GEMMs and the
-    fp32-MFMA attention.  fp32 mode holds all N rows at once, so it runs
-    natively only while its working set fits (``fp32_native_fits``); larger N
-    take the class forward, which chunks the rows."""
+    fp32-MFMA attention.  fp32 mode runs all N rows in one pass while that
+    working set fits (``fp32_native_fits``) and in blocks of rows above
+    (``fp32_block_rows``); only a device on which not one row fits takes the
+    class forward, which chunks the rows."""
     base = (
         not use_kernels
         and inference(self)
@@ -70,9 +83,11 @@ def triangle_attention_forward(self, x, mask=None, chunk_size=None, use_kernels=
     )
     starting = getattr(self, "starting", True)
     if base and autocast_off() and x.dtype == torch.float32 and self.layer_norm.weight.dtype == torch.float32:
-        if not fp32_native_fits(x.shape[1], torch.cuda.get_device_properties(x.device).total_memory):
+        rows = fp32_block_rows(x.shape[1], torch.cuda.get_device_properties(x.device).total_memory)
+        if rows == 0:
             return type(self).forward(self, x, mask, chunk_size=chunk_size, use_kernels=use_kernels)
-        outs = [ops.triattn_fp32(self, x[b], None if mask is None else mask[b], starting) for b in range(x.shape[0])]
+        outs = [ops.triattn_fp32(self, x[b], None if mask is None else mask[b], starting, block_rows=rows)
+                for b in range(x.shape[0])]
         return torch.stack(outs)
     supported = base and (bf16_autocast() or x.dtype == torch.bfloat16) and x.dtype in (torch.float32, torch.bfloat16)
     if not supported:

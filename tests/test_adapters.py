@@ -254,17 +254,28 @@ def test_split_bf16_threshold_follows_width_and_rows():
         ops.exact_fp32_linears(before)
 
 
-def test_fp32_triangle_attention_native_only_while_its_working_set_fits():
-    """fp32-mode triangle attention holds ~4.6 KB per pair for all N rows at
-    once: natively up to about N = 5300 on a 288 GB MI355X, the class forward
-    (upstream's chunked rows) above, e.g. at the kernels' N = 8192 limit."""
-    from boltz_lumi_amd.triangle import FP32_BYTES_PER_PAIR, fp32_native_fits
+def test_fp32_triangle_attention_one_pass_or_row_blocks_by_working_set():
+    """fp32-mode triangle attention holds up to 4.6 KB per pair for all N rows
+    at once: one pass up to about N = 5300 on a 288 GB MI355X; above, blocks
+    of frame rows whose working set fits beside the full-frame output, bias
+    and mask (532 bytes per pair), e.g. at the kernels' N = 8192 limit; the
+    class forward only where not one row fits."""
+    from boltz_lumi_amd.triangle import (FP32_BYTES_PER_PAIR, FP32_FRAME_BYTES_PER_PAIR, FP32_MEMORY_SHARE,
+                                         fp32_block_rows, fp32_native_fits)
 
     mi355x = 288 * 1024 ** 3
     assert fp32_native_fits(1024, mi355x) and fp32_native_fits(4096, mi355x) and fp32_native_fits(5300, mi355x)
     assert not fp32_native_fits(6500, mi355x) and not fp32_native_fits(8192, mi355x)
     assert not fp32_native_fits(4096, 64 * 1024 ** 3)  # a smaller device caps earlier
     assert FP32_BYTES_PER_PAIR * 8192 ** 2 > 288e9  # all rows at once would not fit at N = 8192
+    assert fp32_block_rows(5300, mi355x) == 5300
+    for n in (6500, 8192):
+        rows = fp32_block_rows(n, mi355x)
+        assert 0 < rows < n
+        held = FP32_FRAME_BYTES_PER_PAIR * n * n + FP32_BYTES_PER_PAIR * rows * n
+        assert held <= FP32_MEMORY_SHARE * mi355x < held + FP32_BYTES_PER_PAIR * n  # the most rows that fit
+    assert fp32_block_rows(8192, 96 * 1024 ** 3) > 0
+    assert fp32_block_rows(8192, 64 * 1024 ** 3) == 0  # the frame alone would not fit: class forward
 
 
 @pytest.mark.parametrize("training", [False, True])
