@@ -113,3 +113,37 @@ def test_pair_transition_largest_size(gpu):
     assert ok
     assert max_rel(got, want) < TOL
     assert max_rel(res - base, want) < TOL
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_fp32_triattn_row_blocks_at_large_n(gpu, starting, monkeypatch):
+    """fp32-mode triangle attention at N = 6144, where one pass does not fit
+    (4.6 KB per pair, 174 GB): the installed forward runs blocks of frame rows
+    and the sampled rows meet the fp32-mode bar (1e-4) against the fp32
+    oracle's rows."""
+    from boltz_lumi_amd import triangle
+
+    n = 6144
+    total = torch.cuda.get_device_properties(gpu).total_memory
+    rows_per_block = triangle.fp32_block_rows(n, total)
+    print(f"fp32 triattn n={n} starting={starting}: blocks of {rows_per_block} rows", flush=True)
+    assert 0 < rows_per_block < n
+    seen = []
+    original = ops.triattn_fp32
+    monkeypatch.setattr(ops, "triattn_fp32", lambda *a, **k: seen.append(k.get("block_rows")) or original(*a, **k))
+    cls = R.TriangleAttention if starting else R.TriangleAttentionEndingNode
+    torch.manual_seed(2)
+    m = R.randomize(cls(128, 32, 4)).to(gpu).eval()
+    x, mask, rows = inputs(n, gpu)
+    with torch.inference_mode():
+        out = triangle.triangle_attention_forward(m, x[None], mask[None])[0]
+        assert seen == [rows_per_block] and out.dtype == torch.float32
+        got = pick(out, rows, starting)
+        ok = finite(out)
+        del out
+        torch.cuda.empty_cache()
+        want = m.forward_rows(x[None], mask[None], rows)[0]
+    assert ok
+    err = max_rel(got, want)
+    print(f"fp32 triattn n={n} starting={starting}: sampled rows max_rel {err:.2e}", flush=True)
+    assert err < 1e-4
