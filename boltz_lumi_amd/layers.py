@@ -29,6 +29,16 @@ def _require_cuda(x: torch.Tensor, what: str) -> None:
         raise RuntimeError(f"{what}: the gfx950 path needs a GPU tensor (got {x.device})")
 
 
+def _batch_out(x, out, out_mode):
+    """The module output for a batch: ``out`` when given (accumulate mode
+    needs it), else one tensor of x's shape that each batch element's kernel
+    writes its slice of (no stacking copy)."""
+    if out is not None or out_mode == ops.OUT_ACCUMULATE:
+        return out
+    dtype = torch.bfloat16 if out_mode == ops.OUT_BF16 else torch.float32
+    return torch.empty(x.shape, device=x.device, dtype=dtype)
+
+
 class LayerNorm(nn.Module):
     """Triangle-attention LayerNorm (upstream ``primitives.LayerNorm``; ``c_in`` is a tuple)."""
 
@@ -73,12 +83,12 @@ class TriangleAttention(nn.Module):
     def forward(self, x, mask=None, chunk_size=None, use_kernels=False, out_mode=ops.OUT_BF16, out=None,
                 workspace=None):
         _require_cuda(x, type(self).__name__)
-        outs = []
+        out = _batch_out(x, out, out_mode)
         for b in range(x.shape[0]):
             mb = None if mask is None else mask[b].float().contiguous()
-            ob = None if out is None else out[b]
-            outs.append(ops.triattn(self, x[b].contiguous(), mb, self.starting, out_mode, ob, workspace))
-        return out if out is not None else torch.stack(outs)
+            ops.triattn(self, x[b].contiguous(), mb, self.starting, out_mode, None if out is None else out[b],
+                        workspace)
+        return out
 
 
 class TriangleAttentionEndingNode(TriangleAttention):
@@ -105,12 +115,11 @@ class _TriangleMultiplication(nn.Module):
 
     def forward(self, x, mask, use_kernels=False, out_mode=ops.OUT_BF16, out=None, workspace=None):
         _require_cuda(x, type(self).__name__)
-        outs = []
+        out = _batch_out(x, out, out_mode)
         for b in range(x.shape[0]):
-            ob = None if out is None else out[b]
-            outs.append(ops.trimul(self, x[b].float().contiguous(), mask[b].float().contiguous(), self.outgoing,
-                                   out_mode, ob, workspace))
-        return out if out is not None else torch.stack(outs)
+            ops.trimul(self, x[b].float().contiguous(), mask[b].float().contiguous(), self.outgoing, out_mode,
+                       None if out is None else out[b], workspace)
+        return out
 
 
 class TriangleMultiplicationOutgoing(_TriangleMultiplication):

@@ -88,7 +88,8 @@ def triangle_attention_forward(self, x, mask=None, chunk_size=None, use_kernels=
             return type(self).forward(self, x, mask, chunk_size=chunk_size, use_kernels=use_kernels)
         outs = [ops.triattn_fp32(self, x[b], None if mask is None else mask[b], starting, block_rows=rows)
                 for b in range(x.shape[0])]
-        return torch.stack(outs)
+        # one batch element: its result as a view (the ending node's is a transposed one, as upstream's)
+        return outs[0].unsqueeze(0) if len(outs) == 1 else torch.stack(outs)
     supported = base and (bf16_autocast() or x.dtype == torch.bfloat16) and x.dtype in (torch.float32, torch.bfloat16)
     if not supported:
         return type(self).forward(self, x, mask, chunk_size=chunk_size, use_kernels=use_kernels)
