@@ -67,10 +67,10 @@ def test_fp32_triangle_attention_falls_back_under_grad(gpu):
 @pytest.mark.parametrize("exact", [False, True])
 @pytest.mark.parametrize("starting", [True, False])
 def test_fp32_working_set_within_the_native_bound(gpu, starting, exact):
-    """fp32 mode holds every row at once, so it runs natively only while
-    ``FP32_BYTES_PER_PAIR`` * N^2 fits the device (``fp32_native_fits``): the
-    memory one call allocates on top of its input, output included, must stay
-    within that per-pair figure."""
+    """The one-pass fp32 path holds every row at once and runs while
+    ``FP32_BYTES_PER_PAIR`` * N^2 fits the device (``fp32_native_fits``; row
+    blocks above): the memory one call allocates on top of its input, output
+    included, must stay within that per-pair figure."""
     from boltz_lumi_amd.triangle import FP32_BYTES_PER_PAIR
 
     n = 1024
