@@ -1,8 +1,11 @@
 """Writes tests/golden/pair_modules_n6.npz: frozen input / output vectors of
 the Pairformer pair modules and one whole PairformerLayer at their production
-widths (128 pair channels, 384 single channels) and N = 6 tokens, the outputs
-evaluated by the fp64 explicit-loop restatement (oracle/brute.py) on the
-stored fp32 inputs.
+widths (128 pair channels, 384 single channels) and N = 6 tokens, and
+tests/golden/diffusion_blocks_n6.npz: the score model's token-transformer
+blocks at their width (768) for 2 samples of 6 tokens (AdaLN,
+ConditionedTransitionBlock, AttentionPairBias with a given bias, multiplicity
+2, one key masked).  The outputs are evaluated by the fp64 explicit-loop
+restatement (oracle/brute.py) on the stored fp32 inputs.
 
 The reference ships no golden vectors (its tests run live upstream Boltz on a
 GPU), so these are self-fixtures: they freeze the oracle and the product
@@ -99,6 +102,42 @@ def main():
     data["pairformer_layer/z_out"] = np.asarray(z_out, dtype=np.float32)
     np.savez_compressed(OUT, **data)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")
+    diffusion_blocks()
+
+
+DIFFUSION_OUT = Path(__file__).resolve().parent / "diffusion_blocks_n6.npz"
+# case -> (constructor, seed)
+DIFFUSION_MODULES = {
+    "adaln": (lambda: R.AdaLN(768, 768), 201),
+    "conditioned_transition": (lambda: R.ConditionedTransitionBlock(768, 768), 202),
+    "attention_pair_bias": (lambda: R.AttentionPairBias(768, num_heads=16, compute_pair_bias=False), 203),
+}
+MULTIPLICITY = 2
+
+
+def diffusion_blocks():
+    g = torch.Generator().manual_seed(200)
+    a = torch.randn(MULTIPLICITY, N, 768, generator=g).numpy()
+    s = torch.randn(MULTIPLICITY, N, 768, generator=g).numpy()
+    bias = torch.randn(1, N, N, 16, generator=g).numpy()  # [B / multiplicity, Q, K, H], shared by the samples
+    mask = np.ones((MULTIPLICITY, N), dtype=np.float32)
+    mask[1, 2] = 0  # one key of the second sample
+    data = {"a": a, "s": s, "bias": bias, "mask": mask, "multiplicity": np.array(MULTIPLICITY)}
+    a64, s64, bias64, mask64 = (x.astype(np.float64) for x in (a, s, bias, mask))
+    for name, (ctor, seed) in DIFFUSION_MODULES.items():
+        module = build(ctor, seed)
+        print(f"{name}: fp64 loops", flush=True)
+        if name == "adaln":
+            out = B.adaln(module, a64, s64)
+        elif name == "conditioned_transition":
+            out = B.conditioned_transition(module, a64, s64)
+        else:
+            out = B.attention_pair_bias_keys(module, s64, s64, bias64, mask64, MULTIPLICITY)
+        data[f"{name}/seed"] = np.array(seed)
+        data[f"{name}/weight_stats"] = weight_stats(module)
+        data[f"{name}/out"] = np.asarray(out, dtype=np.float32)
+    np.savez_compressed(DIFFUSION_OUT, **data)
+    print(f"wrote {DIFFUSION_OUT} ({DIFFUSION_OUT.stat().st_size} bytes)")
 
 
 if __name__ == "__main__":

@@ -93,3 +93,39 @@ def test_pairformer_layer_matches_frozen_loops(golden):
         assert max_rel(s_out[0].double().numpy()[open_tok], golden["pairformer_layer/s_out"][open_tok]) < bar, dtype
     # the layer's update differs from any single branch's: the fixture covers the whole composition
     assert max_rel(dz[keep], golden["transition_z/out"][keep]) > 0.5
+
+
+# ---------------------------------------------------------------- diffusion blocks
+
+DIFFUSION = Path(__file__).resolve().parent / "golden" / "diffusion_blocks_n6.npz"
+DIFFUSION_MODULES = {
+    "adaln": lambda: R.AdaLN(768, 768),
+    "conditioned_transition": lambda: R.ConditionedTransitionBlock(768, 768),
+    "attention_pair_bias": lambda: R.AttentionPairBias(768, num_heads=16, compute_pair_bias=False),
+}
+
+
+@pytest.fixture(scope="module")
+def golden_diffusion():
+    with np.load(DIFFUSION, allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+def call_diffusion(name, module, t, dtype):
+    a, s, bias, mask = (torch.from_numpy(t[k]).to(dtype) for k in ("a", "s", "bias", "mask"))
+    if name == "attention_pair_bias":
+        return module(s, bias, mask, s, multiplicity=int(t["multiplicity"]))
+    return module(a, s)
+
+
+@pytest.mark.parametrize("name", list(DIFFUSION_MODULES))
+def test_diffusion_block_matches_frozen_loops(golden_diffusion, name):
+    """The token transformer's blocks at width 768 (2 samples of 6 tokens;
+    the attention with a given bias shared by the samples, one key masked)."""
+    module = build(DIFFUSION_MODULES[name], golden_diffusion, name)
+    want = golden_diffusion[f"{name}/out"]
+    with torch.no_grad():
+        got64 = call_diffusion(name, module.double(), golden_diffusion, torch.float64)
+        got32 = call_diffusion(name, module.float(), golden_diffusion, torch.float32)
+    assert max_rel(got64, want) < 1e-6
+    assert max_rel(got32, want) < 1e-5

@@ -2,10 +2,11 @@
 (fp64 explicit loops, production width, N = 6, a token masked in the middle):
 the five pair modules and one PairformerLayer, each patched by ``install`` at
 Boltz's module path and run as Boltz runs them (inference, bf16 autocast),
-within the north star's bf16 bar.  Attention outputs are compared on the open
-pairs, the sequence stack on the open tokens (the masked token's fully masked
-query row is a uniform softmax in fp32 / bf16, softmax(S) in the fp64 loops;
-tests/test_golden.py)."""
+within the north star's bf16 bar; and the score model's width-768 blocks
+(tests/golden/diffusion_blocks_n6.npz) in fp32 at the fp32 bar.  Attention
+outputs are compared on the open pairs, the sequence stack on the open tokens
+(the masked token's fully masked query row is a uniform softmax in fp32 /
+bf16, softmax(S) in the fp64 loops; tests/test_golden.py)."""
 
 from pathlib import Path
 
@@ -124,3 +125,51 @@ def test_installed_pairformer_layer_matches_frozen_loops(golden, gpu, native_cal
     err_s = max_rel(s_out[0].double().cpu().numpy()[open_tok], golden["pairformer_layer/s_out"][open_tok])
     print(f"golden pairformer_layer: z update max_rel {err_z:.2e}, s max_rel {err_s:.2e}", flush=True)
     assert err_z < TOL and err_s < TOL
+
+
+DIFFUSION = Path(__file__).resolve().parent / "golden" / "diffusion_blocks_n6.npz"
+
+
+def test_installed_diffusion_blocks_match_frozen_loops(gpu, monkeypatch):
+    """The score model's token-transformer blocks at width 768 through the
+    installed forwards in fp32 (autocast off, as the reference runs the score
+    model): AdaLN and ConditionedTransitionBlock patched by ``install`` at
+    ``structure_module.score_model``, the attention through
+    ``pair_bias.prepared_forward`` (its patched forward); the fp32-mode bar
+    1e-4 against the frozen fp64 loops."""
+    from boltz_lumi_amd.pair_bias import prepared_forward
+
+    with np.load(DIFFUSION, allow_pickle=False) as f:
+        t = {k: f[k] for k in f.files}
+    counts = {}
+    for name in ("adaln_modulate", "epilogue", "seq_attention_batched"):
+        original = getattr(ops, name)
+
+        def counted(*args, _name=name, _original=original, **kwargs):
+            counts[_name] = counts.get(_name, 0) + 1
+            return _original(*args, **kwargs)
+
+        monkeypatch.setattr(ops, name, counted)
+    host = nn.Module()
+    host.structure_module = nn.Module()
+    host.structure_module.score_model = sm = nn.Module()
+    sm.adaln = seeded(lambda: R.AdaLN(768, 768), t, "adaln")
+    sm.transition = seeded(lambda: R.ConditionedTransitionBlock(768, 768), t, "conditioned_transition")
+    apb = seeded(lambda: R.AttentionPairBias(768, num_heads=16, compute_pair_bias=False), t, "attention_pair_bias")
+    host = host.to(gpu).eval()
+    apb = apb.to(gpu)
+    a, s, bias, mask = (torch.from_numpy(t[k]).to(gpu) for k in ("a", "s", "bias", "mask"))
+    adapters.install(host, require_boltz2=False)
+    try:
+        assert "forward" in vars(sm.adaln) and "forward" in vars(sm.transition)
+        with torch.inference_mode():
+            got = {"adaln": sm.adaln(a, s), "conditioned_transition": sm.transition(a, s),
+                   "attention_pair_bias": prepared_forward(apb, s, bias, mask, s, int(t["multiplicity"]))}
+    finally:
+        adapters.uninstall(host)
+    assert counts.get("adaln_modulate", 0) >= 2 and counts.get("epilogue", 0) >= 2
+    assert counts.get("seq_attention_batched", 0) == 1
+    for name, out in got.items():
+        err = max_rel(out.float().cpu().numpy(), t[f"{name}/out"])
+        print(f"golden {name}: max_rel {err:.2e}", flush=True)
+        assert err < 1e-4, name
