@@ -48,11 +48,6 @@ __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 __device__ __forceinline__ float load_f(const float* p) { return *p; }
 __device__ __forceinline__ float load_f(const bf16* p) { return (float)*p; }
 
-template <typename T>
-__device__ __forceinline__ void store_f(T* p, float v) {
-  *p = (T)v;
-}
-
 // 16-byte load through a global (addrspace 1) pointer.  When a source pointer
 // is picked at run time the compiler can lose its address space and emit a
 // flat load, which also counts against lgkmcnt: every later LDS wait then

@@ -426,7 +426,6 @@ __global__ __launch_bounds__(256, 2) void trimul_out_kernel(const float* x, cons
   int tile = blockIdx.x, prev = -1;
   if (tile < total) fetch(tile);
   for (; tile < total; tile += gridDim.x) {
-    const int i = tile / tiles_x, j0 = (tile % tiles_x) * kP3;
     const float rs = prs;
     f32x4 xc[kRowsPer];
 #pragma unroll
