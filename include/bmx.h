@@ -27,7 +27,9 @@ extern "C" {
 
 typedef void* bmx_stream_t; /* hipStream_t */
 
-/* Last error message of the calling thread ("" after a successful call). */
+/* Last error message of the calling thread ("" after a successful call), and the ABI version (2:
+ * row_scale added to bmx_trimul_fwd / bmx_triattn_fwd).  No reference counterpart: the reference's
+ * torch extensions report errors as Python exceptions (kernels/_build.py:9-34 builds them). */
 const char* bmx_last_error(void);
 int bmx_abi_version(void);
 
@@ -53,7 +55,8 @@ int bmx_adaln(const void* a, const void* scale, const void* shift, void* out, in
               float eps, bmx_stream_t stream);
 
 /* bmx_adaln with the scale / shift rows at stride ld_mod (ld_mod >= dim, multiple of 4): column
- * slices of one conditioning projection shared by the layers of a diffusion transformer. */
+ * slices of one conditioning projection shared by the layers of a diffusion transformer
+ * (adaln_forward, src/boltz_lumi/diffusion.py:52-57). */
 int bmx_adaln_strided(const void* a, const void* scale, const void* shift, int64_t ld_mod, void* out, int dtype,
                       int64_t rows, int dim, float eps, bmx_stream_t stream);
 
@@ -186,10 +189,13 @@ int bmx_trimul_fwd_noalloc(const float* x, const float* mask, int64_t n, int out
                            const float* norm_out_b, float eps_out, const void* w_pout, const void* w_gout, void* out,
                            int out_mode, bmx_stream_t stream);
 
-/* Workspace needed by bmx_triattn_fwd (bytes). */
+/* Workspace needed by bmx_triattn_fwd (bytes).  Sizing query: the reference's intermediates are
+ * torch allocations inside triangle.py:32-104, which this caller-owned workspace replaces. */
 size_t bmx_triattn_workspace_bytes(int64_t n);
 
-/* Rows of the packed projection weight of bmx_triattn_fwd (416). */
+/* Rows of the packed projection weight of bmx_triattn_fwd (416): upstream's q / k / v linears,
+ * which the reference runs through _prep_qkv (triangle.py:80), with the triangle-bias linear's rows
+ * appended and zero rows up to 416. */
 int bmx_triattn_proj_rows(void);
 
 /* TriangleAttention{,EndingNode}.forward (c_in 128, 4 heads x 32) for one batch element.
@@ -217,7 +223,8 @@ int bmx_pack_mfma_weights(const void* src, int64_t rows, int64_t cols, void* dst
 int bmx_pair_transition_fwd(const void* x, int x_dtype, int64_t rows, const float* ln_w, const float* ln_b, float eps,
                             const void* w12, const void* w3, void* out, int out_mode, bmx_stream_t stream);
 
-/* Bytes of the folded pair-bias weights written by bmx_pair_bias_fold (8256). */
+/* Bytes of the folded pair-bias weights written by bmx_pair_bias_fold (8256); sizing query for
+ * the fold of AttentionPairBias.proj_z (pair_bias.py:21-36). */
 size_t bmx_pair_bias_fold_bytes(void);
 
 /* Fold the sequence stack's pair-bias LayerNorm affine (ln_w, ln_b: [128]) and projection
@@ -310,7 +317,9 @@ int bmx_seq_attention_x3_batched_fwd(const float* q, const float* k, const float
 
 /* bmx_seq_attention_x3_batched_fwd writing each output row as the split-bf16 operand of the next
  * linear (proj_o): out_op [batch * nq][3 * heads * D + 64] bf16, rows [hi | hi | lo | 1 1 0 ...]
- * as bmx_split3_bf16 writes them (16-byte aligned).  Saves the fp32 output and its split pass. */
+ * as bmx_split3_bf16 writes them (16-byte aligned).  Saves the fp32 output and its split pass.
+ * Replaces the same part of AttentionPairBias.forward as bmx_seq_attention_x3_batched_fwd
+ * (pair_bias.py:21-36) together with proj_o's input. */
 int bmx_seq_attention_x3_batched_split_fwd(const float* q, const float* k, const float* v, const float* bias,
                                            const float* mask, const float* g, int64_t batch, int64_t nq, int64_t nk,
                                            int64_t ldq, int64_t ldk, int64_t sq, int64_t sk, int64_t sbias,
