@@ -36,7 +36,7 @@ def _native_shape_ok(module, x) -> bool:
 # linears (tests/test_gpu_fp32_triattn.py); the bound keeps a margin.
 FP32_BYTES_PER_PAIR = 4608
 # ... and runs in one pass while that fits in this share of the device memory
-# (N up to about 5300 on a 288 GB MI355X).  Larger N run in blocks of frame
+# (N up to about 5500 on a 288 GiB MI355X).  Larger N run in blocks of frame
 # rows, which hold the output frame, the triangle bias and the mask (this many
 # bytes per pair) for the whole frame and the rest for one block at a time.
 FP32_MEMORY_SHARE = 0.45
