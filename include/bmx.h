@@ -103,7 +103,8 @@ int bmx_gated_residual(const float* a, const float* gate, int64_t ld_gate, const
  * likewise for the bias): x W + b up to about 2^-16 relative per product.  Operands are
  * written dense at row stride kp; inputs are fp32, 16-byte aligned; out 8-byte aligned. */
 
-/* Operand rows of x (rows of k values at row stride ldx; k, ldx multiples of 4). */
+/* Operand rows of x (rows of k values at row stride ldx; k, ldx multiples of 4): the operand of
+ * the linears above that take x itself (diffusion.py:52-68, pair_bias.py:15-36). */
 int bmx_split3_bf16(const float* x, int64_t rows, int64_t k, int64_t ldx, void* out, bmx_stream_t stream);
 
 /* Operand rows of LayerNorm-without-affine(x) (dim <= 1024, dim % 4 == 0): the s_norm input of
@@ -163,7 +164,9 @@ int bmx_bias_softmax(const void* scores, const void* bias, const float* mask, vo
  * 2 = contraction / attention core, 4 = output; 7 runs the whole module.  The
  * workspace carries the intermediates between separately launched stages. */
 
-/* Workspace needed by bmx_trimul_fwd (bytes; 3 * 128 * np^2 bf16, np = round_up(n,256)). */
+/* Workspace needed by bmx_trimul_fwd (bytes; 3 * 128 * np^2 bf16, np = round_up(n,256)).  Sizing
+ * query: the reference's intermediates are torch allocations inside normalized_forward
+ * (multiplication.py:48-137), which this caller-owned workspace replaces. */
 size_t bmx_trimul_workspace_bytes(int64_t n);
 
 /* TriangleMultiplication{Outgoing,Incoming}.forward for one batch element.

@@ -22,6 +22,26 @@ def test_header_matches_binding_table():
     assert declared_symbols() == sorted(N.SIGNATURES)
 
 
+def test_every_entry_point_is_documented():
+    """Each declaration's comment names the reference interface it replaces
+    (a file:line citation) or says it has no reference counterpart, and the
+    integration guide's ABI table lists it."""
+    text = (ROOT / "include" / "bmx.h").read_text()
+    guide = (ROOT / "INTEGRATION.md").read_text()
+    decl = re.compile(r"(/\*(?:(?!\*/).)*\*/)\s*((?:(?:int|size_t|const char\*)\s+bmx_\w+\([^;]*;\s*)+)", re.S)
+    seen = set()
+    for m in decl.finditer(text):
+        comment = " ".join(m.group(1).split())
+        names = re.findall(r"(bmx_\w+)\(", m.group(2))
+        cited = re.search(r"\.(py|cu|hip):\d", comment) or "no reference counterpart" in comment.lower() \
+            or "no counterpart in the reference" in comment.lower() or "no reference kernel" in comment.lower()
+        for name in names:
+            seen.add(name)
+            assert cited, f"{name}: its comment cites no reference interface: {comment[:120]}"
+            assert re.search(rf"\b{name}\b", guide), f"{name} is missing from INTEGRATION.md"
+    assert seen == set(declared_symbols())
+
+
 @pytest.fixture(scope="module")
 def lib():
     if not N.lib_path().exists():
