@@ -38,7 +38,7 @@ def test_every_entry_point_is_documented():
         for name in names:
             seen.add(name)
             assert cited, f"{name}: its comment cites no reference interface: {comment[:120]}"
-            assert re.search(rf"\b{name}\b", guide), f"{name} is missing from INTEGRATION.md"
+            assert re.search(rf"\b{name}\b", guide), f"{name} is missing from the integration guide's ABI table"
     assert seen == set(declared_symbols())
 
 
