@@ -17,7 +17,7 @@ from oracle import boltz_ref as R
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-2
-SIZES = [2, 15, 16, 17, 63, 65, 127, 129, 255, 257]
+SIZES = [1, 2, 15, 16, 17, 63, 65, 127, 129, 255, 257]
 
 
 def case(n, gpu):
@@ -127,3 +127,21 @@ def test_output_modes_are_exact_compositions(gpu, n, op):
         xi = x.clone()
         run(xi, ops.OUT_ACCUMULATE, xi)
         assert torch.equal(xi, x + y)
+
+
+def test_empty_inputs_return_empty_outputs(gpu):
+    """N = 0 (and zero transition rows): every fused op returns an empty result
+    of the right shape and dtype without launching a kernel."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.empty(0, 0, 128, device=gpu)
+    mask = torch.empty(0, 0, device=gpu)
+    att = R.randomize(R.TriangleAttention(128, 32, 4), generator=g).to(gpu).eval()
+    mul = R.randomize(R.TriangleMultiplicationOutgoing(128), generator=g).to(gpu).eval()
+    tr = R.randomize(R.Transition(128, 512), generator=g).to(gpu).eval()
+    with torch.inference_mode():
+        outs = [ops.triattn(att, x, mask, True), ops.trimul(mul, x, mask, True),
+                ops.pair_transition(tr, torch.empty(0, 128, device=gpu))]
+    torch.cuda.synchronize()
+    assert [tuple(o.shape) for o in outs] == [(0, 0, 128), (0, 0, 128), (0, 128)]
+    assert all(o.dtype == torch.bfloat16 for o in outs)
+
