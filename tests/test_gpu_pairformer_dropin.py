@@ -129,6 +129,26 @@ def test_installed_layer_at_the_reference_token_counts(gpu, n):
     assert err_z < TOL and err_s < TOL
 
 
+@pytest.mark.parametrize("n,padded", [(1, 0), (2, 1), (5, 2)])
+def test_installed_layer_at_the_smallest_sizes(gpu, n, padded):
+    """The installed layer (fused pair stack and sequence stack) at one, two
+    and five tokens, the last ones padded, against the fp32 oracle layer:
+    the kernels' tiles hold almost nothing but padding."""
+    print(f"installed PairformerLayer n={n} padded={padded}", flush=True)
+    ref, layer = installed(3, gpu)
+    s, z, mask, pm = inputs(n, padded, 4)
+    sg, zg, mg, pmg = (t.to(gpu) for t in (s, z, mask, pm))
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        s_got, z_got = layer(sg, zg, mg, pmg, 128)
+    with torch.no_grad():
+        s_ref, z_ref = ref(s, z, mask, pm)
+    assert z_got.shape == z.shape and s_got.shape == s.shape
+    assert torch.isfinite(z_got).all() and torch.isfinite(s_got).all()
+    err_z, err_s = rel(z_got, z_ref, z), rel(s_got, s_ref, s)
+    print(f"  z update {err_z:.2e}  s update {err_s:.2e}", flush=True)
+    assert err_z < TOL and err_s < TOL
+
+
 def test_generator_state_follows_upstream(gpu):
     ref, layer = installed(2, gpu)
     s, z, mask, pm = (t.to(gpu) for t in inputs(96, 5, 3))
